@@ -1,0 +1,187 @@
+/*
+ * mtlattn C ABI -- the drop-in boundary of the MI355X (gfx950) varlen
+ * flash-attention library libmtlattn_hip.so.
+ *
+ * Every entry point replaces one export of the reference's pybind11 module
+ * `mtlattn._C` (src/ext.mm:784-811). Signatures use plain pointers, sizes and
+ * an opaque stream handle only (no torch types), so any FFI can bind them; the
+ * torch extension mtlattn_amd/csrc/torch_ext.cpp is one such binder.
+ *
+ * Conventions shared by all entry points:
+ *  - Tensors are device pointers. q/k/v/out/dout are [tokens, heads, D] with
+ *    the last two dims contiguous (head stride == D) and a free row stride
+ *    (in elements), as src/ext.mm:322-325 requires.
+ *  - cu_seqlens_{q,kv} are device int32 [num_seqs + 1] cumulative offsets.
+ *    Sequence bounds are clamped to [0, total] on the device, so malformed
+ *    offsets never address outside the tensors.
+ *  - Causal masking is end-aligned: query i sees key j iff
+ *    j <= i + (kv_len - q_len); window W > 0 adds j > i + (kv_len - q_len) - W.
+ *  - GQA: query head h reads kv head h / (Hq / Hkv).
+ *  - The library never allocates device memory. Callers pass scratch space
+ *    sized by the matching *_workspace_size() query.
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream)
+ *    of the current device; nothing synchronises with the host.
+ *  - Return value: MTLATTN_OK (0) or a negative MTLATTN_ERR_*; the message is
+ *    available from mtlattn_last_error() on the calling thread.
+ */
+#ifndef MTLATTN_CAPI_H
+#define MTLATTN_CAPI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MTLATTN_ABI_VERSION 1
+
+/* element types of q/k/v/out/dout/dq/dk/dv */
+enum {
+    MTLATTN_DTYPE_F32 = 0,
+    MTLATTN_DTYPE_F16 = 1,
+    MTLATTN_DTYPE_BF16 = 2
+};
+
+enum {
+    MTLATTN_OK = 0,
+    MTLATTN_ERR_INVALID = -1,     /* bad argument (shape, stride, null pointer) */
+    MTLATTN_ERR_UNSUPPORTED = -2, /* valid request this build has no kernel for */
+    MTLATTN_ERR_WORKSPACE = -3,   /* workspace missing or too small */
+    MTLATTN_ERR_LAUNCH = -4       /* HIP reported an error at launch */
+};
+
+/*
+ * Problem description shared by every entry point. Mirrors the scalar part
+ * of the reference's kernel argument block `Params` (src/ext.mm:44-57) plus
+ * the bias strides of src/ext.mm:348-365.
+ */
+typedef struct mtlattn_problem {
+    int32_t dtype;            /* MTLATTN_DTYPE_* of q/k/v */
+    int32_t num_seqs;         /* B; cu_seqlens have B + 1 entries */
+    int64_t total_q;          /* rows of q / out / dout */
+    int64_t total_kv;         /* rows of k / v */
+    int32_t num_heads_q;      /* Hq */
+    int32_t num_heads_kv;     /* Hkv; Hq % Hkv == 0 */
+    int32_t head_dim;         /* D */
+    int32_t max_seqlen_q;     /* caller's bound on q lengths (decode routing only) */
+    float scale;              /* logit = scale * q.k (+ bias) */
+    int32_t causal;           /* 0 / 1 */
+    int32_t window;           /* <= 0: no sliding window */
+    const int32_t* cu_seqlens_q;   /* device int32 [B + 1] */
+    const int32_t* cu_seqlens_kv;  /* device int32 [B + 1] */
+    const float* bias;        /* optional fp32 additive mask, NULL = none */
+    int64_t bias_q_stride;    /* elements between query rows of bias */
+    int64_t bias_h_stride;    /* elements between heads; 0 = broadcast over heads */
+    int64_t bias_kv_cols;     /* size of bias's key dim; keys beyond read as 0 */
+} mtlattn_problem;
+
+/* Version of this header the library was built from (== MTLATTN_ABI_VERSION). */
+int mtlattn_abi_version(void);
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* mtlattn_last_error(void);
+
+/* Compute-unit count of `device` (256 on MI355X); <= 0 on error.
+ * Replaces _C.gpu_core_count (src/ext.mm:785). */
+int mtlattn_gpu_core_count(int device);
+
+/*
+ * Forward: out = softmax(scale * q k^T + bias + mask) v per sequence, plus the
+ * natural-log LSE per (row, head) when `lse` is non-NULL.
+ * Replaces _C.varlen_attention (src/ext.mm:293-489) including its routing:
+ * few-query / long-KV calls go to split-KV decode + combine
+ * (src/ext.mm:367-390), everything else to the flash forward.
+ *   out : contiguous [total_q, Hq, D], same dtype as q
+ *   lse : NULL or fp32 [total_q, Hq] (rows with no allowed key get -inf)
+ */
+size_t mtlattn_varlen_fwd_workspace_size(const mtlattn_problem* p);
+int mtlattn_varlen_fwd(const mtlattn_problem* p,
+                       const void* q, int64_t q_row_stride,
+                       const void* k, int64_t k_row_stride,
+                       const void* v, int64_t v_row_stride,
+                       void* out, float* lse,
+                       void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/*
+ * Backward: (dq, dk, dv) of the forward above given dout and the forward's
+ * out and lse. dk/dv of a kv head are summed over its Hq/Hkv query heads
+ * inside the kernels (no atomics; bitwise run-to-run deterministic).
+ * Replaces _C.varlen_attention_bwd (src/ext.mm:502-594). The reference needs
+ * contiguous inputs (mtlattn/__init__.py:42-45); this entry also takes row
+ * strides. dq/dk/dv are written contiguous in the input dtype.
+ */
+size_t mtlattn_varlen_bwd_workspace_size(const mtlattn_problem* p);
+int mtlattn_varlen_bwd(const mtlattn_problem* p,
+                       const void* q, int64_t q_row_stride,
+                       const void* k, int64_t k_row_stride,
+                       const void* v, int64_t v_row_stride,
+                       const void* out, int64_t out_row_stride,
+                       const void* dout, int64_t dout_row_stride,
+                       const float* lse,
+                       void* dq, void* dk, void* dv,
+                       void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/*
+ * delta[row, h] = sum_d dout[row, h, d] * out[row, h, d] in fp32.
+ * Replaces the torch reduction at src/ext.mm:518 / bwd_delta_impl
+ * (src/attention.metal:724-733). delta: fp32 [total_q, Hq].
+ */
+int mtlattn_bwd_preprocess(const mtlattn_problem* p,
+                           const void* out, int64_t out_row_stride,
+                           const void* dout, int64_t dout_row_stride,
+                           float* delta, void* stream);
+
+/*
+ * dQ alone (test entry). Replaces _C.mpp_bwd_dq (src/ext.mm:656-711).
+ * dq_dtype: MTLATTN_DTYPE_F32 (as the reference returns) or p->dtype.
+ */
+int mtlattn_bwd_dq(const mtlattn_problem* p,
+                   const void* q, int64_t q_row_stride,
+                   const void* k, int64_t k_row_stride,
+                   const void* v, int64_t v_row_stride,
+                   const void* dout, int64_t dout_row_stride,
+                   const float* lse, const float* delta,
+                   void* dq, int32_t dq_dtype, void* stream);
+
+/*
+ * dK and dV alone (test entry). Replaces _C.mpp_bwd_dkv (src/ext.mm:597-653).
+ * dkv_dtype: MTLATTN_DTYPE_F32 (as the reference returns) or p->dtype.
+ */
+int mtlattn_bwd_dkv(const mtlattn_problem* p,
+                    const void* q, int64_t q_row_stride,
+                    const void* k, int64_t k_row_stride,
+                    const void* v, int64_t v_row_stride,
+                    const void* dout, int64_t dout_row_stride,
+                    const float* lse, const float* delta,
+                    void* dk, void* dv, int32_t dkv_dtype, void* stream);
+
+/*
+ * Split-KV decode with an explicit split count (test entry): each split
+ * attends one chunk of every sequence's keys and writes a normalised fp32
+ * partial O and its LSE; a combine kernel merges them and also writes the
+ * final LSE when `lse` is non-NULL. num_splits == 1 is a plain forward.
+ * Replaces _C.attn_splitkv (src/ext.mm:716-773; kernels
+ * src/attn_mpp.metal:384-535). Requires fp16/bf16, D in {64, 128}, no bias,
+ * no window, max_seqlen_q * (Hq / Hkv) rows per kv head handled in groups of 16.
+ */
+size_t mtlattn_attn_splitkv_workspace_size(const mtlattn_problem* p, int32_t num_splits);
+int mtlattn_attn_splitkv(const mtlattn_problem* p,
+                         const void* q, int64_t q_row_stride,
+                         const void* k, int64_t k_row_stride,
+                         const void* v, int64_t v_row_stride,
+                         void* out, float* lse, int32_t num_splits,
+                         void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* Split count the forward's decode routing would choose for `p` (0 = the
+ * call is not routed to split-KV). Retunes src/ext.mm:372-388 for 256 CUs. */
+int32_t mtlattn_decode_num_splits(const mtlattn_problem* p);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTLATTN_CAPI_H */

@@ -1,0 +1,359 @@
+// C ABI of libmtlattn_hip.so (declared in include/mtlattn_capi.h): argument
+// validation, kernel-family routing and workspace sizing. Replaces the host
+// dispatcher of the reference (src/ext.mm:293-773) minus everything torch- or
+// Metal-specific; it never allocates device memory and never syncs the host.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "../../include/mtlattn_capi.h"
+#include "kernels.h"
+
+using namespace mtlattn;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return MTLATTN_OK;
+}
+
+int launch_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return ok();
+    return fail(MTLATTN_ERR_LAUNCH, "mtlattn: %s launch failed: %s", what, hipGetErrorString(e));
+}
+
+bool env_set(const char* name) {
+    const char* v = std::getenv(name);
+    return v != nullptr && v[0] != '\0' && std::strcmp(v, "0") != 0;
+}
+
+// Force the portable VALU kernels (MTLATTN_NO_MPP keeps the reference's name
+// for "skip the fast path", src/ext.mm:396).
+bool force_generic() { return env_set("MTLATTN_NO_MPP") || env_set("MTLATTN_NO_MFMA"); }
+
+bool is16(int dtype) { return dtype == MTLATTN_DTYPE_F16 || dtype == MTLATTN_DTYPE_BF16; }
+
+int elem_size(int dtype) { return dtype == MTLATTN_DTYPE_F32 ? 4 : 2; }
+
+bool aligned16(const void* ptr, int64_t row_stride, int dtype) {
+    return ((uintptr_t)ptr & 15u) == 0 && (row_stride * elem_size(dtype)) % 16 == 0;
+}
+
+// Shape/flag checks shared by every entry (src/ext.mm:306-331).
+int check_problem(const mtlattn_problem* p) {
+    if (p == nullptr) return fail(MTLATTN_ERR_INVALID, "mtlattn: null problem descriptor");
+    if (p->dtype != MTLATTN_DTYPE_F32 && p->dtype != MTLATTN_DTYPE_F16 && p->dtype != MTLATTN_DTYPE_BF16)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: unsupported dtype code %d", p->dtype);
+    if (p->num_seqs < 1) return fail(MTLATTN_ERR_INVALID, "mtlattn: cu_seqlens_q/kv must both be [B+1]");
+    if (p->total_q < 0 || p->total_kv < 0) return fail(MTLATTN_ERR_INVALID, "mtlattn: negative token count");
+    if (p->total_q > 0x7fffffffLL || p->total_kv > 0x7fffffffLL)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: more than 2^31 tokens is unsupported");
+    if (p->head_dim < 1 || p->head_dim > 256)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: head_dim %d unsupported (expected 1..256)", p->head_dim);
+    if (p->num_heads_kv <= 0 || p->num_heads_q <= 0 || p->num_heads_q % p->num_heads_kv != 0)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: query heads (%d) must be a multiple of kv heads (%d)",
+                    p->num_heads_q, p->num_heads_kv);
+    if (p->cu_seqlens_q == nullptr || p->cu_seqlens_kv == nullptr)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: cu_seqlens must be device int32 pointers");
+    if (p->bias != nullptr) {
+        if (p->bias_q_stride < 0 || p->bias_h_stride < 0 || p->bias_kv_cols < 0)
+            return fail(MTLATTN_ERR_INVALID, "mtlattn: attn_mask strides must be non-negative");
+    }
+    return MTLATTN_OK;
+}
+
+Geometry make_geo(const mtlattn_problem* p) {
+    Geometry g;
+    g.cu_q = p->cu_seqlens_q;
+    g.cu_kv = p->cu_seqlens_kv;
+    g.total_q = p->total_q;
+    g.total_kv = p->total_kv;
+    g.num_seqs = p->num_seqs;
+    g.hq = p->num_heads_q;
+    g.hkv = p->num_heads_kv;
+    g.g = p->num_heads_q / p->num_heads_kv;
+    g.d = p->head_dim;
+    g.scale = p->scale;
+    g.causal = p->causal ? 1 : 0;
+    g.window = p->window > 0 ? p->window : 0;
+    g.bias = p->bias;
+    g.bias_qs = p->bias_q_stride;
+    g.bias_hs = p->bias_h_stride;
+    g.bias_cols = p->bias_kv_cols;
+    return g;
+}
+
+int device_cus() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
+// Heads per 16-row decode group (largest divisor of g with heads * max_q <= 16).
+int decode_heads_per_group(int g, int max_q) {
+    int hpb = 16 / (max_q > 0 ? max_q : 1);
+    if (hpb > g) hpb = g;
+    if (hpb < 1) hpb = 1;
+    while (g % hpb != 0) --hpb;
+    return hpb;
+}
+
+// Split-KV applicability without the routing heuristics (kernel limits).
+bool splitkv_supported(const mtlattn_problem* p) {
+    return is16(p->dtype) && mfma_head_dim(p->head_dim) && p->bias == nullptr && p->window <= 0 &&
+           p->max_seqlen_q >= 1 && p->max_seqlen_q <= 16;
+}
+
+size_t splitkv_bytes(const mtlattn_problem* p, int ns) {
+    const size_t rows = (size_t)p->total_q * (size_t)p->num_heads_q;
+    const size_t o = rows * (size_t)p->head_dim * sizeof(float) * (size_t)ns;
+    const size_t l = rows * sizeof(float) * (size_t)ns;
+    return ((o + 255) & ~(size_t)255) + l;
+}
+
+int run_splitkv(const mtlattn_problem* p, const void* q, int64_t qrs, const void* k, int64_t krs, const void* v,
+                int64_t vrs, void* out, float* lse, int ns, void* ws, size_t ws_bytes, hipStream_t st) {
+    if (ws_bytes < splitkv_bytes(p, ns) || (ws == nullptr && splitkv_bytes(p, ns) > 0))
+        return fail(MTLATTN_ERR_WORKSPACE, "mtlattn: split-KV workspace too small (%zu < %zu bytes)", ws_bytes,
+                    splitkv_bytes(p, ns));
+    DecodeArgs a;
+    a.geo = make_geo(p);
+    a.q = q; a.q_rs = qrs; a.k = k; a.k_rs = krs; a.v = v; a.v_rs = vrs;
+    a.o = out; a.lse = lse;
+    const size_t rows = (size_t)p->total_q * (size_t)p->num_heads_q;
+    const size_t obytes = rows * (size_t)p->head_dim * sizeof(float) * (size_t)ns;
+    a.o_part = (float*)ws;
+    a.lse_part = (float*)((char*)ws + ((obytes + 255) & ~(size_t)255));
+    a.num_splits = ns;
+    a.max_q = p->max_seqlen_q;
+    return launch_status(launch_decode(p->dtype, a, st), "split-KV decode");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mtlattn_abi_version(void) { return MTLATTN_ABI_VERSION; }
+
+const char* mtlattn_last_error(void) { return g_last_error.c_str(); }
+
+int mtlattn_gpu_core_count(int device) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
+        fail(MTLATTN_ERR_INVALID, "mtlattn: no HIP device %d", device);
+        return 0;
+    }
+    return n;
+}
+
+int32_t mtlattn_decode_num_splits(const mtlattn_problem* p) {
+    if (check_problem(p) != MTLATTN_OK) return 0;
+    // Reference gate (src/ext.mm:372-376): few queries, long KV, no bias/window.
+    if (p->total_q <= 0 || env_set("MTLATTN_NO_SPLITKV") || force_generic() || !splitkv_supported(p)) return 0;
+    const int64_t avg_kv = p->total_kv / (p->num_seqs > 0 ? p->num_seqs : 1);
+    if (avg_kv < 2048) return 0;
+    // Splits: enough waves to fill every CU ~64 deep (waves are independent and
+    // short, so oversubscription balances ragged lengths), but >= 256 keys each.
+    const int g = p->num_heads_q / p->num_heads_kv;
+    const int64_t units = (int64_t)p->num_seqs * p->num_heads_kv * (g / decode_heads_per_group(g, p->max_seqlen_q));
+    int64_t ns = ((int64_t)device_cus() * 64 + units - 1) / units;
+    const int64_t cap = avg_kv / 256 > 1 ? avg_kv / 256 : 1;
+    if (ns > cap) ns = cap;
+    if (ns > 256) ns = 256;
+    if (ns < 1) ns = 1;
+    return (int32_t)ns;
+}
+
+size_t mtlattn_varlen_fwd_workspace_size(const mtlattn_problem* p) {
+    const int32_t ns = mtlattn_decode_num_splits(p);
+    return ns > 0 ? splitkv_bytes(p, ns) : 0;
+}
+
+int mtlattn_varlen_fwd(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
+                       int64_t k_row_stride, const void* v, int64_t v_row_stride, void* out, float* lse,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_problem(p);
+    if (rc != MTLATTN_OK) return rc;
+    if (p->total_q == 0) return ok();
+    if (q == nullptr || out == nullptr || (p->total_kv > 0 && (k == nullptr || v == nullptr)))
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: null q/k/v/out pointer");
+    hipStream_t st = (hipStream_t)stream;
+    const int32_t ns = mtlattn_decode_num_splits(p);
+    const bool vec_ok = aligned16(q, q_row_stride, p->dtype) && aligned16(k, k_row_stride, p->dtype) &&
+                        aligned16(v, v_row_stride, p->dtype) && ((uintptr_t)out & 15u) == 0;
+    if (ns > 0 && vec_ok)
+        return run_splitkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, ns, workspace,
+                           workspace_bytes, st);
+    FwdArgs a;
+    a.geo = make_geo(p);
+    a.q = q; a.q_rs = q_row_stride; a.k = k; a.k_rs = k_row_stride; a.v = v; a.v_rs = v_row_stride;
+    a.o = out; a.lse = lse;
+    if (is16(p->dtype) && mfma_head_dim(p->head_dim) && vec_ok && !force_generic())
+        return launch_status(launch_fwd_mfma(p->dtype, a, st), "flash forward");
+    return launch_status(launch_fwd_generic(p->dtype, a, st), "generic forward");
+}
+
+size_t mtlattn_varlen_bwd_workspace_size(const mtlattn_problem* p) {
+    if (check_problem(p) != MTLATTN_OK) return 0;
+    return (size_t)p->total_q * (size_t)p->num_heads_q * sizeof(float);
+}
+
+int mtlattn_bwd_preprocess(const mtlattn_problem* p, const void* out, int64_t out_row_stride, const void* dout,
+                           int64_t dout_row_stride, float* delta, void* stream) {
+    int rc = check_problem(p);
+    if (rc != MTLATTN_OK) return rc;
+    if (p->total_q == 0) return ok();
+    if (out == nullptr || dout == nullptr || delta == nullptr)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: null out/dout/delta pointer");
+    const Geometry g = make_geo(p);
+    return launch_status(launch_bwd_preprocess(p->dtype, g, out, out_row_stride, dout, dout_row_stride, delta,
+                                               (hipStream_t)stream),
+                         "delta preprocess");
+}
+
+namespace {
+
+BwdArgs make_bwd(const mtlattn_problem* p, const void* q, int64_t qrs, const void* k, int64_t krs, const void* v,
+                 int64_t vrs, const void* dout, int64_t dors, const float* lse, const float* delta) {
+    BwdArgs a;
+    a.geo = make_geo(p);
+    a.q = q; a.q_rs = qrs; a.k = k; a.k_rs = krs; a.v = v; a.v_rs = vrs; a.dout = dout; a.do_rs = dors;
+    a.lse = lse; a.delta = delta;
+    a.dq = nullptr; a.dk = nullptr; a.dv = nullptr; a.out_f32 = 0;
+    return a;
+}
+
+bool bwd_mfma_ok(const mtlattn_problem* p, const void* q, int64_t qrs, const void* k, int64_t krs, const void* v,
+                 int64_t vrs, const void* dout, int64_t dors) {
+    return is16(p->dtype) && mfma_head_dim(p->head_dim) && !force_generic() && aligned16(q, qrs, p->dtype) &&
+           aligned16(k, krs, p->dtype) && aligned16(v, vrs, p->dtype) && aligned16(dout, dors, p->dtype);
+}
+
+}  // namespace
+
+int mtlattn_bwd_dq(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
+                   int64_t k_row_stride, const void* v, int64_t v_row_stride, const void* dout,
+                   int64_t dout_row_stride, const float* lse, const float* delta, void* dq, int32_t dq_dtype,
+                   void* stream) {
+    int rc = check_problem(p);
+    if (rc != MTLATTN_OK) return rc;
+    if (dq_dtype != MTLATTN_DTYPE_F32 && dq_dtype != p->dtype)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: dq dtype must be fp32 or the input dtype");
+    if (p->total_q == 0) return ok();
+    if (q == nullptr || dout == nullptr || lse == nullptr || delta == nullptr || dq == nullptr ||
+        (p->total_kv > 0 && (k == nullptr || v == nullptr)))
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: null pointer argument");
+    BwdArgs a = make_bwd(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride, lse, delta);
+    a.dq = dq;
+    a.out_f32 = dq_dtype == MTLATTN_DTYPE_F32 ? 1 : 0;
+    hipStream_t st = (hipStream_t)stream;
+    if (bwd_mfma_ok(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride))
+        return launch_status(launch_bwd_dq_mfma(p->dtype, a, st), "dQ");
+    return launch_status(launch_bwd_dq_generic(p->dtype, a, st), "generic dQ");
+}
+
+int mtlattn_bwd_dkv(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
+                    int64_t k_row_stride, const void* v, int64_t v_row_stride, const void* dout,
+                    int64_t dout_row_stride, const float* lse, const float* delta, void* dk, void* dv,
+                    int32_t dkv_dtype, void* stream) {
+    int rc = check_problem(p);
+    if (rc != MTLATTN_OK) return rc;
+    if (dkv_dtype != MTLATTN_DTYPE_F32 && dkv_dtype != p->dtype)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: dk/dv dtype must be fp32 or the input dtype");
+    if (p->total_kv == 0) return ok();
+    if (k == nullptr || v == nullptr || dk == nullptr || dv == nullptr ||
+        (p->total_q > 0 && (q == nullptr || dout == nullptr || lse == nullptr || delta == nullptr)))
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: null pointer argument");
+    BwdArgs a = make_bwd(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride, lse, delta);
+    a.dk = dk;
+    a.dv = dv;
+    a.out_f32 = dkv_dtype == MTLATTN_DTYPE_F32 ? 1 : 0;
+    hipStream_t st = (hipStream_t)stream;
+    if (bwd_mfma_ok(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride))
+        return launch_status(launch_bwd_dkv_mfma(p->dtype, a, st), "dK/dV");
+    return launch_status(launch_bwd_dkv_generic(p->dtype, a, st), "generic dK/dV");
+}
+
+int mtlattn_varlen_bwd(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
+                       int64_t k_row_stride, const void* v, int64_t v_row_stride, const void* out,
+                       int64_t out_row_stride, const void* dout, int64_t dout_row_stride, const float* lse,
+                       void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_problem(p);
+    if (rc != MTLATTN_OK) return rc;
+    const size_t need = mtlattn_varlen_bwd_workspace_size(p);
+    if (workspace_bytes < need || (need > 0 && workspace == nullptr))
+        return fail(MTLATTN_ERR_WORKSPACE, "mtlattn: backward workspace too small (%zu < %zu bytes)",
+                    workspace_bytes, need);
+    float* delta = (float*)workspace;
+    if (p->total_q > 0) {
+        rc = mtlattn_bwd_preprocess(p, out, out_row_stride, dout, dout_row_stride, delta, stream);
+        if (rc != MTLATTN_OK) return rc;
+        rc = mtlattn_bwd_dq(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride, lse,
+                            delta, dq, p->dtype, stream);
+        if (rc != MTLATTN_OK) return rc;
+    }
+    rc = mtlattn_bwd_dkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride, lse, delta,
+                         dk, dv, p->dtype, stream);
+    if (rc != MTLATTN_OK) return rc;
+    // Rows outside every sequence take no part in the forward: zero gradient.
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t es = elem_size(p->dtype);
+    const int64_t qrow = (int64_t)p->num_heads_q * p->head_dim * es, krow = (int64_t)p->num_heads_kv * p->head_dim * es;
+    hipError_t e = launch_zero_outside(dq, qrow, p->total_q, p->cu_seqlens_q, p->num_seqs, st);
+    if (e == hipSuccess) e = launch_zero_outside(dk, krow, p->total_kv, p->cu_seqlens_kv, p->num_seqs, st);
+    if (e == hipSuccess) e = launch_zero_outside(dv, krow, p->total_kv, p->cu_seqlens_kv, p->num_seqs, st);
+    return launch_status(e, "gradient tail fill");
+}
+
+size_t mtlattn_attn_splitkv_workspace_size(const mtlattn_problem* p, int32_t num_splits) {
+    if (check_problem(p) != MTLATTN_OK || num_splits < 1) return 0;
+    return splitkv_bytes(p, num_splits);
+}
+
+int mtlattn_attn_splitkv(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
+                         int64_t k_row_stride, const void* v, int64_t v_row_stride, void* out, float* lse,
+                         int32_t num_splits, void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_problem(p);
+    if (rc != MTLATTN_OK) return rc;
+    if (!is16(p->dtype)) return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: half/bf16");
+    if (!mfma_head_dim(p->head_dim)) return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: D in {64,128}");
+    if (p->bias != nullptr || p->window > 0)
+        return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: no attn_mask or window on the split-KV path");
+    if (p->max_seqlen_q < 1 || p->max_seqlen_q > 16)
+        return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: max_seqlen_q must be in [1, 16]");
+    if (num_splits < 1 || num_splits > 4096) return fail(MTLATTN_ERR_INVALID, "splitkv: num_splits in [1, 4096]");
+    if (p->total_q == 0) return ok();
+    if (q == nullptr || out == nullptr || (p->total_kv > 0 && (k == nullptr || v == nullptr)))
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: null q/k/v/out pointer");
+    if (!aligned16(q, q_row_stride, p->dtype) || !aligned16(k, k_row_stride, p->dtype) ||
+        !aligned16(v, v_row_stride, p->dtype) || ((uintptr_t)out & 15u) != 0)
+        return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: q/k/v rows must be 16-byte aligned");
+    return run_splitkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, num_splits, workspace,
+                       workspace_bytes, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,215 @@
+// Device-side building blocks shared by the gfx950 attention kernels:
+// element types, bf16/fp16 <-> fp32 conversion, MFMA wrappers with their lane
+// layouts, LDS swizzles and varlen tile bookkeeping.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mtlattn {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kPosInf = __builtin_huge_valf();
+
+// ---------------------------------------------------------------------------
+// Element types. Storage is the raw 16-bit pattern (or fp32).
+// ---------------------------------------------------------------------------
+struct BF16 {
+    using raw = uint16_t;
+    static constexpr int code = 2;
+    __device__ static inline float to_float(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
+    // lo/hi packed into one dword, round-to-nearest-even (v_cvt_pk_bf16_f32)
+    __device__ static inline uint32_t pack2(float lo, float hi) {
+        bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+    __device__ static inline uint16_t from_float(float x) {
+        __bf16 b = (__bf16)x;
+        return __builtin_bit_cast(uint16_t, b);
+    }
+};
+
+struct F16 {
+    using raw = uint16_t;
+    static constexpr int code = 1;
+    __device__ static inline float to_float(uint16_t x) {
+        return (float)__builtin_bit_cast(_Float16, x);
+    }
+    __device__ static inline uint32_t pack2(float lo, float hi) {
+        f16x2_t v = {(_Float16)lo, (_Float16)hi};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+    __device__ static inline uint16_t from_float(float x) {
+        _Float16 h = (_Float16)x;
+        return __builtin_bit_cast(uint16_t, h);
+    }
+};
+
+struct F32 {
+    using raw = float;
+    static constexpr int code = 0;
+    __device__ static inline float to_float(float x) { return x; }
+    __device__ static inline float from_float(float x) { return x; }
+};
+
+// Unpack element e (0/1) of a dword holding two 16-bit values.
+template <typename T>
+__device__ inline float lo16(uint32_t w) { return T::to_float((uint16_t)(w & 0xffffu)); }
+template <typename T>
+__device__ inline float hi16(uint32_t w) { return T::to_float((uint16_t)(w >> 16)); }
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers. Operands are 8 packed 16-bit values in a u32x4.
+//
+// v_mfma_f32_32x32x16_{bf16,f16}: C[32x32] += A[32x16] * B[16x32]
+//   A: lane l holds row m = l%32, k = 8*(l/32) + j in dword j/2 (j = 0..7)
+//   B: lane l holds col n = l%32, k = 8*(l/32) + j
+//   C: lane l holds col n = l%32, rows m = 8*(r/4) + 4*(l/32) + r%4, r = 0..15
+// v_mfma_f32_16x16x32_{bf16,f16}: C[16x16] += A[16x32] * B[32x16]
+//   A: lane l holds row m = l%16, k = 8*(l/16) + j
+//   B: lane l holds col n = l%16, k = 8*(l/16) + j
+//   C: lane l holds col n = l%16, rows m = 4*(l/16) + r, r = 0..3
+// The contraction index k may be permuted freely as long as A and B agree;
+// the kernels use that to feed softmax results straight from C registers.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ inline f32x16_t mfma32(const u32x4_t& a, const u32x4_t& b, const f32x16_t& c);
+template <>
+__device__ inline f32x16_t mfma32<BF16>(const u32x4_t& a, const u32x4_t& b, const f32x16_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+template <>
+__device__ inline f32x16_t mfma32<F16>(const u32x4_t& a, const u32x4_t& b, const f32x16_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ inline f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c);
+template <>
+__device__ inline f32x4_t mfma16<BF16>(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+template <>
+__device__ inline f32x4_t mfma16<F16>(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Global / LDS vector access helpers.
+// ---------------------------------------------------------------------------
+__device__ inline u32x4_t ld16(const void* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+__device__ inline void st16(void* p, const u32x4_t& v) { *reinterpret_cast<u32x4_t*>(p) = v; }
+__device__ inline u32x2_t ld8(const void* p) { return *reinterpret_cast<const u32x2_t*>(p); }
+__device__ inline void st8(void* p, const u32x2_t& v) { *reinterpret_cast<u32x2_t*>(p) = v; }
+
+// Two 16-bit values (low halves / high halves of a and b) packed into a dword.
+__device__ inline uint32_t pack_lo16(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
+__device__ inline uint32_t pack_hi16(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xffff0000u); }
+
+// Transpose 4 rows x 8 columns of 16-bit values (each row one u32x4) into
+// 8 columns x 4 rows: out[c] = {row0[c], row1[c], row2[c], row3[c]} as a u32x2.
+__device__ inline void transpose4x8(const u32x4_t r[4], u32x2_t out[8]) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        out[2 * w + 0] = u32x2_t{pack_lo16(r[0][w], r[1][w]), pack_lo16(r[2][w], r[3][w])};
+        out[2 * w + 1] = u32x2_t{pack_hi16(r[0][w], r[1][w]), pack_hi16(r[2][w], r[3][w])};
+    }
+}
+
+// ---------------------------------------------------------------------------
+// LDS layouts.
+// Row-major tile [rows][D] of 16-bit values, 16-byte chunks XOR-swizzled by
+// (row & 7): a 32-lane MFMA operand read (32 rows, one chunk) and a coalesced
+// 16-lane row write are both bank-conflict free.
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ inline uint32_t rm_offset(int row, int chunk) {   // bytes
+    return (uint32_t)(row * (2 * D) + ((chunk ^ (row & 7)) << 4));
+}
+
+// Transposed tile [D][64] (64 columns of 16-bit, 128 B per row), 8-byte groups
+// of 4 columns XOR-swizzled by f(row) = (row & 15) ^ ((row >> 4) & 7): the
+// MFMA operand read (32 consecutive rows, one group) and the transposing write
+// (16 rows 8 apart, one group) are both conflict free.
+__device__ inline uint32_t tr_offset(int row, int group) {   // bytes
+    const int f = (row & 15) ^ ((row >> 4) & 7);
+    return (uint32_t)(row * 128 + ((group ^ f) << 3));
+}
+
+// ---------------------------------------------------------------------------
+// Wave reductions (64 lanes).
+// ---------------------------------------------------------------------------
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Varlen bookkeeping.
+// Tiles of `tile` rows are numbered globally without a host sync: sequence s
+// owns tiles [T_s, T_{s+1}) with T_s = cu[s] / tile + s, which always covers
+// ceil(len_s / tile) tiles. A grid of total / tile + num_seqs + 1 blocks is an
+// upper bound computable from tensor shapes alone.
+// ---------------------------------------------------------------------------
+struct SeqRange {
+    int start, end;   // clamped to [0, total]
+};
+
+__device__ inline SeqRange seq_range(const int* __restrict__ cu, int s, int64_t total) {
+    int a = cu[s], b = cu[s + 1];
+    const int t = (int)total;
+    a = a < 0 ? 0 : (a > t ? t : a);
+    b = b < a ? a : (b > t ? t : b);
+    return {a, b};
+}
+
+// Largest s in [0, num_seqs) with cu[s] / tile + s <= t (binary search; all
+// lanes compute the same value).
+__device__ inline int find_seq_for_tile(const int* __restrict__ cu, int num_seqs, int tile, int t,
+                                        int64_t total) {
+    int lo = 0, hi = num_seqs - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        int c = cu[mid];
+        c = c < 0 ? 0 : (c > (int)total ? (int)total : c);
+        if (c / tile + mid <= t) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+__device__ inline int tile_base(const int* __restrict__ cu, int s, int tile, int64_t total) {
+    int c = cu[s];
+    c = c < 0 ? 0 : (c > (int)total ? (int)total : c);
+    return c / tile + s;
+}
+
+// Map a linear block id so that consecutive logical ids run on the same XCD
+// (blocks are dispatched round-robin over the 8 XCDs of an MI355X), keeping
+// the K/V of one (sequence, head) in one XCD's L2.
+__device__ inline int xcd_remap(int id, int n) {
+    if ((n & 7) != 0) return id;
+    return (id & 7) * (n >> 3) + (id >> 3);
+}
+
+}  // namespace mtlattn

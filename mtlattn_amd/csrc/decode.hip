@@ -1,0 +1,298 @@
+// Split-KV decode for fp16/bf16 on gfx950 (counterpart of the reference's
+// attn_vl_split + attn_combine, src/attn_mpp.metal:384-535, redesigned).
+//
+// Decode is HBM-bound: the design goal is to read every K/V byte exactly once.
+//   * GQA packing: the q_len x (heads of one GQA group) query rows that share
+//     a kv head form the N dimension (16) of v_mfma_f32_16x16x32, so each K/V
+//     row is read once per kv head instead of once per query head (the
+//     reference's grid z = Hq re-reads it g times, src/ext.mm:760-761).
+//   * One wave = one split of one (sequence, kv head, head group). Waves never
+//     synchronise with each other, so a workgroup is just 4 independent waves.
+//   * Per 32-key tile: K goes straight from HBM into MFMA A-operand registers
+//     (16 B per lane); V is loaded coalesced and transposed through a per-wave
+//     LDS buffer for the P.V product. The next tile's loads are issued before
+//     the current tile is computed.
+//   * Each split writes a normalised fp32 partial O and its LSE; the combine
+//     kernel merges splits with LSE weights and, unlike the reference's
+//     (src/attn_mpp.metal:498-521), also writes the final LSE.
+#include "common.h"
+#include "kernels.h"
+#include "../../include/mtlattn_capi.h"
+
+namespace mtlattn {
+
+namespace {
+
+constexpr int kDecWaves = 4;
+constexpr int kDecKT = 32;      // keys per tile
+
+struct DecKParams {
+    const uint16_t* q; const uint16_t* k; const uint16_t* v;
+    float* o_part; float* lse_part;
+    const int* cu_q; const int* cu_kv;
+    int64_t q_rs, k_rs, v_rs;
+    int64_t total_q, total_kv;
+    int num_seqs, hq, hkv, g, hpb, n_hg, ns;
+    float scale_log2;
+    int causal;
+};
+
+// V^T tile [D][32] (64 B per row); 8-byte groups XOR-swizzled by row.
+__device__ inline uint32_t dec_tr_offset(int row, int group) {
+    const int f = ((row >> 1) ^ (row >> 3)) & 7;
+    return (uint32_t)(row * 64 + ((group ^ f) << 3));
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams p) {
+    constexpr int KC = D / 32;          // 32-wide k-chunks over D (QK^T)
+    constexpr int DB = D / 16;          // 16-row output blocks over D
+    constexpr int VU = D / 64;          // (4 keys x 8 d) units per lane per tile: (8 * D/8) / 64
+    __shared__ __attribute__((aligned(16))) char smem[kDecWaves * D * kDecKT * 2];
+
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n16 = lane & 15, lg = lane >> 4;
+    char* vt = smem + w * (D * kDecKT * 2);
+
+    int wid = blockIdx.x * kDecWaves + w;
+    const int split = wid % p.ns; wid /= p.ns;
+    const int hgi = wid % p.n_hg; wid /= p.n_hg;
+    const int hk = wid % p.hkv;
+    const int s = wid / p.hkv;
+    if (s >= p.num_seqs) return;
+    const SeqRange qr = seq_range(p.cu_q, s, p.total_q);
+    const SeqRange kr = seq_range(p.cu_kv, s, p.total_kv);
+    const int q_len = qr.end - qr.start, kv_len = kr.end - kr.start;
+    if (q_len == 0) return;
+    const int coff = kv_len - q_len;
+
+    // Row n of the N dimension: head hh = n / q_len of this group, query qi = n % q_len.
+    const int rows = p.hpb * q_len;
+    const bool row_ok = n16 < rows && n16 < 16;
+    const int hh = row_ok ? n16 / q_len : 0;
+    const int qi = row_ok ? n16 - hh * q_len : 0;
+    const int head = hk * p.g + hgi * p.hpb + hh;
+    const int64_t grow = qr.start + qi;
+
+    u32x4_t qf[KC];
+    {
+        const uint16_t* qp = p.q + grow * p.q_rs + (int64_t)head * D + 8 * lg;
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) qf[kc] = row_ok ? ld16(qp + 32 * kc) : u32x4_t{0, 0, 0, 0};
+    }
+
+    int chunk = (kv_len + p.ns - 1) / p.ns;
+    chunk = (chunk + kDecKT - 1) / kDecKT * kDecKT;
+    const int ks = split * chunk;
+    const int ke = min(kv_len, ks + chunk);
+    const int n_tiles = ke > ks ? (ke - ks + kDecKT - 1) / kDecKT : 0;
+
+    const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * D;
+    const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * D;
+
+    // Register tiles: K A-operands [2 key blocks][KC], V rows [VU units][4 keys].
+    u32x4_t ka[2][KC], vr[VU][4];
+    auto load = [&](int kt, u32x4_t (&ka_)[2][KC], u32x4_t (&vr_)[VU][4]) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            const int key = kt + 16 * mb + n16;
+            const bool ok = key < ke;
+            const uint16_t* kp = kbase + (int64_t)(ok ? key : 0) * p.k_rs + 8 * lg;
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc) ka_[mb][kc] = ok ? ld16(kp + 32 * kc) : u32x4_t{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < VU; ++u) {
+            const int uid = lane + 64 * u;
+            const int dc = uid % (D / 8), kg = uid / (D / 8);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = kt + 4 * kg + i;
+                vr_[u][i] = key < ke ? ld16(vbase + (int64_t)key * p.v_rs + 8 * dc) : u32x4_t{0, 0, 0, 0};
+            }
+        }
+    };
+
+    float m_run = kNegInf, l_run = 0.f;
+    f32x4_t oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    if (n_tiles > 0) load(ks, ka, vr);
+    for (int it = 0; it < n_tiles; ++it) {
+        const int kt = ks + it * kDecKT;
+        // stage V^T of this tile in the wave's LDS buffer
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int u = 0; u < VU; ++u) {
+            const int uid = lane + 64 * u;
+            const int dc = uid % (D / 8), kg = uid / (D / 8);
+            u32x2_t tr[8];
+            transpose4x8(vr[u], tr);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) st8(vt + dec_tr_offset(8 * dc + i, kg), tr[i]);
+        }
+        // S^T = K Q^T for the two 16-key blocks
+        f32x4_t sc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) sc[mb] = mfma16<T>(ka[mb][kc], qf[kc], sc[mb]);
+        }
+        // prefetch the next tile while the softmax and P.V run
+        if (it + 1 < n_tiles) load(kt + kDecKT, ka, vr);
+
+        const bool need_mask = (kt + kDecKT > ke) || (p.causal && kt + kDecKT - 1 > coff);
+        float mx = kNegInf;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = kt + 16 * mb + 4 * lg + r;
+                bool ok = row_ok;
+                if (need_mask) {
+                    ok = ok && key < ke;
+                    if (p.causal) ok = ok && key <= qi + coff;
+                }
+                const float x = ok ? sc[mb][r] * p.scale_log2 : kNegInf;
+                sc[mb][r] = x;
+                mx = fmaxf(mx, x);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = m_new == kNegInf ? 0.f : m_new;
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+        m_run = m_new;
+        float ls = 0.f;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = __builtin_amdgcn_exp2f(sc[mb][r] - m_use);
+                ls += e;
+                sc[mb][r] = e;
+            }
+        }
+        l_run = l_run * corr + ls;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) oacc[db] *= corr;
+        // P^T operand: slot j < 4 -> key 4 lg + j, j >= 4 -> key 16 + 4 lg + j - 4.
+        const u32x4_t pf = u32x4_t{T::pack2(sc[0][0], sc[0][1]), T::pack2(sc[0][2], sc[0][3]),
+                                   T::pack2(sc[1][0], sc[1][1]), T::pack2(sc[1][2], sc[1][3])};
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const int d = 16 * db + n16;
+            const u32x2_t x0 = ld8(vt + dec_tr_offset(d, lg));
+            const u32x2_t x1 = ld8(vt + dec_tr_offset(d, 4 + lg));
+            oacc[db] = mfma16<T>(u32x4_t{x0[0], x0[1], x1[0], x1[1]}, pf, oacc[db]);
+        }
+    }
+
+    // l_run is split over the 4 lane groups holding a row's keys.
+    float lt = l_run + __shfl_xor(l_run, 16);
+    lt += __shfl_xor(lt, 32);
+    if (row_ok) {
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        float* op = p.o_part + (((int64_t)split * p.total_q + grow) * p.hq + head) * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const int d = 16 * db + 4 * lg;
+            *reinterpret_cast<f32x4_t*>(op + d) = oacc[db] * inv;
+        }
+        if (lg == 0)
+            p.lse_part[((int64_t)split * p.total_q + grow) * p.hq + head] =
+                lt > 0.f ? m_run * kLn2 + logf(lt) : kNegInf;
+    }
+}
+
+// One wave per (row, head): O = sum_s w_s O_s / sum_s w_s with w_s = exp(lse_s - max lse).
+template <typename T>
+__global__ __launch_bounds__(256) void decode_combine_kernel(const float* __restrict__ o_part,
+                                                             const float* __restrict__ lse_part,
+                                                             typename T::raw* __restrict__ out,
+                                                             float* __restrict__ lse_out, int64_t total_q,
+                                                             int hq, int d, int ns) {
+    const int64_t rh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (rh >= total_q * hq) return;
+    const int64_t stride = total_q * hq;
+    float m = kNegInf;
+    for (int s = 0; s < ns; ++s) m = fmaxf(m, lse_part[s * stride + rh]);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float wsum = 0.f;
+    if (m != kNegInf) {
+        for (int s = 0; s < ns; ++s) {
+            const float l = lse_part[s * stride + rh];
+            if (l == kNegInf) continue;
+            const float wgt = __expf(l - m);
+            wsum += wgt;
+            const float* op = o_part + (s * stride + rh) * d;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int dd = lane + 64 * i;
+                if (dd < d) acc[i] += wgt * op[dd];
+            }
+        }
+    }
+    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int dd = lane + 64 * i;
+        if (dd < d) out[rh * d + dd] = T::from_float(acc[i] * inv);
+    }
+    if (lse_out != nullptr && lane == 0) lse_out[rh] = wsum > 0.f ? m + logf(wsum) : kNegInf;
+}
+
+template <typename T, int D>
+hipError_t launch_typed(const DecodeArgs& a, hipStream_t st) {
+    const Geometry& g = a.geo;
+    DecKParams p;
+    p.q = (const uint16_t*)a.q; p.k = (const uint16_t*)a.k; p.v = (const uint16_t*)a.v;
+    p.o_part = a.o_part; p.lse_part = a.lse_part;
+    p.cu_q = g.cu_q; p.cu_kv = g.cu_kv;
+    p.q_rs = a.q_rs; p.k_rs = a.k_rs; p.v_rs = a.v_rs;
+    p.total_q = g.total_q; p.total_kv = g.total_kv;
+    p.num_seqs = g.num_seqs; p.hq = g.hq; p.hkv = g.hkv; p.g = g.g;
+    const int mq = a.max_q > 0 ? a.max_q : 1;
+    int hpb = 16 / mq;                  // heads per 16-row group: largest divisor of g that fits
+    if (hpb < 1) return hipErrorInvalidValue;
+    if (hpb > g.g) hpb = g.g;
+    while (g.g % hpb != 0) --hpb;
+    p.hpb = hpb;
+    p.n_hg = g.g / hpb;
+    p.ns = a.num_splits;
+    p.scale_log2 = g.scale * kLog2e;
+    p.causal = g.causal;
+    const int64_t waves = (int64_t)g.num_seqs * g.hkv * p.n_hg * p.ns;
+    const int64_t blocks = (waves + kDecWaves - 1) / kDecWaves;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    if (blocks > 0)
+        hipLaunchKernelGGL((decode_split_kernel<T, D>), dim3((unsigned)blocks), dim3(kDecWaves * 64), 0, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t rh = g.total_q * g.hq;
+    if (rh > 0)
+        hipLaunchKernelGGL(decode_combine_kernel<T>, dim3((unsigned)((rh + 3) / 4)), dim3(256), 0, st,
+                           (const float*)a.o_part, (const float*)a.lse_part, (typename T::raw*)a.o, a.lse,
+                           g.total_q, g.hq, D, p.ns);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_decode(int dtype, const DecodeArgs& a, hipStream_t st) {
+    const int d = a.geo.d;
+    if (dtype == MTLATTN_DTYPE_BF16) {
+        if (d == 128) return launch_typed<BF16, 128>(a, st);
+        if (d == 64) return launch_typed<BF16, 64>(a, st);
+    } else if (dtype == MTLATTN_DTYPE_F16) {
+        if (d == 128) return launch_typed<F16, 128>(a, st);
+        if (d == 64) return launch_typed<F16, 64>(a, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace mtlattn

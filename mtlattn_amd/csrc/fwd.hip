@@ -1,0 +1,310 @@
+// Flash forward for fp16/bf16 on gfx950 MFMA (counterpart of the reference's
+// attn_vl, src/attn_mpp.metal:178-317, redesigned for CDNA4).
+//
+// Work decomposition
+//   * Workgroup = 8 waves (512 threads, 2 waves per SIMD). Each wave owns 32
+//     query rows of one query head. The workgroup packs `hpw` = gcd(g, 8) query
+//     heads of one GQA group, so every K/V tile staged in LDS serves
+//     hpw * (8 / hpw) * 32 = 256 query-head rows.
+//   * Key tiles of 64 rows are double-buffered in LDS: K row-major (swizzled),
+//     V transposed to [D][64] in registers on the way in, so the P.V product
+//     reads V^T operands with contiguous 8-byte LDS loads.
+//   * Per wave and key tile:  S^T = K Q^T  (v_mfma_f32_32x32x16, 2 x D/16
+//     instructions), online softmax in base 2 on the C registers (each lane
+//     holds one query column, so max/sum need one cross-half exchange), then
+//     O^T += V^T P^T (4 x D/32 instructions) with P rounded to the input type.
+//   * Causal/window tiles outside a wave's band are skipped; the workgroup's
+//     key loop starts at the window bottom and stops at the causal horizon, so
+//     sliding-window cost is O(W) (src/attn_mpp.metal:216-225).
+//   * Varlen tiles are numbered without a host sync (common.h), blocks are
+//     remapped so neighbouring query tiles of one (sequence, head) share an XCD.
+#include "common.h"
+#include "kernels.h"
+#include "../../include/mtlattn_capi.h"
+
+namespace mtlattn {
+
+namespace {
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kKT = 64;          // keys per tile
+
+struct FwdKParams {
+    const uint16_t* q; const uint16_t* k; const uint16_t* v;
+    uint16_t* o; float* lse;
+    const int* cu_q; const int* cu_kv;
+    const float* bias;
+    int64_t q_rs, k_rs, v_rs;
+    int64_t bias_qs, bias_hs, bias_cols;
+    int64_t total_q, total_kv;
+    int num_seqs, hq, g, hpw, n_tiles, n_hg;
+    float scale_log2;
+    int causal, window;
+};
+
+template <typename T, int D, bool BIAS>
+__global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
+    constexpr int DC = D / 16;               // MFMA k-chunks over D
+    constexpr int DB = D / 32;               // 32-row output blocks over D
+    constexpr int KS_BYTES = kKT * D * 2;
+    constexpr int STAGE = 2 * KS_BYTES;      // K tile + V^T tile
+    constexpr int VUNITS = 2 * D;            // (4 keys x 8 d) units per V tile
+    constexpr int KCH = kKT * D / 8 / 256;   // 16-byte K chunks per loader thread
+    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int QT = 32 * (kWaves / p.hpw);
+    const int L = xcd_remap(blockIdx.x, p.n_tiles * p.n_hg);
+    const int hg = L / p.n_tiles;
+    const int t = p.n_tiles - 1 - (L - hg * p.n_tiles);   // late (heavier) tiles first
+    const int s = find_seq_for_tile(p.cu_q, p.num_seqs, QT, t, p.total_q);
+    const int tb = tile_base(p.cu_q, s, QT, p.total_q);
+    if (t < tb) return;
+    const SeqRange qr = seq_range(p.cu_q, s, p.total_q);
+    const SeqRange kr = seq_range(p.cu_kv, s, p.total_kv);
+    const int q_len = qr.end - qr.start, kv_len = kr.end - kr.start;
+    const int q0 = (t - tb) * QT;
+    if (q0 >= q_len) return;
+
+    const int wph = kWaves / p.hpw;
+    const int head = hg * p.hpw + w / wph;
+    const int hk = head / p.g;
+    const int qa = q0 + 32 * (w % wph);          // first query row of this wave (seq-local)
+    const int coff = kv_len - q_len;
+    const bool wave_active = qa < q_len;
+    const int wq_last = min(q_len, qa + 32) - 1;
+
+    // Q^T operand fragments: lane holds query qa + l32, d = 16 kc + 8 hi + (0..7).
+    u32x4_t qf[DC];
+    {
+        const int row = qa + l32;
+        const bool ok = row < q_len;
+        const uint16_t* qp = p.q + (int64_t)(qr.start + (ok ? row : 0)) * p.q_rs + (int64_t)head * D + 8 * hi;
+#pragma unroll
+        for (int kc = 0; kc < DC; ++kc) qf[kc] = ok ? ld16(qp + 16 * kc) : u32x4_t{0, 0, 0, 0};
+    }
+
+    // Key range of the whole workgroup.
+    const int q_last_wg = min(q_len, q0 + QT) - 1;
+    const int kv_hi = p.causal ? min(kv_len, q_last_wg + coff + 1) : kv_len;
+    int kv_lo = 0;
+    if (p.window > 0) {
+        kv_lo = max(0, q0 + coff - p.window + 1);
+        kv_lo = (kv_lo / kKT) * kKT;
+    }
+    const int n_kv_tiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kKT - 1) / kKT : 0;
+
+    const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * D;
+    const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * D;
+
+    // Loader roles: waves 0-3 stage V (transposed), waves 4-7 stage K.
+    u32x4_t pre[4];
+    auto load_tile = [&](int kt) {
+        if (w < 4) {
+            if (tid < VUNITS) {
+                const int dc = tid % (D / 8), kg = tid / (D / 8);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = kt + 4 * kg + i;
+                    pre[i] = key < kv_len ? ld16(vbase + (int64_t)key * p.v_rs + 8 * dc) : u32x4_t{0, 0, 0, 0};
+                }
+            }
+        } else {
+            const int t2 = tid - 256;
+#pragma unroll
+            for (int i = 0; i < KCH; ++i) {
+                const int cid = t2 + 256 * i;
+                const int row = cid / (D / 8), c = cid % (D / 8);
+                const int key = kt + row;
+                pre[i] = key < kv_len ? ld16(kbase + (int64_t)key * p.k_rs + 8 * c) : u32x4_t{0, 0, 0, 0};
+            }
+        }
+    };
+    auto store_tile = [&](int buf) {
+        char* Ks = smem + buf * STAGE;
+        char* Vt = Ks + KS_BYTES;
+        if (w < 4) {
+            if (tid < VUNITS) {
+                const int dc = tid % (D / 8), kg = tid / (D / 8);
+                u32x2_t tr[8];
+                transpose4x8(pre, tr);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) st8(Vt + tr_offset(8 * dc + i, kg), tr[i]);
+            }
+        } else {
+            const int t2 = tid - 256;
+#pragma unroll
+            for (int i = 0; i < KCH; ++i) {
+                const int cid = t2 + 256 * i;
+                st16(Ks + rm_offset<D>(cid / (D / 8), cid % (D / 8)), pre[i]);
+            }
+        }
+    };
+
+    float m_run = kNegInf, l_run = 0.f;
+    f32x16_t oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] = f32x16_t{};
+
+    const int qrow = qa + l32;
+    const float* brow = nullptr;
+    if (BIAS && qrow < q_len)
+        brow = p.bias + (int64_t)(qr.start + qrow) * p.bias_qs + (int64_t)head * p.bias_hs;
+
+    if (n_kv_tiles > 0) {
+        load_tile(kv_lo);
+        store_tile(0);
+        __syncthreads();
+        for (int it = 0; it < n_kv_tiles; ++it) {
+            const int kt = kv_lo + it * kKT;
+            const bool has_next = it + 1 < n_kv_tiles;
+            if (has_next) load_tile(kt + kKT);
+
+            bool skip = !wave_active;
+            if (p.causal && kt > wq_last + coff) skip = true;
+            if (p.window > 0 && kt + kKT - 1 < qa + coff - p.window + 1) skip = true;
+            if (!skip) {
+                const char* Ks = smem + (it & 1) * STAGE;
+                const char* Vt = Ks + KS_BYTES;
+                f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
+#pragma unroll
+                for (int kc = 0; kc < DC; ++kc) {
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) {
+                        const u32x4_t a = ld16(Ks + rm_offset<D>(32 * kb + l32, 2 * kc + hi));
+                        sacc[kb] = mfma32<T>(a, qf[kc], sacc[kb]);
+                    }
+                }
+                const bool need_mask = (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
+                                       (p.window > 0 && kt < wq_last + coff - p.window + 1);
+                // scaled base-2 logits (+ bias), masked entries -> -inf
+                float mx = kNegInf;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
+                        float x = sacc[kb][r] * p.scale_log2;
+                        bool ok = true;
+                        if (need_mask) {
+                            ok = key < kv_len;
+                            if (p.causal) ok = ok && key <= qrow + coff;
+                            if (p.window > 0) ok = ok && key > qrow + coff - p.window;
+                        }
+                        if (BIAS && ok && brow != nullptr && key < p.bias_cols) x += brow[key] * kLog2e;
+                        x = ok ? x : kNegInf;
+                        sacc[kb][r] = x;
+                        mx = fmaxf(mx, x);
+                    }
+                }
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                const float m_new = fmaxf(m_run, mx);
+                const float m_use = m_new == kNegInf ? 0.f : m_new;
+                const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+                m_run = m_new;
+                float ls = 0.f;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float e = __builtin_amdgcn_exp2f(sacc[kb][r] - m_use);
+                        ls += e;
+                        sacc[kb][r] = e;
+                    }
+                }
+                l_run = l_run * corr + ls;
+                if (__any(corr != 1.f)) {
+#pragma unroll
+                    for (int db = 0; db < DB; ++db) oacc[db] *= corr;
+                }
+                // P^T operands: chunk c covers tile keys 16c + 8(j/4) + 4hi + j%4.
+                u32x4_t pf[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int kb = c >> 1, r0 = 8 * (c & 1);
+                    pf[c] = u32x4_t{T::pack2(sacc[kb][r0 + 0], sacc[kb][r0 + 1]),
+                                    T::pack2(sacc[kb][r0 + 2], sacc[kb][r0 + 3]),
+                                    T::pack2(sacc[kb][r0 + 4], sacc[kb][r0 + 5]),
+                                    T::pack2(sacc[kb][r0 + 6], sacc[kb][r0 + 7])};
+                }
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+#pragma unroll
+                    for (int db = 0; db < DB; ++db) {
+                        const int d = 32 * db + l32;
+                        const u32x2_t x0 = ld8(Vt + tr_offset(d, 4 * c + hi));
+                        const u32x2_t x1 = ld8(Vt + tr_offset(d, 4 * c + 2 + hi));
+                        oacc[db] = mfma32<T>(u32x4_t{x0[0], x0[1], x1[0], x1[1]}, pf[c], oacc[db]);
+                    }
+                }
+            }
+            if (has_next) store_tile((it + 1) & 1);
+            __syncthreads();
+        }
+    }
+
+    // Epilogue: lanes l and l^32 hold the two halves of one query's row sum.
+    const float lt = l_run + __shfl_xor(l_run, 32);
+    if (wave_active && qrow < q_len) {
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        uint16_t* op = p.o + (int64_t)(qr.start + qrow) * ((int64_t)p.hq * D) + (int64_t)head * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const int d = 32 * db + 8 * rg + 4 * hi;
+                st8(op + d, u32x2_t{T::pack2(oacc[db][4 * rg + 0] * inv, oacc[db][4 * rg + 1] * inv),
+                                    T::pack2(oacc[db][4 * rg + 2] * inv, oacc[db][4 * rg + 3] * inv)});
+            }
+        }
+        if (p.lse != nullptr && hi == 0)
+            p.lse[(int64_t)(qr.start + qrow) * p.hq + head] = lt > 0.f ? m_run * kLn2 + logf(lt) : kNegInf;
+    }
+}
+
+int gcd_int(int a, int b) { while (b) { const int t = a % b; a = b; b = t; } return a; }
+
+template <typename T, int D>
+hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
+    const Geometry& g = a.geo;
+    FwdKParams p;
+    p.q = (const uint16_t*)a.q; p.k = (const uint16_t*)a.k; p.v = (const uint16_t*)a.v;
+    p.o = (uint16_t*)a.o; p.lse = a.lse;
+    p.cu_q = g.cu_q; p.cu_kv = g.cu_kv; p.bias = g.bias;
+    p.q_rs = a.q_rs; p.k_rs = a.k_rs; p.v_rs = a.v_rs;
+    p.bias_qs = g.bias_qs; p.bias_hs = g.bias_hs; p.bias_cols = g.bias_cols;
+    p.total_q = g.total_q; p.total_kv = g.total_kv;
+    p.num_seqs = g.num_seqs; p.hq = g.hq; p.g = g.g;
+    p.hpw = gcd_int(g.g, kWaves);
+    const int QT = 32 * (kWaves / p.hpw);
+    p.n_tiles = (int)(g.total_q / QT) + g.num_seqs + 1;
+    p.n_hg = g.hq / p.hpw;
+    p.scale_log2 = g.scale * kLog2e;
+    p.causal = g.causal; p.window = g.window > 0 ? g.window : 0;
+    const int64_t blocks = (int64_t)p.n_tiles * p.n_hg;
+    if (blocks <= 0) return hipSuccess;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    if (g.bias != nullptr)
+        hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true>), dim3((unsigned)blocks), dim3(kThreads), 0, st, p);
+    else
+        hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false>), dim3((unsigned)blocks), dim3(kThreads), 0, st, p);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_fwd_mfma(int dtype, const FwdArgs& a, hipStream_t st) {
+    const int d = a.geo.d;
+    if (dtype == MTLATTN_DTYPE_BF16) {
+        if (d == 128) return launch_typed<BF16, 128>(a, st);
+        if (d == 64) return launch_typed<BF16, 64>(a, st);
+    } else if (dtype == MTLATTN_DTYPE_F16) {
+        if (d == 128) return launch_typed<F16, 128>(a, st);
+        if (d == 64) return launch_typed<F16, 64>(a, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace mtlattn

@@ -1,0 +1,75 @@
+// Kernel parameter blocks and host-side launchers of the gfx950 kernels.
+// Included by the kernel sources and by the C ABI (capi.hip); not installed.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mtlattn {
+
+// Tensor geometry shared by every kernel (the scalar block of the reference's
+// Params, src/ext.mm:44-57, with 64-bit row strides).
+struct Geometry {
+    const int* cu_q;
+    const int* cu_kv;
+    int64_t total_q, total_kv;
+    int num_seqs, hq, hkv, g, d;
+    float scale;
+    int causal, window;
+    const float* bias;            // nullptr = no bias
+    int64_t bias_qs, bias_hs, bias_cols;
+};
+
+struct FwdArgs {
+    Geometry geo;
+    const void* q; int64_t q_rs;
+    const void* k; int64_t k_rs;
+    const void* v; int64_t v_rs;
+    void* o;                      // contiguous [total_q, hq, d]
+    float* lse;                   // nullable [total_q, hq]
+};
+
+struct BwdArgs {
+    Geometry geo;
+    const void* q; int64_t q_rs;
+    const void* k; int64_t k_rs;
+    const void* v; int64_t v_rs;
+    const void* dout; int64_t do_rs;
+    const float* lse;             // [total_q, hq]
+    const float* delta;           // [total_q, hq]
+    void* dq;                     // contiguous [total_q, hq, d]
+    void* dk;                     // contiguous [total_kv, hkv, d]
+    void* dv;
+    int out_f32;                  // 1: dq/dk/dv are fp32, 0: input dtype
+};
+
+struct DecodeArgs {
+    Geometry geo;
+    const void* q; int64_t q_rs;
+    const void* k; int64_t k_rs;
+    const void* v; int64_t v_rs;
+    void* o;                      // contiguous [total_q, hq, d]
+    float* lse;                   // nullable
+    float* o_part;                // [ns, total_q, hq, d]
+    float* lse_part;              // [ns, total_q, hq]
+    int num_splits;
+    int max_q;                    // bound on q lengths; heads_per_group * max_q <= 16
+};
+
+// Launchers return hipSuccess or the launch error. `dtype` is MTLATTN_DTYPE_*.
+hipError_t launch_fwd_mfma(int dtype, const FwdArgs& a, hipStream_t st);
+hipError_t launch_fwd_generic(int dtype, const FwdArgs& a, hipStream_t st);
+hipError_t launch_bwd_preprocess(int dtype, const Geometry& geo, const void* o, int64_t o_rs,
+                                 const void* dout, int64_t do_rs, float* delta, hipStream_t st);
+hipError_t launch_bwd_dq_mfma(int dtype, const BwdArgs& a, hipStream_t st);
+hipError_t launch_bwd_dkv_mfma(int dtype, const BwdArgs& a, hipStream_t st);
+hipError_t launch_bwd_dq_generic(int dtype, const BwdArgs& a, hipStream_t st);
+hipError_t launch_bwd_dkv_generic(int dtype, const BwdArgs& a, hipStream_t st);
+hipError_t launch_zero_outside(void* ptr, int64_t row_bytes, int64_t total_rows, const int* cu, int num_seqs,
+                               hipStream_t st);
+hipError_t launch_decode(int dtype, const DecodeArgs& a, hipStream_t st);
+
+// Which head dims have MFMA kernels.
+inline bool mfma_head_dim(int d) { return d == 64 || d == 128; }
+
+}  // namespace mtlattn

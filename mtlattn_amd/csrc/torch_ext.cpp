@@ -1,0 +1,274 @@
+// mtlattn._C for PyTorch-ROCm: the thin torch binding over the C ABI of
+// libmtlattn_hip.so. Replaces the reference's pybind11 module
+// (src/ext.mm:784-811) with the same function names, argument names and
+// defaults. Tensor checks mirror src/ext.mm:306-365 (TORCH_CHECK ->
+// RuntimeError); outputs and scratch are allocated through torch's caching
+// allocator; work is enqueued on the current HIP stream of the input's device
+// with no host synchronisation.
+#include <torch/extension.h>
+
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <c10/core/DeviceGuard.h>
+
+#include <tuple>
+
+#include "../../include/mtlattn_capi.h"
+
+namespace {
+
+int dtype_code(at::ScalarType t) {
+    switch (t) {
+        case at::kFloat: return MTLATTN_DTYPE_F32;
+        case at::kHalf: return MTLATTN_DTYPE_F16;
+        case at::kBFloat16: return MTLATTN_DTYPE_BF16;
+        default: TORCH_CHECK(false, "mtlattn: unsupported dtype ", t);
+    }
+    return -1;
+}
+
+void check_rc(int rc) { TORCH_CHECK(rc == MTLATTN_OK, mtlattn_last_error()); }
+
+void* current_stream(const at::Tensor& t) {
+    return (void*)at::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream();
+}
+
+bool defined(const c10::optional<at::Tensor>& t) { return t.has_value() && t->defined() && t->numel() > 0; }
+
+// q/k/v layout checks of src/ext.mm:306-331.
+void check_qkv(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
+    TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(), "mtlattn: q/k/v must be GPU (HIP) tensors");
+    TORCH_CHECK(q.dim() == 3 && k.dim() == 3 && v.dim() == 3, "mtlattn: q/k/v must be [M, H, D]");
+    const auto H = q.size(1), H_kv = k.size(1), D = q.size(2);
+    TORCH_CHECK(D >= 1 && D <= 256, "mtlattn: head_dim ", D, " unsupported (expected 1..256)");
+    TORCH_CHECK(v.size(1) == H_kv && k.size(2) == D && v.size(2) == D, "mtlattn: k/v head/dim shape mismatch");
+    TORCH_CHECK(k.size(0) == v.size(0), "mtlattn: k/v token count mismatch");
+    TORCH_CHECK(H_kv > 0 && H % H_kv == 0, "mtlattn: query heads (", H, ") must be a multiple of kv heads (", H_kv,
+                ")");
+    TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type(), "mtlattn: dtype mismatch");
+    dtype_code(q.scalar_type());
+    for (const auto& t : {q, k, v}) {
+        TORCH_CHECK((t.size(2) == 1 || t.stride(2) == 1) && (t.size(1) == 1 || t.stride(1) == D),
+                    "mtlattn: inner dims must be contiguous ([M, H, D] with row-only striding)");
+        TORCH_CHECK(t.get_device() == q.get_device(), "mtlattn: q/k/v must be on the same device");
+    }
+}
+
+void check_cu(const at::Tensor& cu_q, const at::Tensor& cu_kv, const at::Tensor& q) {
+    TORCH_CHECK(cu_q.is_cuda() && cu_kv.is_cuda(), "mtlattn: cu_seqlens must be on the GPU");
+    TORCH_CHECK(cu_q.get_device() == q.get_device() && cu_kv.get_device() == q.get_device(),
+                "mtlattn: cu_seqlens must be on the device of q");
+    TORCH_CHECK(cu_q.scalar_type() == at::kInt && cu_kv.scalar_type() == at::kInt, "mtlattn: cu_seqlens must be int32");
+    TORCH_CHECK(cu_q.dim() == 1 && cu_kv.dim() == 1 && cu_q.numel() == cu_kv.numel() && cu_q.numel() >= 2,
+                "mtlattn: cu_seqlens_q/kv must both be [B+1]");
+}
+
+int64_t row_stride(const at::Tensor& t) { return t.size(0) > 1 ? t.stride(0) : t.size(1) * t.size(2); }
+
+// Bias checks of src/ext.mm:348-365, plus the key-dim extent for bounds.
+void fill_bias(mtlattn_problem& p, const c10::optional<at::Tensor>& attn_bias, const at::Tensor& q,
+               at::Tensor& keep) {
+    p.bias = nullptr;
+    p.bias_q_stride = p.bias_h_stride = p.bias_kv_cols = 0;
+    if (!defined(attn_bias)) return;
+    keep = *attn_bias;
+    TORCH_CHECK(keep.is_cuda() && keep.get_device() == q.get_device(), "mtlattn: attn_mask must be a GPU tensor");
+    TORCH_CHECK(keep.scalar_type() == at::kFloat, "mtlattn: attn_mask must be float32");
+    TORCH_CHECK(keep.dim() == 3, "mtlattn: attn_mask must be [total_q, H or 1, max_kv]");
+    TORCH_CHECK(keep.size(0) == q.size(0), "mtlattn: attn_mask dim0 (", keep.size(0), ") must equal total_q (",
+                q.size(0), ")");
+    TORCH_CHECK(keep.size(1) == q.size(1) || keep.size(1) == 1, "mtlattn: attn_mask dim1 must be num_heads (",
+                q.size(1), ") or 1 (broadcast)");
+    TORCH_CHECK(keep.size(2) <= 1 || keep.stride(2) == 1, "mtlattn: attn_mask last dim must be contiguous");
+    p.bias = keep.data_ptr<float>();
+    p.bias_q_stride = keep.stride(0);
+    p.bias_h_stride = keep.size(1) == 1 ? 0 : keep.stride(1);
+    p.bias_kv_cols = keep.size(2);
+}
+
+mtlattn_problem make_problem(const at::Tensor& q, const at::Tensor& k, const at::Tensor& cu_q,
+                             const at::Tensor& cu_kv, int64_t max_seqlen_q, double scale, bool causal,
+                             int64_t window) {
+    mtlattn_problem p;
+    std::memset(&p, 0, sizeof(p));
+    p.dtype = dtype_code(q.scalar_type());
+    p.num_seqs = (int32_t)(cu_q.numel() - 1);
+    p.total_q = q.size(0);
+    p.total_kv = k.size(0);
+    p.num_heads_q = (int32_t)q.size(1);
+    p.num_heads_kv = (int32_t)k.size(1);
+    p.head_dim = (int32_t)q.size(2);
+    p.max_seqlen_q = (int32_t)std::min<int64_t>(max_seqlen_q, 0x7fffffff);
+    p.scale = (float)scale;
+    p.causal = causal ? 1 : 0;
+    p.window = window > 0 ? (int32_t)std::min<int64_t>(window, 0x7fffffff) : 0;
+    p.cu_seqlens_q = cu_q.data_ptr<int32_t>();
+    p.cu_seqlens_kv = cu_kv.data_ptr<int32_t>();
+    return p;
+}
+
+at::Tensor workspace(int64_t bytes, const at::Tensor& like) {
+    return at::empty({std::max<int64_t>(bytes, 1)}, like.options().dtype(at::kByte));
+}
+
+// _C.varlen_attention (src/ext.mm:293-489).
+at::Tensor varlen_attention(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                            const at::Tensor& cu_seqlens_q, const at::Tensor& cu_seqlens_kv, int64_t max_seqlen_q,
+                            double scale, bool causal, int64_t window, c10::optional<at::Tensor> lse_out,
+                            c10::optional<at::Tensor> attn_bias) {
+    check_qkv(q, k, v);
+    check_cu(cu_seqlens_q, cu_seqlens_kv, q);
+    const c10::OptionalDeviceGuard guard(q.device());
+    auto cu_q = cu_seqlens_q.contiguous(), cu_kv = cu_seqlens_kv.contiguous();
+    auto out = at::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+    float* lse = nullptr;
+    if (defined(lse_out)) {
+        const at::Tensor& l = *lse_out;
+        TORCH_CHECK(l.is_cuda() && l.scalar_type() == at::kFloat && l.is_contiguous() && l.dim() == 2 &&
+                        l.size(0) == q.size(0) && l.size(1) == q.size(1),
+                    "mtlattn: lse_out must be a contiguous fp32 [total_q, H] GPU tensor");
+        lse = l.data_ptr<float>();
+    }
+    if (q.size(0) == 0) return out;
+    mtlattn_problem p = make_problem(q, k, cu_q, cu_kv, max_seqlen_q, scale, causal, window);
+    at::Tensor bias_keep;
+    fill_bias(p, attn_bias, q, bias_keep);
+    const size_t ws_bytes = mtlattn_varlen_fwd_workspace_size(&p);
+    at::Tensor ws = workspace((int64_t)ws_bytes, q);
+    check_rc(mtlattn_varlen_fwd(&p, q.data_ptr(), row_stride(q), k.data_ptr(), row_stride(k), v.data_ptr(),
+                                row_stride(v), out.data_ptr(), lse, ws.data_ptr(), ws_bytes, current_stream(q)));
+    return out;
+}
+
+// _C.varlen_attention_bwd (src/ext.mm:502-594).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> varlen_attention_bwd(
+    const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& o, const at::Tensor& dout,
+    const at::Tensor& lse, const at::Tensor& cu_seqlens_q, const at::Tensor& cu_seqlens_kv, double scale,
+    bool causal, int64_t window, c10::optional<at::Tensor> attn_bias) {
+    check_qkv(q, k, v);
+    check_cu(cu_seqlens_q, cu_seqlens_kv, q);
+    TORCH_CHECK(o.sizes() == q.sizes() && dout.sizes() == q.sizes(), "mtlattn: o/dout must match q's shape");
+    TORCH_CHECK(o.scalar_type() == q.scalar_type() && dout.scalar_type() == q.scalar_type(),
+                "mtlattn: o/dout dtype mismatch");
+    check_qkv(o, dout, dout);
+    TORCH_CHECK(lse.is_cuda() && lse.scalar_type() == at::kFloat && lse.is_contiguous() && lse.dim() == 2 &&
+                    lse.size(0) == q.size(0) && lse.size(1) == q.size(1),
+                "mtlattn: lse must be a contiguous fp32 [total_q, H] GPU tensor");
+    const c10::OptionalDeviceGuard guard(q.device());
+    auto cu_q = cu_seqlens_q.contiguous(), cu_kv = cu_seqlens_kv.contiguous();
+    auto dQ = at::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+    auto dK = at::empty({k.size(0), k.size(1), k.size(2)}, k.options());
+    auto dV = at::empty({v.size(0), v.size(1), v.size(2)}, v.options());
+    mtlattn_problem p = make_problem(q, k, cu_q, cu_kv, q.size(0), scale, causal, window);
+    at::Tensor bias_keep;
+    fill_bias(p, attn_bias, q, bias_keep);
+    const size_t ws_bytes = mtlattn_varlen_bwd_workspace_size(&p);
+    at::Tensor ws = workspace((int64_t)ws_bytes, q);
+    check_rc(mtlattn_varlen_bwd(&p, q.data_ptr(), row_stride(q), k.data_ptr(), row_stride(k), v.data_ptr(),
+                                row_stride(v), o.data_ptr(), row_stride(o), dout.data_ptr(), row_stride(dout),
+                                lse.data_ptr<float>(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(), ws.data_ptr(),
+                                ws_bytes, current_stream(q)));
+    return {dQ, dK, dV};
+}
+
+// _C.attn_splitkv (src/ext.mm:716-773).
+at::Tensor attn_splitkv(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& cu_q_in,
+                        const at::Tensor& cu_kv_in, int64_t max_seqlen_q, double scale, bool causal,
+                        int64_t num_splits) {
+    check_qkv(q, k, v);
+    check_cu(cu_q_in, cu_kv_in, q);
+    const c10::OptionalDeviceGuard guard(q.device());
+    auto cu_q = cu_q_in.contiguous(), cu_kv = cu_kv_in.contiguous();
+    auto out = at::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+    mtlattn_problem p = make_problem(q, k, cu_q, cu_kv, max_seqlen_q, scale, causal, 0);
+    const size_t ws_bytes = mtlattn_attn_splitkv_workspace_size(&p, (int32_t)num_splits);
+    at::Tensor ws = workspace((int64_t)ws_bytes, q);
+    check_rc(mtlattn_attn_splitkv(&p, q.data_ptr(), row_stride(q), k.data_ptr(), row_stride(k), v.data_ptr(),
+                                  row_stride(v), out.data_ptr(), nullptr, (int32_t)num_splits, ws.data_ptr(), ws_bytes,
+                                  current_stream(q)));
+    return out;
+}
+
+// _C.mpp_bwd_dq (src/ext.mm:656-711): fp32 dQ.
+at::Tensor mpp_bwd_dq(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& dO,
+                      const at::Tensor& lse, const at::Tensor& delta, const at::Tensor& cu_q_in,
+                      const at::Tensor& cu_kv_in, int64_t max_seqlen_q, double scale, bool causal, int64_t window,
+                      c10::optional<at::Tensor> attn_bias) {
+    check_qkv(q, k, v);
+    check_cu(cu_q_in, cu_kv_in, q);
+    TORCH_CHECK(dO.sizes() == q.sizes() && dO.scalar_type() == q.scalar_type(), "mtlattn: dO must match q");
+    const c10::OptionalDeviceGuard guard(q.device());
+    auto cu_q = cu_q_in.contiguous(), cu_kv = cu_kv_in.contiguous();
+    auto dOc = dO.contiguous();
+    auto lsec = lse.to(at::kFloat).contiguous(), deltac = delta.to(at::kFloat).contiguous();
+    auto dQ = at::zeros({q.size(0), q.size(1), q.size(2)}, q.options().dtype(at::kFloat));
+    mtlattn_problem p = make_problem(q, k, cu_q, cu_kv, max_seqlen_q, scale, causal, window);
+    at::Tensor bias_keep;
+    fill_bias(p, attn_bias, q, bias_keep);
+    check_rc(mtlattn_bwd_dq(&p, q.data_ptr(), row_stride(q), k.data_ptr(), row_stride(k), v.data_ptr(),
+                            row_stride(v), dOc.data_ptr(), row_stride(dOc), lsec.data_ptr<float>(),
+                            deltac.data_ptr<float>(), dQ.data_ptr(), MTLATTN_DTYPE_F32, current_stream(q)));
+    return dQ;
+}
+
+// _C.mpp_bwd_dkv (src/ext.mm:597-653): fp32 (dK, dV).
+std::tuple<at::Tensor, at::Tensor> mpp_bwd_dkv(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                               const at::Tensor& dO, const at::Tensor& lse, const at::Tensor& delta,
+                                               const at::Tensor& cu_q_in, const at::Tensor& cu_kv_in,
+                                               int64_t max_seqlen_kv, double scale, bool causal, int64_t window,
+                                               c10::optional<at::Tensor> attn_bias) {
+    (void)max_seqlen_kv;   // grids are sized from tensor shapes; no host sync needed
+    check_qkv(q, k, v);
+    check_cu(cu_q_in, cu_kv_in, q);
+    TORCH_CHECK(dO.sizes() == q.sizes() && dO.scalar_type() == q.scalar_type(), "mtlattn: dO must match q");
+    const c10::OptionalDeviceGuard guard(q.device());
+    auto cu_q = cu_q_in.contiguous(), cu_kv = cu_kv_in.contiguous();
+    auto dOc = dO.contiguous();
+    auto lsec = lse.to(at::kFloat).contiguous(), deltac = delta.to(at::kFloat).contiguous();
+    auto dK = at::zeros({k.size(0), k.size(1), k.size(2)}, k.options().dtype(at::kFloat));
+    auto dV = at::zeros_like(dK);
+    mtlattn_problem p = make_problem(q, k, cu_q, cu_kv, q.size(0), scale, causal, window);
+    at::Tensor bias_keep;
+    fill_bias(p, attn_bias, q, bias_keep);
+    check_rc(mtlattn_bwd_dkv(&p, q.data_ptr(), row_stride(q), k.data_ptr(), row_stride(k), v.data_ptr(),
+                             row_stride(v), dOc.data_ptr(), row_stride(dOc), lsec.data_ptr<float>(),
+                             deltac.data_ptr<float>(), dK.data_ptr(), dV.data_ptr(), MTLATTN_DTYPE_F32,
+                             current_stream(q)));
+    return {dK, dV};
+}
+
+// The reference's "is the fast path usable here" probe (src/ext.mm:780-782):
+// the MFMA kernels are compiled into this build for gfx950.
+bool mpp_available() { return true; }
+
+int64_t gpu_core_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    return mtlattn_gpu_core_count(dev);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.def("mpp_available", &mpp_available, "True: the MFMA fast path is compiled in for gfx950");
+    m.def("gpu_core_count", &gpu_core_count, "Compute-unit count of the current device (0 if unknown)");
+    m.def("abi_version", [] { return mtlattn_abi_version(); }, "C ABI version of libmtlattn_hip.so");
+    m.def("attn_splitkv", &attn_splitkv, "split-KV decode with an explicit split count (test entry)", py::arg("q"),
+          py::arg("k"), py::arg("v"), py::arg("cu_q"), py::arg("cu_kv"), py::arg("max_seqlen_q"), py::arg("scale"),
+          py::arg("causal"), py::arg("num_splits"));
+    m.def("mpp_bwd_dkv", &mpp_bwd_dkv, "dK/dV backward kernel, fp32 outputs (test entry)", py::arg("q"), py::arg("k"),
+          py::arg("v"), py::arg("dO"), py::arg("lse"), py::arg("delta"), py::arg("cu_q"), py::arg("cu_kv"),
+          py::arg("max_seqlen_kv"), py::arg("scale"), py::arg("causal") = false, py::arg("window") = 0,
+          py::arg("attn_bias") = c10::nullopt);
+    m.def("mpp_bwd_dq", &mpp_bwd_dq, "dQ backward kernel, fp32 output (test entry)", py::arg("q"), py::arg("k"),
+          py::arg("v"), py::arg("dO"), py::arg("lse"), py::arg("delta"), py::arg("cu_q"), py::arg("cu_kv"),
+          py::arg("max_seqlen_q"), py::arg("scale"), py::arg("causal") = false, py::arg("window") = 0,
+          py::arg("attn_bias") = c10::nullopt);
+    m.def("varlen_attention", &varlen_attention, "Fused varlen attention forward (MI355X)", py::arg("q"),
+          py::arg("k"), py::arg("v"), py::arg("cu_seqlens_q"), py::arg("cu_seqlens_kv"), py::arg("max_seqlen_q"),
+          py::arg("scale"), py::arg("causal") = false, py::arg("window") = 0, py::arg("lse_out") = c10::nullopt,
+          py::arg("attn_bias") = c10::nullopt);
+    m.def("varlen_attention_bwd", &varlen_attention_bwd, "Varlen attention backward (dQ, dK, dV)", py::arg("q"),
+          py::arg("k"), py::arg("v"), py::arg("o"), py::arg("dout"), py::arg("lse"), py::arg("cu_seqlens_q"),
+          py::arg("cu_seqlens_kv"), py::arg("scale"), py::arg("causal") = false, py::arg("window") = 0,
+          py::arg("attn_bias") = c10::nullopt);
+}

@@ -1,0 +1,472 @@
+"""GPU parity: the HIP kernels (through mtlattn's public API and _C) against
+the CPU oracle on the same seeded inputs.
+
+Ports the reference's case matrix (tests/test_correctness.py:312-465) with its
+absolute tolerances, and adds LSE, split-KV, determinism and bookkeeping
+checks. Every case prints its name first so a failing run names its case.
+"""
+
+import math
+import os
+
+import pytest
+import torch
+
+import oracle
+from tests.helpers import REF_ATOL, cu_of, err_stats, randn
+
+pytestmark = pytest.mark.gpu
+
+torch.set_num_threads(min(16, os.cpu_count() or 1))
+
+
+@pytest.fixture(scope="module")
+def mt():
+    import mtlattn
+    return mtlattn
+
+
+def _banner(name):
+    print(f"\n[case] {name}", flush=True)
+
+
+def _inputs(q_lens, kv_lens, Hq, Hkv, D, dtype, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    q = randn((sum(q_lens), Hq, D), dtype, g)
+    k = randn((sum(kv_lens), Hkv, D), dtype, g)
+    v = randn((sum(kv_lens), Hkv, D), dtype, g)
+    return q, k, v
+
+
+def _make_bias(Mq, H, max_kv, broadcast, seed=7):
+    """Additive bias as tests/test_correctness.py:214-223 builds it: randn with
+    every 7th key pushed down by 30."""
+    g = torch.Generator().manual_seed(seed)
+    b = torch.randn((Mq, 1 if broadcast else H, max_kv), generator=g)
+    b[:, :, ::7] -= 30.0
+    return b
+
+
+def _fwd(mt, name, q_lens, kv_lens, Hq, Hkv, D, dtype, atol=None, causal=False, window=0,
+         bias=None, check_lse=True, seed=0):
+    _banner(name)
+    atol = REF_ATOL[dtype] if atol is None else atol
+    q, k, v = _inputs(q_lens, kv_lens, Hq, Hkv, D, dtype, seed)
+    cq, ck = cu_of(q_lens), cu_of(kv_lens)
+    scale = 1.0 / math.sqrt(D)
+    dev = "cuda"
+    lse = torch.empty(sum(q_lens), Hq, dtype=torch.float32, device=dev)
+    bdev = None if bias is None else bias.to(dev)
+    out = mt._C.varlen_attention(q.to(dev), k.to(dev), v.to(dev), cq.to(dev), ck.to(dev),
+                                 max(q_lens), scale, causal, window, lse, bdev)
+    out2 = mt.varlen_attention(q.to(dev), k.to(dev), v.to(dev), cq.to(dev), ck.to(dev),
+                               max(q_lens), scale, causal=causal, window=window, attn_bias=bdev)
+    torch.cuda.synchronize()
+    ref, ref_lse = oracle.varlen_forward(q, k, v, cq, ck, scale, causal, window, bias)
+    err = (out.cpu().float() - ref).abs().max().item()
+    st = err_stats(out, ref, dtype)
+    print(f"  max_err={err:.3e} atol={atol} rel={st['rel']:.3e} floor={st['floor']:.3e}", flush=True)
+    assert torch.isfinite(out.float()).all()
+    assert err < atol, f"{name}: max_err {err} >= {atol}"
+    assert torch.equal(out.cpu(), out2.cpu()), f"{name}: _C and public API disagree"
+    if check_lse:
+        fin = torch.isfinite(ref_lse)
+        lse_c = lse.cpu()
+        assert torch.equal(torch.isfinite(lse_c), fin), f"{name}: LSE -inf pattern differs"
+        lerr = (lse_c[fin] - ref_lse[fin]).abs().max().item() if fin.any() else 0.0
+        print(f"  lse_err={lerr:.3e}", flush=True)
+        assert lerr < (2e-5 if dtype == torch.float32 else 2e-3), f"{name}: lse err {lerr}"
+    return out
+
+
+def _bwd(mt, name, q_lens, kv_lens, Hq, Hkv, D, dtype, atol, causal=False, window=0, bias=None,
+         seed=0):
+    _banner(name)
+    q, k, v = _inputs(q_lens, kv_lens, Hq, Hkv, D, dtype, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    dout = randn((sum(q_lens), Hq, D), dtype, g)
+    cq, ck = cu_of(q_lens), cu_of(kv_lens)
+    dev = "cuda"
+    qm = q.to(dev).requires_grad_()
+    km = k.to(dev).requires_grad_()
+    vm = v.to(dev).requires_grad_()
+    out = mt.varlen_attention(qm, km, vm, cq.to(dev), ck.to(dev), max(q_lens), causal=causal,
+                              window=window, attn_bias=None if bias is None else bias.to(dev))
+    out.backward(dout.to(dev))
+    torch.cuda.synchronize()
+    ro, _, rq, rk, rv = oracle.varlen_forward_backward(q, k, v, dout, cq, ck, None, causal, window, bias)
+    errs = {}
+    for nm, a, b in (("out", out, ro), ("dQ", qm.grad, rq), ("dK", km.grad, rk), ("dV", vm.grad, rv)):
+        assert torch.isfinite(a.float()).all(), f"{name}: non-finite {nm}"
+        errs[nm] = (a.detach().cpu().float() - b).abs().max().item()
+    print("  " + " ".join(f"{k_}={v_:.3e}" for k_, v_ in errs.items()) + f" atol={atol}", flush=True)
+    worst = max(errs["dQ"], errs["dK"], errs["dV"])
+    assert worst < atol, f"{name}: grad err {errs}"
+    return qm.grad, km.grad, vm.grad
+
+
+# ---------------------------------------------------------------------------
+# forward: dtype sweep, ragged, cross, packed (tests/test_correctness.py:316-319)
+# ---------------------------------------------------------------------------
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_self_ragged(mt, dtype):
+    _fwd(mt, f"self[{dtype}] ragged", [5, 128, 33, 1000], [5, 128, 33, 1000], 12, 12, 128, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_cross(mt, dtype):
+    _fwd(mt, f"cross[{dtype}]", [64, 7, 300], [128, 1, 900], 12, 12, 128, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_packed(mt, dtype):
+    _banner(f"packed[{dtype}]")
+    g = torch.Generator().manual_seed(1)
+    lens = [37, 256, 1, 1023]
+    M, H, D = sum(lens), 12, 128
+    qkv = randn((M, 3, H, D), dtype, g)
+    q, k, v = qkv.unbind(1)
+    ref, _ = oracle.varlen_forward(q, k, v, cu_of(lens), cu_of(lens))
+    out = mt.flash_attn_varlen_qkvpacked_func(qkv.cuda(), cu_of(lens, "cuda"), max(lens))
+    e1 = (out.cpu().float() - ref).abs().max().item()
+    q_lens, kv_lens = [64, 512], [300, 100]
+    q2 = randn((sum(q_lens), H, D), dtype, g)
+    kv = randn((sum(kv_lens), 2, H, D), dtype, g)
+    k2, v2 = kv.unbind(1)
+    ref2, _ = oracle.varlen_forward(q2, k2, v2, cu_of(q_lens), cu_of(kv_lens))
+    out2 = mt.flash_attn_varlen_kvpacked_func(q2.cuda(), kv.cuda(), cu_of(q_lens, "cuda"),
+                                              cu_of(kv_lens, "cuda"), max(q_lens), max(kv_lens))
+    e2 = (out2.cpu().float() - ref2).abs().max().item()
+    print(f"  qkv_err={e1:.3e} kv_err={e2:.3e}", flush=True)
+    assert e1 < REF_ATOL[dtype] and e2 < REF_ATOL[dtype]
+
+
+# odd head dims, tiny windows, single long sequence (tests/test_correctness.py:321-328)
+def test_head_dims_small(mt):
+    _fwd(mt, "self D=64", [100, 200], [100, 200], 16, 16, 64, torch.float16)
+    _fwd(mt, "self D=80", [77, 13], [77, 13], 8, 8, 80, torch.float16)
+
+
+def test_5000_windows(mt):
+    g = torch.Generator().manual_seed(2)
+    wlens = torch.randint(1, 65, (5000,), generator=g).tolist()
+    _fwd(mt, "5000 windows", wlens, wlens, 12, 12, 128, torch.float16, check_lse=False)
+
+
+def test_single_16384(mt):
+    _banner("1x16384 (heads 0 and 11 checked)")
+    q, k, v = _inputs([16384], [16384], 12, 12, 128, torch.float16)
+    cu = cu_of([16384])
+    out = mt.varlen_attention(q.cuda(), k.cuda(), v.cuda(), cu.cuda(), cu.cuda(), 16384).cpu()
+    ref, _, _, _, _ = oracle.varlen_forward_backward_blocked(q, k, v, None, cu, cu, heads=[0, 11],
+                                                             backward=False, q_block=2048)
+    err = (out[:, [0, 11]].float() - ref[:, [0, 11]]).abs().max().item()
+    print(f"  max_err={err:.3e}", flush=True)
+    assert err < 5e-3
+
+
+# MFMA head dims 64/128 + generic 80/88/96 (tests/test_correctness.py:332-343)
+def test_mfma_d64(mt):
+    _fwd(mt, "D=64 full", [2048], [2048], 12, 12, 64, torch.float16)
+    _fwd(mt, "D=64 causal", [4096], [4096], 12, 12, 64, torch.float16, causal=True)
+    _fwd(mt, "D=64 bf16", [1500], [1500], 8, 8, 64, torch.bfloat16, causal=True)
+    _fwd(mt, "D=64 SWA", [2048], [2048], 12, 12, 64, torch.float16, causal=True, window=128)
+
+
+def test_generic_head_dims(mt):
+    _fwd(mt, "D=96 causal", [2048], [2048], 12, 12, 96, torch.float16, causal=True)
+    _fwd(mt, "D=96 bf16", [1500], [1500], 8, 8, 96, torch.bfloat16)
+    _fwd(mt, "D=80", [2048], [2048], 8, 8, 80, torch.float16)
+    _fwd(mt, "D=80 causal", [1500], [1500], 12, 12, 80, torch.float16, causal=True)
+    _fwd(mt, "D=88", [2048], [2048], 8, 8, 88, torch.float16)
+    _fwd(mt, "D=88 bf16 causal", [1500], [1500], 8, 8, 88, torch.bfloat16, causal=True)
+    _fwd(mt, "D=80 ragged causal", [200, 700], [200, 700], 8, 8, 80, torch.float16, causal=True)
+
+
+def test_large_head_dims(mt):
+    _fwd(mt, "D=160 full", [2048], [2048], 8, 8, 160, torch.float16)
+    _fwd(mt, "D=160 causal", [1500], [1500], 12, 12, 160, torch.float16, causal=True)
+    _fwd(mt, "D=256 full", [2048], [2048], 8, 8, 256, torch.float16)
+    _fwd(mt, "D=256 causal", [1024], [1024], 12, 12, 256, torch.float16, causal=True)
+    _fwd(mt, "D=256 bf16", [1500], [1500], 8, 8, 256, torch.bfloat16, atol=4e-2, causal=True)
+
+
+# decode / split-KV (tests/test_correctness.py:347-353)
+def test_decode_cases(mt):
+    _fwd(mt, "decode B1 kv8192", [1], [8192], 12, 12, 128, torch.float16, causal=True)
+    _fwd(mt, "decode B1 noncausal", [1], [8192], 8, 8, 128, torch.float16)
+    _fwd(mt, "decode B4 ragged", [1, 1, 1, 1], [8192, 4000, 6000, 2048], 8, 8, 128, torch.float16,
+         causal=True)
+    _fwd(mt, "decode B1 D64", [1], [4096], 8, 8, 64, torch.float16, causal=True)
+    _fwd(mt, "decode bf16", [1], [5000], 8, 8, 128, torch.bfloat16, causal=True)
+    _fwd(mt, "decode GQA B1", [1], [8192], 8, 2, 128, torch.float16, causal=True)
+    _fwd(mt, "decode few-q (spec)", [4], [8000], 8, 8, 128, torch.float16, causal=True)
+    _fwd(mt, "decode GQA 64/8 few-q", [3, 2], [9000, 4100], 64, 8, 128, torch.bfloat16, causal=True)
+
+
+# causal (tests/test_correctness.py:367-371)
+def test_causal_cases(mt):
+    _fwd(mt, "causal self D=128", [1024], [1024], 12, 12, 128, torch.float16, causal=True)
+    _fwd(mt, "causal self bf16", [777], [777], 8, 8, 128, torch.bfloat16, causal=True)
+    _fwd(mt, "causal ragged D=128", [33, 256, 1000], [33, 256, 1000], 12, 12, 128, torch.float16,
+         causal=True)
+    _fwd(mt, "causal cross (cached)", [64], [320], 8, 8, 128, torch.float16, causal=True)
+    _fwd(mt, "causal self D=64", [200, 50], [200, 50], 16, 16, 64, torch.float16, causal=True)
+    _fwd(mt, "causal q>kv (empty rows)", [300, 40], [100, 40], 8, 8, 128, torch.bfloat16, causal=True)
+
+
+# GQA / MQA (tests/test_correctness.py:375-379)
+def test_gqa_cases(mt):
+    _fwd(mt, "GQA 12->4 D=128", [512], [512], 12, 4, 128, torch.float16)
+    _fwd(mt, "MQA 8->1 D=128", [33, 300], [33, 300], 8, 1, 128, torch.float16)
+    _fwd(mt, "GQA 8->2 causal", [400], [400], 8, 2, 128, torch.float16, causal=True)
+    _fwd(mt, "MQA cross cached", [16], [512], 8, 1, 128, torch.float16, causal=True)
+    _fwd(mt, "GQA 8->2 D=64", [200, 50], [200, 50], 8, 2, 64, torch.float16)
+    _fwd(mt, "GQA 32->8 causal bf16", [700, 300], [700, 300], 32, 8, 128, torch.bfloat16, causal=True)
+
+
+# sliding window (tests/test_correctness.py:383-387)
+def test_window_cases(mt):
+    _fwd(mt, "SWA causal w=128 D=128", [1024], [1024], 12, 12, 128, torch.float16, causal=True,
+         window=128)
+    _fwd(mt, "SWA causal ragged", [600, 50, 333], [600, 50, 333], 8, 8, 128, torch.float16,
+         causal=True, window=64)
+    _fwd(mt, "SWA w>=len (no-op)", [200], [200], 8, 8, 128, torch.float16, causal=True, window=512)
+    _fwd(mt, "SWA non-causal band", [256], [256], 8, 8, 128, torch.float16, causal=False, window=48)
+    _fwd(mt, "SWA D=64", [300, 40], [300, 40], 16, 16, 64, torch.float16, causal=True, window=80)
+    _fwd(mt, "SWA GQA bf16", [900], [900], 32, 8, 128, torch.bfloat16, causal=True, window=300)
+
+
+# backward (tests/test_correctness.py:390-407)
+def test_bwd_fp32(mt):
+    f = torch.float32
+    _bwd(mt, "bwd full fp32", [256], [256], 8, 8, 128, f, 1e-4)
+    _bwd(mt, "bwd causal fp32", [256], [256], 8, 8, 128, f, 1e-4, causal=True)
+    _bwd(mt, "bwd GQA+causal", [256], [256], 8, 2, 128, f, 1e-4, causal=True)
+    _bwd(mt, "bwd window", [512], [512], 8, 8, 128, f, 1e-4, causal=True, window=64)
+    _bwd(mt, "bwd varlen GQA", [128, 300], [128, 300], 12, 4, 128, f, 1e-4, causal=True)
+
+
+def test_bwd_fp16(mt):
+    h = torch.float16
+    _bwd(mt, "bwd fp16 causal", [256], [256], 8, 8, 128, h, 5e-3, causal=True)
+    _bwd(mt, "bwd fp16 varlen", [128, 300, 64], [128, 300, 64], 8, 8, 128, h, 5e-3, causal=True)
+    _bwd(mt, "bwd fp16 varlen GQA", [200, 50, 333], [200, 50, 333], 12, 4, 128, h, 6e-3, causal=True)
+    _bwd(mt, "bwd fp16 window", [512], [512], 8, 8, 128, h, 5e-3, causal=True, window=64)
+    _bwd(mt, "bwd fp16 D=64", [200, 50], [200, 50], 8, 8, 64, h, 5e-3, causal=True)
+    _bwd(mt, "bwd fp16 D=96 GQA", [256], [256], 8, 2, 96, h, 6e-3, causal=True)
+    _bwd(mt, "bwd fp16 D=80", [256], [256], 8, 8, 80, h, 6e-3, causal=True)
+    _bwd(mt, "bwd fp16 D=88 GQA", [200, 56], [200, 56], 8, 2, 88, h, 6e-3, causal=True)
+    _bwd(mt, "bwd fp16 D=160", [512], [512], 8, 8, 160, h, 6e-3, causal=True)
+    _bwd(mt, "bwd fp16 D=256", [512], [512], 8, 8, 256, h, 6e-3, causal=True)
+
+
+def test_bwd_bf16(mt):
+    b = torch.bfloat16
+    _bwd(mt, "bwd bf16 varlen", [180, 90], [180, 90], 8, 8, 128, b, 4e-2, causal=True)
+    _bwd(mt, "bwd bf16 GQA 32/8 causal", [300, 200], [300, 200], 32, 8, 128, b, 4e-2, causal=True)
+    _bwd(mt, "bwd bf16 non-causal cross", [100, 33], [250, 70], 8, 4, 128, b, 4e-2)
+    _bwd(mt, "bwd bf16 window GQA", [700], [700], 16, 4, 128, b, 4e-2, causal=True, window=200)
+    _bwd(mt, "bwd bf16 D=64 MHA", [400, 1000], [400, 1000], 4, 4, 64, b, 4e-2)
+
+
+# additive bias (tests/test_correctness.py:412-427)
+def test_bias_fwd(mt):
+    h = torch.float16
+    _fwd(mt, "bias fwd perhead D128", [1536], [1536], 8, 8, 128, h, bias=_make_bias(1536, 8, 1536, False))
+    _fwd(mt, "bias fwd broadcast D128", [1536], [1536], 8, 8, 128, h, bias=_make_bias(1536, 8, 1536, True))
+    _fwd(mt, "bias fwd causal D128", [1536], [1536], 12, 12, 128, h, causal=True,
+         bias=_make_bias(1536, 12, 1536, False))
+    _fwd(mt, "bias fwd ragged varlen", [200, 50, 1300], [200, 50, 1300], 8, 8, 128, h,
+         bias=_make_bias(1550, 8, 1300, False))
+    _fwd(mt, "bias fwd cross", [64], [900], 8, 8, 128, h, bias=_make_bias(64, 8, 900, False))
+    _fwd(mt, "bias fwd SWA", [1536], [1536], 8, 8, 128, h, causal=True, window=128,
+         bias=_make_bias(1536, 8, 1536, False))
+    _fwd(mt, "bias fwd bf16", [1500], [1500], 8, 8, 128, torch.bfloat16, bias=_make_bias(1500, 8, 1500, True))
+    _fwd(mt, "bias fwd D64", [2048], [2048], 12, 12, 64, h, bias=_make_bias(2048, 12, 2048, False))
+    _fwd(mt, "bias fwd D96 causal", [2048], [2048], 8, 8, 96, h, causal=True,
+         bias=_make_bias(2048, 8, 2048, False))
+    _fwd(mt, "bias fwd D256", [1024], [1024], 8, 8, 256, h, atol=6e-3, bias=_make_bias(1024, 8, 1024, False))
+
+
+def test_bias_bwd(mt):
+    h = torch.float16
+    _bwd(mt, "bias bwd perhead D128", [1280], [1280], 8, 8, 128, h, 5e-3, bias=_make_bias(1280, 8, 1280, False))
+    _bwd(mt, "bias bwd broadcast D128", [1280], [1280], 8, 8, 128, h, 5e-3, bias=_make_bias(1280, 8, 1280, True))
+    _bwd(mt, "bias bwd causal D128", [1280], [1280], 12, 12, 128, h, 5e-3, causal=True,
+         bias=_make_bias(1280, 12, 1280, False))
+    _bwd(mt, "bias bwd GQA causal", [1024], [1024], 8, 2, 128, h, 6e-3, causal=True,
+         bias=_make_bias(1024, 8, 1024, False))
+    _bwd(mt, "bias bwd ragged", [128, 700], [128, 700], 8, 8, 128, h, 5e-3, bias=_make_bias(828, 8, 700, False))
+    _bwd(mt, "bias bwd D64 bf16", [1280], [1280], 8, 8, 64, torch.bfloat16, 4e-2,
+         bias=_make_bias(1280, 8, 1280, False))
+
+
+# SDPA adapter, padding-mask packing, mask -> bias (tests/test_correctness.py:437-448)
+def test_sdpa_adapter(mt):
+    for (B, Hq, Hkv, N, causal) in [(2, 8, 8, 1024, False), (1, 8, 2, 2048, False), (2, 12, 12, 512, True)]:
+        _banner(f"sdpa B{B} {Hq}/{Hkv} N{N} causal={causal}")
+        g = torch.Generator().manual_seed(0)
+        q = randn((B, Hq, N, 128), torch.float16, g)
+        k = randn((B, Hkv, N, 128), torch.float16, g)
+        v = randn((B, Hkv, N, 128), torch.float16, g)
+        gg = Hq // Hkv
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            q.float(), k.float().repeat_interleave(gg, 1), v.float().repeat_interleave(gg, 1),
+            is_causal=causal)
+        out = mt.sdpa(q.cuda(), k.cuda(), v.cuda(), is_causal=causal).cpu().float()
+        err = (out - ref).abs().max().item()
+        print(f"  max_err={err:.3e}", flush=True)
+        assert err < 5e-3
+
+
+def test_padding_mask(mt):
+    import torch.nn.functional as F
+    for (B, H, N, Ls, causal) in [(4, 8, 1024, [1024, 800, 500, 1024], False), (3, 12, 1024, [1024, 700, 400], True)]:
+        _banner(f"pad mask B{B} causal={causal}")
+        g = torch.Generator().manual_seed(0)
+        q = randn((B, H, N, 128), torch.float16, g)
+        k = randn((B, H, N, 128), torch.float16, g)
+        v = randn((B, H, N, 128), torch.float16, g)
+        pack = lambda x: torch.cat([x[b, :, :Ls[b], :].transpose(0, 1) for b in range(B)], 0)
+        ref, _ = oracle.varlen_forward(pack(q), pack(k), pack(v), cu_of(Ls), cu_of(Ls), causal=causal)
+        mask = torch.zeros(B, 1, 1, N, dtype=torch.bool)
+        for b, Lb in enumerate(Ls):
+            mask[b, 0, 0, :Lb] = True
+        mt.replace_sdpa(min_seqlen=1)
+        try:
+            out = F.scaled_dot_product_attention(q.cuda(), k.cuda(), v.cuda(), attn_mask=mask.cuda(),
+                                                 is_causal=causal).cpu().float()
+        finally:
+            mt.restore_sdpa()
+        outp = torch.cat([out[b, :, :Ls[b], :].transpose(0, 1) for b in range(B)], 0)
+        err = (outp - ref).abs().max().item()
+        pad_zero = all(out[b, :, Ls[b]:, :].abs().max().item() == 0 for b in range(B) if Ls[b] < N)
+        print(f"  max_err={err:.3e} padded_rows_zero={pad_zero}", flush=True)
+        assert err < 5e-3 and pad_zero
+
+
+def test_sdpa_mask(mt):
+    import torch.nn.functional as F
+    for (B, H, N, bool_mask, bh) in [(2, 8, 1024, False, False), (2, 8, 1024, False, True),
+                                     (2, 8, 1024, True, False), (1, 12, 2048, True, True)]:
+        _banner(f"sdpa mask B{B} bool={bool_mask} head_broadcast={bh}")
+        g = torch.Generator().manual_seed(0)
+        q = randn((B, H, N, 128), torch.float16, g)
+        k = randn((B, H, N, 128), torch.float16, g)
+        v = randn((B, H, N, 128), torch.float16, g)
+        hb = 1 if bh else H
+        if bool_mask:
+            m = torch.rand((B, hb, N, N), generator=g) > 0.3
+            m[..., 0] = True
+        else:
+            m = torch.randn((B, hb, N, N), generator=g)
+        out = mt.sdpa(q.cuda(), k.cuda(), v.cuda(), attn_mask=m.cuda()).cpu().float()
+        ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), attn_mask=m)
+        err = (out - ref).abs().max().item()
+        print(f"  max_err={err:.3e}", flush=True)
+        assert err < 5e-3
+
+
+def test_outlier_channels(mt):
+    """Outlier channels x300 (tests/test_correctness.py:449-465): finite output,
+    loose tolerance."""
+    _banner("outlier channels bf16")
+    g = torch.Generator().manual_seed(3)
+    q = randn((2048, 12, 128), torch.bfloat16, g)
+    q[:, :, 5] *= 300
+    k = randn((2048, 12, 128), torch.bfloat16, g)
+    k[:, :, 5] *= 300
+    v = randn((2048, 12, 128), torch.bfloat16, g)
+    cu = cu_of([1024, 1024])
+    out = mt.varlen_attention(q.cuda(), k.cuda(), v.cuda(), cu.cuda(), cu.cuda(), 1024).cpu()
+    ref, _ = oracle.varlen_forward(q, k, v, cu, cu)
+    err = (out.float() - ref).abs().max().item()
+    print(f"  max_err={err:.3e}", flush=True)
+    assert torch.isfinite(out.float()).all() and err < 1e-1
+
+
+# ---------------------------------------------------------------------------
+# bookkeeping invariants beyond the reference's suite
+# ---------------------------------------------------------------------------
+def test_split_kv_invariants(mt):
+    """Any split count gives the unsplit answer; split 1 is a plain forward."""
+    _banner("split-KV num_splits sweep")
+    q_lens, kv_lens = [1, 1, 1], [5000, 2100, 9001]
+    q, k, v = _inputs(q_lens, kv_lens, 16, 4, 128, torch.bfloat16)
+    cq, ck = cu_of(q_lens, "cuda"), cu_of(kv_lens, "cuda")
+    ref, _ = oracle.varlen_forward(q, k, v, cu_of(q_lens), cu_of(kv_lens), causal=True)
+    outs = []
+    for ns in (1, 2, 7, 32, 100):
+        o = mt._C.attn_splitkv(q.cuda(), k.cuda(), v.cuda(), cq, ck, 1, 1 / math.sqrt(128), True, ns).cpu()
+        err = (o.float() - ref).abs().max().item()
+        print(f"  ns={ns} max_err={err:.3e}", flush=True)
+        assert err < 3e-2
+        outs.append(o.float())
+    for o in outs[1:]:
+        assert (o - outs[0]).abs().max().item() < 2e-2
+
+
+def test_ragged_equals_per_sequence(mt):
+    """A ragged batch equals per-sequence calls, bitwise (varlen bookkeeping)."""
+    _banner("ragged == per-sequence (bitwise)")
+    lens = [1, 77, 300, 64, 1000]
+    q, k, v = _inputs(lens, lens, 8, 2, 128, torch.bfloat16, seed=5)
+    cu = cu_of(lens)
+    full = mt.varlen_attention(q.cuda(), k.cuda(), v.cuda(), cu.cuda(), cu.cuda(), max(lens), causal=True).cpu()
+    off = 0
+    for L in lens:
+        one = cu_of([L], "cuda")
+        o = mt.varlen_attention(q[off:off + L].cuda(), k[off:off + L].cuda(), v[off:off + L].cuda(), one, one, L,
+                                causal=True).cpu()
+        assert torch.equal(o, full[off:off + L]), f"len {L} differs"
+        off += L
+
+
+def test_determinism(mt):
+    """Forward and backward are bitwise run-to-run deterministic (no atomics)."""
+    _banner("determinism fwd+bwd")
+    lens = [513, 1024, 77]
+    q, k, v = _inputs(lens, lens, 16, 4, 128, torch.bfloat16, seed=9)
+    g = torch.Generator().manual_seed(10)
+    dout = randn((sum(lens), 16, 128), torch.bfloat16, g).cuda()
+    cu = cu_of(lens, "cuda")
+    res = []
+    for _ in range(2):
+        qm, km, vm = (t.cuda().requires_grad_() for t in (q, k, v))
+        o = mt.varlen_attention(qm, km, vm, cu, cu, max(lens), causal=True)
+        o.backward(dout)
+        res.append([o.detach().cpu(), qm.grad.cpu(), km.grad.cpu(), vm.grad.cpu()])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
+def test_mfma_matches_generic(mt):
+    """The MFMA kernels and the portable kernels agree (both vs the oracle too)."""
+    import subprocess
+    import sys
+    _banner("MFMA vs generic path (subprocess with MTLATTN_NO_MFMA=1)")
+    code = (
+        "import torch, mtlattn, math, sys\n"
+        "sys.path.insert(0, '.')\n"
+        "from tests.helpers import cu_of, randn\n"
+        "g = torch.Generator().manual_seed(4)\n"
+        "lens=[100,257,31]\n"
+        "q=randn((388,8,128),torch.float16,g).cuda(); k=randn((388,4,128),torch.float16,g).cuda(); v=randn((388,4,128),torch.float16,g).cuda()\n"
+        "cu=cu_of(lens,'cuda')\n"
+        "o=mtlattn.varlen_attention(q,k,v,cu,cu,257,causal=True,window=50)\n"
+        "torch.save(o.cpu(), sys.argv[1])\n")
+    outs = []
+    for env in ({}, {"MTLATTN_NO_MFMA": "1"}):
+        path = f"/tmp/mtl_path_{len(env)}.pt"
+        e = dict(os.environ, **env)
+        r = subprocess.run([sys.executable, "-c", code, path], env=e, timeout=300,
+                           cwd=os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+        assert r.returncode == 0
+        outs.append(torch.load(path, weights_only=True).float())
+    err = (outs[0] - outs[1]).abs().max().item()
+    print(f"  mfma_vs_generic={err:.3e}", flush=True)
+    assert err < 5e-3
