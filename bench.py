@@ -36,6 +36,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--only", choices=["c3", "c5"], default=None,
+                    help="run one workload and print nothing but its timing (for profilers)")
     return ap.parse_args()
 
 
@@ -181,6 +183,14 @@ def main():
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    if args.only == "c3":
+        c3, _ = bench_c3(args)
+        print(json.dumps({"c3_ms_per_step": c3["ms_per_step"], "tflops": c3["tflops"]}), flush=True)
+        return
+    if args.only == "c5":
+        dec = bench_c5(args)
+        print(json.dumps({"c5_ms": dec["ms"], "GBps": dec["GBps"]}), flush=True)
+        return
     c3, _ = bench_c3(args)
     dec = None if args.no_decode else bench_c5(args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.seed)

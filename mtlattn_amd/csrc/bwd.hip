@@ -500,8 +500,36 @@ __global__ __launch_bounds__(DkvCfg<D>::NW * 64, 1) void bwd_dkv_kernel(BwdKPara
 }
 
 // ---------------------------------------------------------------------------
-// delta = rowsum(dO * O), one thread per (row, head).
+// delta = rowsum(dO * O). 16-bit types with D % 8 == 0 and 16 | D * 4 lanes:
+// one wave per row, every lane streams 16-byte chunks of the contiguous
+// [H * D] row (coalesced), lanes sharing a head reduce with DPP shuffles.
+// Other cases: one thread per (row, head).
 // ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_preprocess_row_kernel(const uint16_t* __restrict__ o, int64_t o_rs,
+                                                                 const uint16_t* __restrict__ dout, int64_t do_rs,
+                                                                 float* __restrict__ delta, int64_t total_q, int hq,
+                                                                 int d) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= total_q) return;
+    const int lpg = d / 8;                         // lanes per head: 8 (D=64) or 16 (D=128)
+    const int chunks = hq * lpg;                   // 16-byte chunks per row
+    const uint16_t* op = o + row * o_rs;
+    const uint16_t* dp = dout + row * do_rs;
+    for (int c0 = 0; c0 < chunks; c0 += 64) {
+        const int c = c0 + lane;
+        float acc = 0.f;
+        if (c < chunks) {
+            const u32x4_t a = ld16(op + 8 * c), b = ld16(dp + 8 * c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc += lo16<T>(a[e]) * lo16<T>(b[e]) + hi16<T>(a[e]) * hi16<T>(b[e]);
+        }
+        for (int off = lpg >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+        if (c < chunks && (c % lpg) == 0) delta[row * hq + c / lpg] = acc;
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const typename T::raw* __restrict__ o, int64_t o_rs,
                                                              const typename T::raw* __restrict__ dout, int64_t do_rs,
@@ -513,18 +541,6 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const typename T::r
     const typename T::raw* op = o + row * o_rs + (int64_t)h * d;
     const typename T::raw* dp = dout + row * do_rs + (int64_t)h * d;
     float acc = 0.f;
-    if constexpr (sizeof(typename T::raw) == 2) {
-        if ((d & 7) == 0) {
-            for (int c = 0; c < d; c += 8) {
-                const u32x4_t a = ld16(op + c), b = ld16(dp + c);
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    acc += lo16<T>(a[e]) * lo16<T>(b[e]) + hi16<T>(a[e]) * hi16<T>(b[e]);
-            }
-            delta[i] = acc;
-            return;
-        }
-    }
     for (int c = 0; c < d; ++c) acc += T::to_float(op[c]) * T::to_float(dp[c]);
     delta[i] = acc;
 }
@@ -601,6 +617,19 @@ hipError_t launch_bwd_preprocess(int dtype, const Geometry& geo, const void* o, 
                                  const void* dout, int64_t do_rs, float* delta, hipStream_t st) {
     const int64_t n = geo.total_q * geo.hq;
     if (n == 0) return hipSuccess;
+    const bool rowwise = dtype != MTLATTN_DTYPE_F32 && (geo.d == 64 || geo.d == 128) &&
+                         ((uintptr_t)o & 15u) == 0 && ((uintptr_t)dout & 15u) == 0 && (o_rs % 8) == 0 &&
+                         (do_rs % 8) == 0;
+    if (rowwise) {
+        const dim3 grid((unsigned)((geo.total_q + 3) / 4));
+        if (dtype == MTLATTN_DTYPE_BF16)
+            hipLaunchKernelGGL(bwd_preprocess_row_kernel<BF16>, grid, dim3(256), 0, st, (const uint16_t*)o, o_rs,
+                               (const uint16_t*)dout, do_rs, delta, geo.total_q, geo.hq, geo.d);
+        else
+            hipLaunchKernelGGL(bwd_preprocess_row_kernel<F16>, grid, dim3(256), 0, st, (const uint16_t*)o, o_rs,
+                               (const uint16_t*)dout, do_rs, delta, geo.total_q, geo.hq, geo.d);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)((n + 255) / 256));
     if (dtype == MTLATTN_DTYPE_BF16)
         hipLaunchKernelGGL(bwd_preprocess_kernel<BF16>, grid, dim3(256), 0, st, (const uint16_t*)o, o_rs,

@@ -1,0 +1,136 @@
+"""Host-side logic of the Python API (mtlattn_amd/__init__.py) that needs no
+GPU: window mapping, bias preparation, SDPA mask -> bias layout, the
+replace_sdpa gate and fallbacks, and the binding's argument checks."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import mtlattn
+import mtlattn_amd as M
+
+
+def test_import_name_is_the_same_module():
+    assert mtlattn.varlen_attention is M.varlen_attention
+    assert mtlattn._C is M._C
+    assert set(mtlattn.__all__) == {"varlen_attention", "flash_attn_varlen_qkvpacked_func",
+                                    "flash_attn_varlen_kvpacked_func", "sdpa", "replace_sdpa", "restore_sdpa"}
+
+
+def test_binding_exports_reference_names():
+    for n in ("varlen_attention", "varlen_attention_bwd", "attn_splitkv", "mpp_bwd_dq", "mpp_bwd_dkv",
+              "mpp_available", "gpu_core_count"):
+        assert hasattr(M._C, n), n
+    assert M._C.mpp_available() is True
+
+
+def test_window_from_kwargs():
+    # flash_attn window_size=(left, right) -> window = left + 1 (mtlattn/__init__.py:95-101)
+    assert M._window_from_kwargs(0, {"window_size": (127, 0)}) == 128
+    assert M._window_from_kwargs(5, {"window_size": (-1, -1)}) == 5
+    assert M._window_from_kwargs(7, {}) == 7
+    assert M._window_from_kwargs(7, {"window_size": (None, 0)}) == 7
+
+
+def test_prep_bias():
+    assert M._prep_bias(None) is None
+    b = torch.randn(4, 1, 6, dtype=torch.float64)
+    out = M._prep_bias(b)
+    assert out.dtype == torch.float32 and out.stride(-1) == 1
+    nc = torch.randn(4, 6, 2).transpose(1, 2)          # last dim not contiguous
+    assert M._prep_bias(nc).is_contiguous()
+    with pytest.raises(NotImplementedError, match="differentiable attn_bias"):
+        M._prep_bias(torch.randn(2, 1, 3, requires_grad=True))
+
+
+def test_sdpa_mask_to_bias_bool_and_float():
+    B, H, Nq, Nkv = 2, 3, 4, 5
+    m = torch.rand(B, H, Nq, Nkv) > 0.5
+    b = M._sdpa_mask_to_bias(m, B, H, Nq, Nkv)
+    assert b.shape == (B * Nq, H, Nkv) and b.dtype == torch.float32
+    exp = torch.where(m, 0.0, float("-inf")).permute(0, 2, 1, 3).reshape(B * Nq, H, Nkv)
+    assert torch.equal(b, exp)
+    f = torch.randn(1, 1, Nq, Nkv)
+    bf = M._sdpa_mask_to_bias(f, B, H, Nq, Nkv)
+    assert bf.shape == (B * Nq, 1, Nkv)            # head broadcast kept at 1
+    assert torch.equal(bf[Nq:2 * Nq, 0], f[0, 0])
+    two_d = M._sdpa_mask_to_bias(f[0, 0], B, H, Nq, Nkv)
+    assert torch.equal(two_d, bf)
+
+
+@pytest.mark.parametrize("shape,msg", [
+    ((2, 3, 5), "2D or 4D"),
+    ((2, 3, 4, 6), "query/key dims"),
+    ((3, 1, 4, 5), "batch dim"),
+    ((2, 2, 4, 5), "head dim"),
+])
+def test_sdpa_mask_rejects(shape, msg):
+    with pytest.raises(NotImplementedError, match=msg):
+        M._sdpa_mask_to_bias(torch.zeros(shape), 2, 3, 4, 5)
+
+
+def test_basic_ok_gate_on_cpu():
+    q = torch.randn(1, 8, 2048, 64)
+    assert not M._basic_ok(q, q, q, 0.0, 1024)            # not a GPU tensor
+
+    class FakeDev:
+        type = "cuda"
+
+    class T:
+        def __init__(self, shape, dtype=torch.float16, rg=False):
+            self.shape, self.dtype, self.requires_grad, self.device = shape, dtype, rg, FakeDev()
+
+        def dim(self):
+            return len(self.shape)
+
+    ok = T((1, 8, 2048, 64))
+    assert M._basic_ok(ok, T((1, 2, 2048, 64)), ok, 0.0, 1024)
+    assert not M._basic_ok(ok, ok, ok, 0.1, 1024)                         # dropout
+    assert not M._basic_ok(T((1, 8, 2048, 64), torch.float64), ok, ok, 0.0, 1024)
+    assert not M._basic_ok(T((1, 8, 2048, 160)), ok, ok, 0.0, 1024)      # D > 128
+    assert not M._basic_ok(ok, T((1, 3, 2048, 64)), ok, 0.0, 1024)        # GQA divisibility
+    assert not M._basic_ok(T((1, 8, 512, 64)), ok, ok, 0.0, 1024)         # below min_seqlen
+    with torch.enable_grad():
+        assert not M._basic_ok(T((1, 8, 2048, 64), rg=True), ok, ok, 0.0, 1024)
+
+
+def test_replace_restore_idempotent_and_fallback():
+    orig = F.scaled_dot_product_attention
+    M.replace_sdpa()
+    patched = F.scaled_dot_product_attention
+    M.replace_sdpa()                                        # idempotent: still wraps the original
+    try:
+        assert F.scaled_dot_product_attention is not orig
+        q = torch.randn(1, 2, 8, 16)
+        # CPU tensors are never intercepted: identical to native SDPA
+        assert torch.equal(F.scaled_dot_product_attention(q, q, q, is_causal=True),
+                           orig(q, q, q, is_causal=True))
+    finally:
+        M.restore_sdpa()
+    assert F.scaled_dot_product_attention is orig
+    M.restore_sdpa()                                        # no-op
+    assert F.scaled_dot_product_attention is orig
+    del patched
+
+
+def test_padding_mask_detection_rejects_non_padding():
+    q = torch.randn(2, 2, 6, 8)
+    # query-dependent mask: not a key-padding mask
+    m = torch.ones(2, 1, 6, 6, dtype=torch.bool).tril()
+    assert M._try_padding_varlen(q, q, q, m, False, 0.3) is None
+    # non-prefix keep pattern
+    m2 = torch.ones(2, 1, 1, 6, dtype=torch.bool)
+    m2[:, :, :, 1] = False
+    assert M._try_padding_varlen(q, q, q, m2, False, 0.3) is None
+    # cross-attention shapes are not token padding
+    assert M._try_padding_varlen(q, torch.randn(2, 2, 7, 8), torch.randn(2, 2, 7, 8),
+                                 torch.ones(2, 1, 1, 7, dtype=torch.bool), False, 0.3) is None
+
+
+def test_binding_rejects_cpu_tensors():
+    q = torch.randn(4, 2, 8)
+    cu = torch.tensor([0, 4], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU"):
+        M._C.varlen_attention(q, q, q, cu, cu, 4, 0.3, False, 0, None, None)
+    with pytest.raises(RuntimeError, match="GPU"):
+        M.varlen_attention(q, q, q, cu, cu, 4)

@@ -1,0 +1,171 @@
+"""C ABI of libmtlattn_hip.so without a GPU: the library loads, exports every
+function include/mtlattn_capi.h declares, and its host-side validation,
+routing and workspace arithmetic behave as documented. No kernel is launched
+(every call here fails validation or only queries sizes)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mtlattn_capi.h")
+LIB = os.path.join(ROOT, "mtlattn_amd", "libmtlattn_hip.so")
+
+F32, F16, BF16 = 0, 1, 2
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE = 0, -1, -2, -3
+
+
+class Problem(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("num_seqs", ctypes.c_int32),
+        ("total_q", ctypes.c_int64), ("total_kv", ctypes.c_int64),
+        ("num_heads_q", ctypes.c_int32), ("num_heads_kv", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("max_seqlen_q", ctypes.c_int32),
+        ("scale", ctypes.c_float), ("causal", ctypes.c_int32), ("window", ctypes.c_int32),
+        ("cu_seqlens_q", ctypes.c_void_p), ("cu_seqlens_kv", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p), ("bias_q_stride", ctypes.c_int64),
+        ("bias_h_stride", ctypes.c_int64), ("bias_kv_cols", ctypes.c_int64),
+    ]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail("libmtlattn_hip.so is not built (run __graft_entry__.build())")
+    L = ctypes.CDLL(LIB)
+    L.mtlattn_last_error.restype = ctypes.c_char_p
+    for fn in ("mtlattn_varlen_fwd_workspace_size", "mtlattn_varlen_bwd_workspace_size"):
+        getattr(L, fn).restype = ctypes.c_size_t
+        getattr(L, fn).argtypes = [ctypes.POINTER(Problem)]
+    L.mtlattn_attn_splitkv_workspace_size.restype = ctypes.c_size_t
+    L.mtlattn_attn_splitkv_workspace_size.argtypes = [ctypes.POINTER(Problem), ctypes.c_int32]
+    L.mtlattn_decode_num_splits.restype = ctypes.c_int32
+    L.mtlattn_decode_num_splits.argtypes = [ctypes.POINTER(Problem)]
+    return L
+
+
+FAKE = ctypes.c_void_p(0x1000)   # never dereferenced: every call below stops in validation
+
+
+def problem(**kw):
+    p = Problem(dtype=BF16, num_seqs=2, total_q=64, total_kv=64, num_heads_q=8, num_heads_kv=2,
+                head_dim=128, max_seqlen_q=32, scale=0.088, causal=1, window=0,
+                cu_seqlens_q=FAKE, cu_seqlens_kv=FAKE, bias=None, bias_q_stride=0, bias_h_stride=0,
+                bias_kv_cols=0)
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(mtlattn_\w+)\s*\(", text)))
+
+
+def test_exports_every_declared_function(lib):
+    names = declared_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/mtlattn_capi.h but not exported"
+
+
+def test_abi_version(lib):
+    m = re.search(r"#define MTLATTN_ABI_VERSION (\d+)", open(HEADER).read())
+    assert lib.mtlattn_abi_version() == int(m.group(1))
+
+
+def _fwd(lib, p):
+    return lib.mtlattn_varlen_fwd(ctypes.byref(p), FAKE, ctypes.c_int64(3072), FAKE, ctypes.c_int64(768), FAKE,
+                                  ctypes.c_int64(768), FAKE, None, None, ctypes.c_size_t(0), None)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(num_heads_q=6, num_heads_kv=4), "multiple of kv heads"),
+    (dict(head_dim=300), "head_dim 300 unsupported"),
+    (dict(dtype=7), "unsupported dtype"),
+    (dict(num_seqs=0), "[B+1]"),
+    (dict(cu_seqlens_q=None), "cu_seqlens"),
+    (dict(total_q=-1), "negative token count"),
+    (dict(bias=FAKE, bias_q_stride=-5), "strides must be non-negative"),
+])
+def test_forward_validation(lib, kw, msg):
+    rc = _fwd(lib, problem(**kw))
+    assert rc == ERR_INVALID
+    assert msg in lib.mtlattn_last_error().decode()
+
+
+def test_null_problem(lib):
+    assert lib.mtlattn_varlen_fwd(None, FAKE, 0, FAKE, 0, FAKE, 0, FAKE, None, None, 0, None) == ERR_INVALID
+    assert b"null problem" in lib.mtlattn_last_error()
+
+
+def test_empty_query_is_a_no_op(lib):
+    assert _fwd(lib, problem(total_q=0)) == OK
+    assert lib.mtlattn_last_error() == b""
+
+
+def test_null_tensor_pointer(lib):
+    p = problem()
+    rc = lib.mtlattn_varlen_fwd(ctypes.byref(p), None, 0, FAKE, 0, FAKE, 0, FAKE, None, None, 0, None)
+    assert rc == ERR_INVALID and b"null" in lib.mtlattn_last_error()
+
+
+def test_workspace_sizes(lib):
+    p = problem(total_q=1000, num_heads_q=32, num_heads_kv=8)
+    assert lib.mtlattn_varlen_bwd_workspace_size(ctypes.byref(p)) == 1000 * 32 * 4
+    n = lib.mtlattn_attn_splitkv_workspace_size(ctypes.byref(p), 4)
+    o = 1000 * 32 * 128 * 4 * 4
+    assert n == ((o + 255) // 256) * 256 + 1000 * 32 * 4 * 4
+    assert lib.mtlattn_attn_splitkv_workspace_size(ctypes.byref(p), 0) == 0
+
+
+def test_backward_workspace_checked(lib):
+    p = problem()
+    rc = lib.mtlattn_varlen_bwd(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, 0, FAKE, 0, FAKE, FAKE, FAKE, FAKE,
+                                None, ctypes.c_size_t(16), None)
+    assert rc == ERR_WORKSPACE and b"workspace too small" in lib.mtlattn_last_error()
+
+
+def _c5_like(**kw):
+    base = dict(dtype=BF16, num_seqs=64, total_q=64, total_kv=64 * 36864, num_heads_q=64, num_heads_kv=8,
+                head_dim=128, max_seqlen_q=1, causal=1)
+    base.update(kw)
+    return problem(**base)
+
+
+def test_decode_routing(lib, monkeypatch):
+    """Reference gate (src/ext.mm:372-376): few queries, long KV, fp16/bf16,
+    D in {64,128}, no bias, no window."""
+    monkeypatch.delenv("MTLATTN_NO_SPLITKV", raising=False)
+    monkeypatch.delenv("MTLATTN_NO_MPP", raising=False)
+    monkeypatch.delenv("MTLATTN_NO_MFMA", raising=False)
+    ns = lib.mtlattn_decode_num_splits(ctypes.byref(_c5_like()))
+    assert 1 <= ns <= 256
+    assert lib.mtlattn_varlen_fwd_workspace_size(ctypes.byref(_c5_like())) == \
+        lib.mtlattn_attn_splitkv_workspace_size(ctypes.byref(_c5_like()), ns)
+    for kw in (dict(dtype=F32), dict(head_dim=96), dict(window=128), dict(max_seqlen_q=17),
+               dict(total_kv=64 * 2000), dict(bias=FAKE, bias_kv_cols=10)):
+        assert lib.mtlattn_decode_num_splits(ctypes.byref(_c5_like(**kw))) == 0, kw
+    monkeypatch.setenv("MTLATTN_NO_SPLITKV", "1")
+    assert lib.mtlattn_decode_num_splits(ctypes.byref(_c5_like())) == 0
+
+
+def test_splitkv_entry_validation(lib):
+    p = problem(dtype=F32, max_seqlen_q=1)
+    rc = lib.mtlattn_attn_splitkv(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, None, 2, None, 0, None)
+    assert rc == ERR_UNSUPPORTED and b"half/bf16" in lib.mtlattn_last_error()
+    p = problem(max_seqlen_q=1, window=4)
+    rc = lib.mtlattn_attn_splitkv(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, None, 2, None, 0, None)
+    assert rc == ERR_UNSUPPORTED
+    p = problem(max_seqlen_q=1)
+    rc = lib.mtlattn_attn_splitkv(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, None, 0, None, 0, None)
+    assert rc == ERR_INVALID
+
+
+def test_dq_dtype_checked(lib):
+    p = problem()
+    rc = lib.mtlattn_bwd_dq(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, 0, FAKE, FAKE, FAKE, F16, None)
+    assert rc == ERR_INVALID and b"dq dtype" in lib.mtlattn_last_error()

@@ -1,0 +1,160 @@
+"""GPU parity at the five BASELINE configs' real shapes (C1-C5).
+
+Criterion (north star): max|err| / RMS(ref) <= 1e-5 (fp32) or 2e-2 (fp16/bf16)
+per output and gradient tensor, evaluated element-wise as
+|err| <= tol * RMS(ref) + half an ulp of the output type at |ref| (see
+tests/helpers.py); the literal metric and the output type's own rounding
+floor are printed beside it. Large configs are run in full on the GPU and
+compared on sampled sequences / kv-head groups with the memory-bounded oracle
+(per-sequence, per-head independence makes the sample exact).
+"""
+
+import math
+import os
+
+import pytest
+import torch
+
+import oracle
+from tests.helpers import cu_of, err_stats
+
+pytestmark = pytest.mark.gpu
+
+torch.set_num_threads(min(16, os.cpu_count() or 1))
+
+
+def _report(name, pairs):
+    for nm, st in pairs:
+        print(f"  {name} {nm}: rel={st['rel']:.3e} floor={st['floor']:.3e} max_abs={st['max_abs']:.3e} "
+              f"rms={st['rms_ref']:.3e} ok={st['ok_elem']}", flush=True)
+    for nm, st in pairs:
+        assert st["ok_elem"], f"{name} {nm} out of tolerance: {st}"
+
+
+def _run_gpu(q, k, v, do, cq, ck, max_q, causal, window=0, bias=None):
+    import mtlattn
+    dev = "cuda"
+    qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+    out = mtlattn.varlen_attention(qd, kd, vd, cq.to(dev), ck.to(dev), max_q, causal=causal, window=window,
+                                   attn_bias=None if bias is None else bias)
+    out.backward(do.to(dev))
+    torch.cuda.synchronize()
+    return out.detach().cpu(), qd.grad.cpu(), kd.grad.cpu(), vd.grad.cpu()
+
+
+def _gen(shape, g, dtype):
+    return torch.randn(shape, generator=g).to(dtype)
+
+
+def test_c1_fp32_plumbing():
+    print("\n[case] C1 fp32 lens {17,64,129,250} H=4 D=64 non-causal fwd+bwd", flush=True)
+    lens = [17, 64, 129, 250]
+    g = torch.Generator().manual_seed(0)
+    q, k, v, do = (_gen((460, 4, 64), g, torch.float32) for _ in range(4))
+    cu = cu_of(lens)
+    o, dq, dk, dv = _run_gpu(q, k, v, do, cu, cu, max(lens), False)
+    ro, _, rq, rk, rv = oracle.varlen_forward_backward(q, k, v, do, cu, cu, 1 / 8, dtype=torch.float64)
+    _report("C1", [(n, err_stats(a, b, torch.float32)) for n, a, b in
+                   (("out", o, ro), ("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv))])
+
+
+def test_c2_ragged_noncausal_bf16():
+    print("\n[case] C2 bf16 32 seqs U[256,4096] H=16 D=64 non-causal fwd+bwd (3 seqs checked)", flush=True)
+    gl = torch.Generator().manual_seed(0)
+    lens = torch.randint(256, 4097, (32,), generator=gl).tolist()
+    g = torch.Generator().manual_seed(1)
+    T = sum(lens)
+    q, k, v, do = (_gen((T, 16, 64), g, torch.bfloat16) for _ in range(4))
+    cu = cu_of(lens)
+    o, dq, dk, dv = _run_gpu(q, k, v, do, cu, cu, max(lens), False)
+    seqs = [0, lens.index(max(lens)), 31]
+    ro, _, rq, rk, rv = oracle.varlen_forward_backward_blocked(q, k, v, do, cu, cu, 1 / 8, seqs=seqs)
+    rows = torch.cat([torch.arange(int(cu[s]), int(cu[s + 1])) for s in seqs])
+    _report("C2", [(n, err_stats(a[rows], b[rows], torch.bfloat16)) for n, a, b in
+                   (("out", o, ro), ("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv))])
+
+
+def test_c3_causal_gqa_bf16():
+    print("\n[case] C3 bf16 8x4096 Hq=32 Hkv=8 D=128 causal fwd+bwd (seqs 0,7 x kv heads 0,7 checked)",
+          flush=True)
+    B, L, Hq, Hkv, D = 8, 4096, 32, 8, 128
+    g = torch.Generator().manual_seed(0)
+    M = B * L
+    q = _gen((M, Hq, D), g, torch.bfloat16)
+    k = _gen((M, Hkv, D), g, torch.bfloat16)
+    v = _gen((M, Hkv, D), g, torch.bfloat16)
+    do = _gen((M, Hq, D), g, torch.bfloat16)
+    cu = cu_of([L] * B)
+    o, dq, dk, dv = _run_gpu(q, k, v, do, cu, cu, L, True)
+    seqs, heads = [0, 7], [0, 7]
+    ro, _, rq, rk, rv = oracle.varlen_forward_backward_blocked(q, k, v, do, cu, cu, 1 / math.sqrt(D), True,
+                                                               seqs=seqs, heads=heads)
+    rows = torch.cat([torch.arange(s * L, (s + 1) * L) for s in seqs])
+    qh = torch.tensor([h * 4 + j for h in heads for j in range(4)])
+    kh = torch.tensor(heads)
+    sel_q = lambda t: t[rows][:, qh]
+    sel_k = lambda t: t[rows][:, kh]
+    _report("C3", [("out", err_stats(sel_q(o), sel_q(ro), torch.bfloat16)),
+                   ("dq", err_stats(sel_q(dq), sel_q(rq), torch.bfloat16)),
+                   ("dk", err_stats(sel_k(dk), sel_k(rk), torch.bfloat16)),
+                   ("dv", err_stats(sel_k(dv), sel_k(rv), torch.bfloat16))])
+
+
+def test_c4_swa_bias_bf16():
+    print("\n[case] C4 bf16 4x16384 Hq=32 Hkv=8 D=128 causal W=4096 ALiBi-like bias fwd+bwd "
+          "(seq 0 x kv head 0 checked)", flush=True)
+    B, L, Hq, Hkv, D, W = 4, 16384, 32, 8, 128, 4096
+    g = torch.Generator().manual_seed(0)
+    M = B * L
+    q = _gen((M, Hq, D), g, torch.bfloat16)
+    k = _gen((M, Hkv, D), g, torch.bfloat16)
+    v = _gen((M, Hkv, D), g, torch.bfloat16)
+    do = _gen((M, Hq, D), g, torch.bfloat16)
+    cu = cu_of([L] * B)
+    i = torch.arange(L, device="cuda")[:, None]
+    j = torch.arange(L, device="cuda")[None, :]
+    blk = torch.where(j <= i, -(i - j).float() / 16.0, torch.zeros((), device="cuda"))   # seq-local
+    bias = blk.unsqueeze(1).repeat(B, 1, 1)            # [65536, 1, 16384] fp32, 4.29 GB
+    del i, j
+    o, dq, dk, dv = _run_gpu(q, k, v, do, cu, cu, L, True, W, bias)
+    del bias
+    bcpu = blk.unsqueeze(1).cpu()                       # rows of sequence 0 only
+    del blk
+    ro, _, rq, rk, rv = oracle.varlen_forward_backward_blocked(q, k, v, do, cu, cu, 1 / math.sqrt(D), True, W,
+                                                               bcpu, seqs=[0], heads=[0], q_block=1024)
+    qh, kh = torch.arange(4), torch.tensor([0])
+    rows = torch.arange(L)
+    sel_q = lambda t: t[rows][:, qh]
+    sel_k = lambda t: t[rows][:, kh]
+    _report("C4", [("out", err_stats(sel_q(o), sel_q(ro), torch.bfloat16)),
+                   ("dq", err_stats(sel_q(dq), sel_q(rq), torch.bfloat16)),
+                   ("dk", err_stats(sel_k(dk), sel_k(rk), torch.bfloat16)),
+                   ("dv", err_stats(sel_k(dv), sel_k(rv), torch.bfloat16))])
+
+
+def test_c5_split_kv_decode_bf16():
+    import mtlattn
+    print("\n[case] C5 bf16 decode 64 seqs q=1 kv U[8192,65536] Hq=64 Hkv=8 D=128 (8 seqs checked)",
+          flush=True)
+    B, Hq, Hkv, D = 64, 64, 8, 128
+    gl = torch.Generator().manual_seed(0)
+    kv_lens = torch.randint(8192, 65537, (B,), generator=gl).tolist()
+    g = torch.Generator().manual_seed(1)
+    Mk = sum(kv_lens)
+    q = _gen((B, Hq, D), g, torch.bfloat16)
+    k = _gen((Mk, Hkv, D), g, torch.bfloat16)
+    v = _gen((Mk, Hkv, D), g, torch.bfloat16)
+    cq, ck = cu_of([1] * B), cu_of(kv_lens)
+    assert mtlattn._C is not None
+    lse = torch.empty(B, Hq, dtype=torch.float32, device="cuda")
+    out = mtlattn._C.varlen_attention(q.cuda(), k.cuda(), v.cuda(), cq.cuda(), ck.cuda(), 1, 1 / math.sqrt(D),
+                                      True, 0, lse, None).cpu()
+    seqs = [0, 5, 17, 31, 40, 51, 62, 63]
+    ro, rl, _, _, _ = oracle.varlen_forward_backward_blocked(q, k, v, None, cq, ck, 1 / math.sqrt(D), True,
+                                                             seqs=seqs, backward=False, q_block=1)
+    rows = torch.tensor(seqs)
+    st = err_stats(out[rows], ro[rows], torch.bfloat16)
+    lerr = (lse.cpu()[rows] - rl[rows]).abs().max().item()
+    print(f"  C5 lse max_abs={lerr:.3e}", flush=True)
+    _report("C5", [("out", st)])
+    assert lerr < 1e-3
