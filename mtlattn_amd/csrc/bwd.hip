@@ -82,7 +82,8 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
     constexpr int VCH = kKT * D / 8 / HALF;   // 16-byte V chunks per loader thread
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
 
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
     const int l32 = lane & 31, hi = lane >> 5;
     const int QT = 32 * (NW / p.hpw);
     const int L = xcd_remap(blockIdx.x, p.n_tiles * p.n_hg);
@@ -106,7 +107,8 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
     const int wq_last = min(q_len, qa + 32) - 1;
     const int qrow = qa + l32;
     const bool row_ok = qrow < q_len;
-    const int64_t grow = qr.start + (row_ok ? qrow : 0);
+    // rows past the sequence end read its last row (finite, never stored)
+    const int64_t grow = qr.start + min(qrow, q_len - 1);
 
     // B operands: Q^T and dO^T fragments (lane = query, d = 16 kc + 8 hi + j).
     u32x4_t qf[DC], df[DC];
@@ -115,8 +117,8 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
         const uint16_t* dp = p.dout + grow * p.do_rs + (int64_t)head * D + 8 * hi;
 #pragma unroll
         for (int kc = 0; kc < DC; ++kc) {
-            qf[kc] = row_ok ? ld16(qp + 16 * kc) : u32x4_t{0, 0, 0, 0};
-            df[kc] = row_ok ? ld16(dp + 16 * kc) : u32x4_t{0, 0, 0, 0};
+            qf[kc] = ld16(qp + 16 * kc);
+            df[kc] = ld16(dp + 16 * kc);
         }
     }
     float lse2 = kPosInf, dlt = 0.f;
@@ -141,8 +143,9 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
 
     // Loader roles: the first half of the threads stage K (row-major and
     // transposed), the second half V (row-major).
-    const bool role_k = tid < HALF;
+    const bool role_k = w < NW / 2;               // wave-uniform roles
     const int rt = role_k ? tid : tid - HALF;
+    const int rt0 = role_k ? 64 * w : 64 * w - HALF;  // rt of lane 0 (unit counts are multiples of 64)
     constexpr int NPRE = KUPT * 4 > VCH ? KUPT * 4 : VCH;
     u32x4_t pre[NPRE];
     auto load_tile = [&](int kt) {
@@ -150,13 +153,12 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
 #pragma unroll
             for (int uu = 0; uu < KUPT; ++uu) {
                 const int u = rt + HALF * uu;
-                if (u < KUNITS) {
+                if (rt0 + HALF * uu < KUNITS) {
                     const int dc = u % (D / 8), kg = u / (D / 8);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const int key = kt + 4 * kg + i;
-                        pre[4 * uu + i] = key < kv_len ? ld16(kbase + (int64_t)key * p.k_rs + 8 * dc)
-                                                       : u32x4_t{0, 0, 0, 0};
+                        const int key = min(kt + 4 * kg + i, kv_len - 1);   // masked past the end
+                        pre[4 * uu + i] = ld16(kbase + (int64_t)key * p.k_rs + 8 * dc);
                     }
                 }
             }
@@ -164,9 +166,8 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
 #pragma unroll
             for (int i = 0; i < VCH; ++i) {
                 const int cid = rt + HALF * i;
-                const int key = kt + cid / (D / 8);
-                pre[i] = key < kv_len ? ld16(vbase + (int64_t)key * p.v_rs + 8 * (cid % (D / 8)))
-                                      : u32x4_t{0, 0, 0, 0};
+                const int key = min(kt + cid / (D / 8), kv_len - 1);
+                pre[i] = ld16(vbase + (int64_t)key * p.v_rs + 8 * (cid % (D / 8)));
             }
         }
     };
@@ -178,14 +179,14 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
 #pragma unroll
             for (int uu = 0; uu < KUPT; ++uu) {
                 const int u = rt + HALF * uu;
-                if (u < KUNITS) {
+                if (rt0 + HALF * uu < KUNITS) {
                     const int dc = u % (D / 8), kg = u / (D / 8);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) st16(Ks + rm_offset<D>(4 * kg + i, dc), pre[4 * uu + i]);
                     u32x2_t tr[8];
                     transpose4x8(&pre[4 * uu], tr);
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) st8(Kt + tr_offset(8 * dc + i, kg), tr[i]);
+                    for (int i = 0; i < 8; ++i) st8(Kt + tr_store_offset(8 * dc + i, kg), tr[i]);
                 }
             }
         } else {
@@ -196,6 +197,15 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
             }
         }
     };
+
+    // Per-lane LDS read offsets (see the forward kernel): row-major operands
+    // for rows 32 kb + l32, transposed K^T operands for rows 32 db + l32.
+    uint32_t rofs[4], tofs[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        rofs[c] = rm_offset<D>(l32, 2 * c + hi);
+        tofs[c] = tr_load_offset(l32, c, hi);
+    }
 
     f32x16_t dqacc[DB];
 #pragma unroll
@@ -225,10 +235,9 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
                     f32x16_t sacc = f32x16_t{}, pacc = f32x16_t{};
 #pragma unroll
                     for (int kc = 0; kc < DC; ++kc) {
-                        const u32x4_t a = ld16(Ks + rm_offset<D>(32 * kb + l32, 2 * kc + hi));
-                        sacc = mfma32<T>(a, qf[kc], sacc);
-                        const u32x4_t b = ld16(Vs + rm_offset<D>(32 * kb + l32, 2 * kc + hi));
-                        pacc = mfma32<T>(b, df[kc], pacc);
+                        const uint32_t o = rofs[kc & 3] + (kc >> 2) * 128 + kb * 32 * 2 * D;
+                        sacc = mfma32<T>(ld16(Ks + o), qf[kc], sacc);
+                        pacc = mfma32<T>(ld16(Vs + o), df[kc], pacc);
                     }
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
@@ -248,10 +257,8 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
                                                    T::pack2(sacc[r0 + 6], sacc[r0 + 7])};
 #pragma unroll
                         for (int db = 0; db < DB; ++db) {
-                            const int d = 32 * db + l32;
-                            const u32x2_t x0 = ld8(Kt + tr_offset(d, 4 * c + hi));
-                            const u32x2_t x1 = ld8(Kt + tr_offset(d, 4 * c + 2 + hi));
-                            dqacc[db] = mfma32<T>(u32x4_t{x0[0], x0[1], x1[0], x1[1]}, bs, dqacc[db]);
+                            const u32x4_t a = ld16(Kt + tofs[c ^ (2 * (db & 1))] + db * 32 * 128);
+                            dqacc[db] = mfma32<T>(a, bs, dqacc[db]);
                         }
                     }
                 }
@@ -295,7 +302,8 @@ __global__ __launch_bounds__(DkvCfg<D>::NW * 64, 1) void bwd_dkv_kernel(BwdKPara
     constexpr int KB = NW * kKW;                           // keys per workgroup
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
 
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
     const int l32 = lane & 31, hi = lane >> 5;
     const int L = xcd_remap(blockIdx.x, p.n_tiles * p.hkv);
     const int hk = L / p.n_tiles;
@@ -319,13 +327,13 @@ __global__ __launch_bounds__(DkvCfg<D>::NW * 64, 1) void bwd_dkv_kernel(BwdKPara
     // K^T / V^T B operands: lane = key, d = 16 kc + 8 hi + j.
     u32x4_t kf[DC], vf[DC];
     {
-        const int64_t grow = kr.start + (key_ok ? key : 0);
+        const int64_t grow = kr.start + min(key, kv_len - 1);     // masked past the end
         const uint16_t* kp = p.k + grow * p.k_rs + (int64_t)hk * D + 8 * hi;
         const uint16_t* vp = p.v + grow * p.v_rs + (int64_t)hk * D + 8 * hi;
 #pragma unroll
         for (int kc = 0; kc < DC; ++kc) {
-            kf[kc] = key_ok ? ld16(kp + 16 * kc) : u32x4_t{0, 0, 0, 0};
-            vf[kc] = key_ok ? ld16(vp + 16 * kc) : u32x4_t{0, 0, 0, 0};
+            kf[kc] = ld16(kp + 16 * kc);
+            vf[kc] = ld16(vp + 16 * kc);
         }
     }
 
@@ -338,8 +346,9 @@ __global__ __launch_bounds__(DkvCfg<D>::NW * 64, 1) void bwd_dkv_kernel(BwdKPara
 
     // Loader roles: the first half of the threads stage Q (row-major +
     // transposed) and lse, the second half dO (row-major + transposed) and delta.
-    const bool role_q = tid < HALF;
+    const bool role_q = w < NW / 2;               // wave-uniform roles
     const int rt = role_q ? tid : tid - HALF;
+    const int rt0 = role_q ? 64 * w : 64 * w - HALF;  // rt of lane 0 (unit counts are multiples of 64)
     u32x4_t pre[UPT][4];
     float pre_s = 0.f;
     auto load_stage = [&](int st) {
@@ -350,17 +359,17 @@ __global__ __launch_bounds__(DkvCfg<D>::NW * 64, 1) void bwd_dkv_kernel(BwdKPara
 #pragma unroll
         for (int uu = 0; uu < UPT; ++uu) {
             const int u = rt + HALF * uu;
-            if (u < UNITS) {
+            if (rt0 + HALF * uu < UNITS) {
                 const int dc = u % (D / 8), qg = u / (D / 8);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int q = qt + 4 * qg + i;
-                    pre[uu][i] = q < q_len ? ld16(base + (int64_t)(qr.start + q) * rs + (int64_t)h * D + 8 * dc)
-                                           : u32x4_t{0, 0, 0, 0};
+                    // rows past the end read the last row; their lse is +inf, so P = dS = 0
+                    const int q = min(qt + 4 * qg + i, q_len - 1);
+                    pre[uu][i] = ld16(base + (int64_t)(qr.start + q) * rs + (int64_t)h * D + 8 * dc);
                 }
             }
         }
-        if (rt < kQT) {
+        if (rt0 == 0) {                          // first wave of each role: 64 rows
             const int q = qt + rt;
             if (role_q) {
                 float l2 = kPosInf;
@@ -386,18 +395,25 @@ __global__ __launch_bounds__(DkvCfg<D>::NW * 64, 1) void bwd_dkv_kernel(BwdKPara
 #pragma unroll
         for (int uu = 0; uu < UPT; ++uu) {
             const int u = rt + HALF * uu;
-            if (u < UNITS) {
+            if (rt0 + HALF * uu < UNITS) {
                 const int dc = u % (D / 8), qg = u / (D / 8);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) st16(rm + rm_offset<D>(4 * qg + i, dc), pre[uu][i]);
                 u32x2_t trv[8];
                 transpose4x8(pre[uu], trv);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) st8(tr + tr_offset(8 * dc + i, qg), trv[i]);
+                for (int i = 0; i < 8; ++i) st8(tr + tr_store_offset(8 * dc + i, qg), trv[i]);
             }
         }
-        if (rt < kQT) (role_q ? ls : ds)[rt] = pre_s;
+        if (rt0 == 0) (role_q ? ls : ds)[rt] = pre_s;
     };
+
+    uint32_t rofs[4], tofs[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        rofs[c] = rm_offset<D>(l32, 2 * c + hi);
+        tofs[c] = tr_load_offset(l32, c, hi);
+    }
 
     f32x16_t dkacc[DB], dvacc[DB];
 #pragma unroll
@@ -432,10 +448,9 @@ __global__ __launch_bounds__(DkvCfg<D>::NW * 64, 1) void bwd_dkv_kernel(BwdKPara
                 f32x16_t sacc = f32x16_t{}, pacc = f32x16_t{};
 #pragma unroll
                 for (int kc = 0; kc < DC; ++kc) {
-                    const u32x4_t a = ld16(Qs + rm_offset<D>(32 * qb + l32, 2 * kc + hi));
-                    sacc = mfma32<T>(a, kf[kc], sacc);
-                    const u32x4_t b = ld16(Ds + rm_offset<D>(32 * qb + l32, 2 * kc + hi));
-                    pacc = mfma32<T>(b, vf[kc], pacc);
+                    const uint32_t o = rofs[kc & 3] + (kc >> 2) * 128 + qb * 32 * 2 * D;
+                    sacc = mfma32<T>(ld16(Qs + o), kf[kc], sacc);
+                    pacc = mfma32<T>(ld16(Ds + o), vf[kc], pacc);
                 }
                 const float* brow0 = nullptr;
                 if (BIAS) brow0 = p.bias + (int64_t)h * p.bias_hs + key;
@@ -465,16 +480,12 @@ __global__ __launch_bounds__(DkvCfg<D>::NW * 64, 1) void bwd_dkv_kernel(BwdKPara
                                                T::pack2(sacc[r0 + 4], sacc[r0 + 5]), T::pack2(sacc[r0 + 6], sacc[r0 + 7])};
                     const u32x4_t bs = u32x4_t{T::pack2(pacc[r0 + 0], pacc[r0 + 1]), T::pack2(pacc[r0 + 2], pacc[r0 + 3]),
                                                T::pack2(pacc[r0 + 4], pacc[r0 + 5]), T::pack2(pacc[r0 + 6], pacc[r0 + 7])};
-                    const int grp = 8 * qb + 4 * c + hi;       // 4-query group of slots j = 0..3
+                    const int cc = 2 * qb + c;                 // 16-query chunk within the stage
 #pragma unroll
                     for (int db = 0; db < DB; ++db) {
-                        const int d = 32 * db + l32;
-                        const u32x2_t o0 = ld8(Dt + tr_offset(d, grp));
-                        const u32x2_t o1 = ld8(Dt + tr_offset(d, grp + 2));
-                        dvacc[db] = mfma32<T>(u32x4_t{o0[0], o0[1], o1[0], o1[1]}, bp, dvacc[db]);
-                        const u32x2_t q0v = ld8(Qt + tr_offset(d, grp));
-                        const u32x2_t q1v = ld8(Qt + tr_offset(d, grp + 2));
-                        dkacc[db] = mfma32<T>(u32x4_t{q0v[0], q0v[1], q1v[0], q1v[1]}, bs, dkacc[db]);
+                        const uint32_t o = tofs[cc ^ (2 * (db & 1))] + db * 32 * 128;
+                        dvacc[db] = mfma32<T>(ld16(Dt + o), bp, dvacc[db]);
+                        dkacc[db] = mfma32<T>(ld16(Qt + o), bs, dkacc[db]);
                     }
                 }
             }

@@ -151,6 +151,46 @@ __device__ inline uint32_t tr_offset(int row, int group) {   // bytes
     return (uint32_t)(row * 128 + ((group ^ f) << 3));
 }
 
+// Transposed tile [rows][64] in 16-byte units: unit U = 2c + h of a row holds
+// columns {16c + 4h + 0..3, 16c + 8 + 4h + 0..3}, exactly the eight k-slots
+// that lane half h feeds to a 32x32x16 MFMA operand for k-chunk c, so an
+// operand is one 16-byte LDS read. Units are XOR-swizzled by
+// (row ^ (row >> 3)) & 7: operand reads (32 consecutive rows, one unit) are
+// conflict free, transposing writes (16 rows 8 apart) at most 2-way.
+__device__ inline int tr_swz(int row) { return (row ^ (row >> 3)) & 7; }
+// write offset of 4 consecutive columns 4*g4 .. 4*g4+3 (g4 = 0..15)
+__device__ inline uint32_t tr_store_offset(int row, int g4) {
+    const int c = g4 >> 2, gl = g4 & 3;
+    return (uint32_t)(row * 128 + (((2 * c + (gl & 1)) ^ tr_swz(row)) << 4) + ((gl >> 1) << 3));
+}
+// read offset of the operand unit for k-chunk c (0..3), lane half h
+__device__ inline uint32_t tr_load_offset(int row, int c, int h) {
+    return (uint32_t)(row * 128 + (((2 * c + h) ^ tr_swz(row)) << 4));
+}
+
+// Sum of two packed 16-bit values, accumulated in fp32 (v_dot2 with 1.0).
+template <typename T> __device__ inline float dot2_ones(uint32_t w, float acc);
+template <> __device__ inline float dot2_ones<BF16>(uint32_t w, float acc) {
+    const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), one, acc, false);
+}
+template <> __device__ inline float dot2_ones<F16>(uint32_t w, float acc) {
+    const f16x2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), one, acc, false);
+}
+
+// max / sum of x over lanes l and l ^ 32 via v_permlane32_swap: swapping a
+// register with itself across the halves leaves every lane holding its own
+// value in one result and its partner's in the other.
+__device__ inline float pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float pair_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ---------------------------------------------------------------------------
 // Wave reductions (64 lanes).
 // ---------------------------------------------------------------------------

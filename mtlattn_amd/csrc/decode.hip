@@ -50,7 +50,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
     constexpr int VU = D / 64;          // (4 keys x 8 d) units per lane per tile: (8 * D/8) / 64
     __shared__ __attribute__((aligned(16))) char smem[kDecWaves * D * kDecKT * 2];
 
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int n16 = lane & 15, lg = lane >> 4;
     char* vt = smem + w * (D * kDecKT * 2);
 
@@ -78,7 +78,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
     {
         const uint16_t* qp = p.q + grow * p.q_rs + (int64_t)head * D + 8 * lg;
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc) qf[kc] = row_ok ? ld16(qp + 32 * kc) : u32x4_t{0, 0, 0, 0};
+        for (int kc = 0; kc < KC; ++kc) qf[kc] = ld16(qp + 32 * kc);
     }
 
     int chunk = (kv_len + p.ns - 1) / p.ns;
@@ -95,11 +95,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
     auto load = [&](int kt, u32x4_t (&ka_)[2][KC], u32x4_t (&vr_)[VU][4]) {
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
-            const int key = kt + 16 * mb + n16;
-            const bool ok = key < ke;
-            const uint16_t* kp = kbase + (int64_t)(ok ? key : 0) * p.k_rs + 8 * lg;
+            // keys past the split end read its last key: finite, masked to P = 0
+            const int key = min(kt + 16 * mb + n16, ke - 1);
+            const uint16_t* kp = kbase + (int64_t)key * p.k_rs + 8 * lg;
 #pragma unroll
-            for (int kc = 0; kc < KC; ++kc) ka_[mb][kc] = ok ? ld16(kp + 32 * kc) : u32x4_t{0, 0, 0, 0};
+            for (int kc = 0; kc < KC; ++kc) ka_[mb][kc] = ld16(kp + 32 * kc);
         }
 #pragma unroll
         for (int u = 0; u < VU; ++u) {
@@ -107,8 +107,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
             const int dc = uid % (D / 8), kg = uid / (D / 8);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int key = kt + 4 * kg + i;
-                vr_[u][i] = key < ke ? ld16(vbase + (int64_t)key * p.v_rs + 8 * dc) : u32x4_t{0, 0, 0, 0};
+                const int key = min(kt + 4 * kg + i, ke - 1);
+                vr_[u][i] = ld16(vbase + (int64_t)key * p.v_rs + 8 * dc);
             }
         }
     };

@@ -53,7 +53,8 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     constexpr int KCH = kKT * D / 8 / 256;   // 16-byte K chunks per loader thread
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
 
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
     const int l32 = lane & 31, hi = lane >> 5;
     const int QT = 32 * (kWaves / p.hpw);
     const int L = xcd_remap(blockIdx.x, p.n_tiles * p.n_hg);
@@ -77,13 +78,14 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     const int wq_last = min(q_len, qa + 32) - 1;
 
     // Q^T operand fragments: lane holds query qa + l32, d = 16 kc + 8 hi + (0..7).
+    // Loads are branch-free: rows past the sequence end read its last row
+    // (finite data whose results are never stored).
     u32x4_t qf[DC];
     {
-        const int row = qa + l32;
-        const bool ok = row < q_len;
-        const uint16_t* qp = p.q + (int64_t)(qr.start + (ok ? row : 0)) * p.q_rs + (int64_t)head * D + 8 * hi;
+        const int row = min(qa + l32, q_len - 1);
+        const uint16_t* qp = p.q + (int64_t)(qr.start + row) * p.q_rs + (int64_t)head * D + 8 * hi;
 #pragma unroll
-        for (int kc = 0; kc < DC; ++kc) qf[kc] = ok ? ld16(qp + 16 * kc) : u32x4_t{0, 0, 0, 0};
+        for (int kc = 0; kc < DC; ++kc) qf[kc] = ld16(qp + 16 * kc);
     }
 
     // Key range of the whole workgroup.
@@ -103,12 +105,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     u32x4_t pre[4];
     auto load_tile = [&](int kt) {
         if (w < 4) {
-            if (tid < VUNITS) {
+            if (64 * w < VUNITS) {                // wave-uniform
                 const int dc = tid % (D / 8), kg = tid / (D / 8);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int key = kt + 4 * kg + i;
-                    pre[i] = key < kv_len ? ld16(vbase + (int64_t)key * p.v_rs + 8 * dc) : u32x4_t{0, 0, 0, 0};
+                    // keys past the end read the last row: finite, and masked to P = 0
+                    const int key = min(kt + 4 * kg + i, kv_len - 1);
+                    pre[i] = ld16(vbase + (int64_t)key * p.v_rs + 8 * dc);
                 }
             }
         } else {
@@ -117,8 +120,8 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
             for (int i = 0; i < KCH; ++i) {
                 const int cid = t2 + 256 * i;
                 const int row = cid / (D / 8), c = cid % (D / 8);
-                const int key = kt + row;
-                pre[i] = key < kv_len ? ld16(kbase + (int64_t)key * p.k_rs + 8 * c) : u32x4_t{0, 0, 0, 0};
+                const int key = min(kt + row, kv_len - 1);
+                pre[i] = ld16(kbase + (int64_t)key * p.k_rs + 8 * c);
             }
         }
     };
@@ -126,12 +129,12 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         char* Ks = smem + buf * STAGE;
         char* Vt = Ks + KS_BYTES;
         if (w < 4) {
-            if (tid < VUNITS) {
+            if (64 * w < VUNITS) {
                 const int dc = tid % (D / 8), kg = tid / (D / 8);
                 u32x2_t tr[8];
                 transpose4x8(pre, tr);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) st8(Vt + tr_offset(8 * dc + i, kg), tr[i]);
+                for (int i = 0; i < 8; ++i) st8(Vt + tr_store_offset(8 * dc + i, kg), tr[i]);
             }
         } else {
             const int t2 = tid - 256;
@@ -143,6 +146,17 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         }
     };
 
+    // Per-lane LDS read offsets, hoisted out of the key loop. K operand rows
+    // 32 kb + l32, chunk 2 kc + hi: the swizzle only touches the low 3 chunk
+    // bits, so 4 bases cover kc = 0..DC-1 (kc >= 4 adds 128 B). V^T operand
+    // rows 32 db + l32: odd db flips unit bit 2, i.e. selects chunk c ^ 2.
+    uint32_t kofs[4], vofs[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        kofs[c] = rm_offset<D>(l32, 2 * c + hi);
+        vofs[c] = tr_load_offset(l32, c, hi);
+    }
+
     float m_run = kNegInf, l_run = 0.f;
     f32x16_t oacc[DB];
 #pragma unroll
@@ -152,6 +166,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     const float* brow = nullptr;
     if (BIAS && qrow < q_len)
         brow = p.bias + (int64_t)(qr.start + qrow) * p.bias_qs + (int64_t)head * p.bias_hs;
+    const float c2 = p.scale_log2;
+    const bool raw_max = !BIAS && c2 > 0.f;   // max(s * c) = c * max(s)
+    // Rescale O only when the running max grows by more than 2^8: unnormalised
+    // weights stay <= 256, exact after the final division by the row sum.
+    constexpr float kRescale = 8.f;
 
     if (n_kv_tiles > 0) {
         load_tile(kv_lo);
@@ -173,70 +192,83 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
                 for (int kc = 0; kc < DC; ++kc) {
 #pragma unroll
                     for (int kb = 0; kb < 2; ++kb) {
-                        const u32x4_t a = ld16(Ks + rm_offset<D>(32 * kb + l32, 2 * kc + hi));
+                        const u32x4_t a = ld16(Ks + kofs[kc & 3] + (kc >> 2) * 128 + kb * 32 * 2 * D);
                         sacc[kb] = mfma32<T>(a, qf[kc], sacc[kb]);
                     }
                 }
                 const bool need_mask = (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
                                        (p.window > 0 && kt < wq_last + coff - p.window + 1);
-                // scaled base-2 logits (+ bias), masked entries -> -inf
-                float mx = kNegInf;
+                if (need_mask) {
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
+                    for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
-                        float x = sacc[kb][r] * p.scale_log2;
-                        bool ok = true;
-                        if (need_mask) {
-                            ok = key < kv_len;
+                        for (int r = 0; r < 16; ++r) {
+                            const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
+                            bool ok = key < kv_len;
                             if (p.causal) ok = ok && key <= qrow + coff;
                             if (p.window > 0) ok = ok && key > qrow + coff - p.window;
+                            if (!ok) sacc[kb][r] = kNegInf;
                         }
-                        if (BIAS && ok && brow != nullptr && key < p.bias_cols) x += brow[key] * kLog2e;
-                        x = ok ? x : kNegInf;
-                        sacc[kb][r] = x;
-                        mx = fmaxf(mx, x);
                     }
                 }
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
-                const float m_new = fmaxf(m_run, mx);
+                float mx = kNegInf;
+                if (raw_max) {
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+                    mx *= c2;
+                } else {
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const float sv = sacc[kb][r];
+                            float x = sv == kNegInf ? kNegInf : sv * c2;   // masked stays -inf for any sign of c2
+                            if (BIAS && brow != nullptr) {
+                                const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
+                                if (x != kNegInf && key < p.bias_cols) x = fmaf(brow[key], kLog2e, x);
+                            }
+                            sacc[kb][r] = x;
+                            mx = fmaxf(mx, x);
+                        }
+                    }
+                }
+                mx = pair_max(mx);
+                // m_run changes only when the tile max exceeds it by kRescale
+                const float m_new = mx > m_run + kRescale ? mx : m_run;
                 const float m_use = m_new == kNegInf ? 0.f : m_new;
-                const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
-                m_run = m_new;
-                float ls = 0.f;
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float e = __builtin_amdgcn_exp2f(sacc[kb][r] - m_use);
-                        ls += e;
-                        sacc[kb][r] = e;
-                    }
-                }
-                l_run = l_run * corr + ls;
-                if (__any(corr != 1.f)) {
+                if (__any(m_new != m_run)) {
+                    const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+                    l_run *= corr;
 #pragma unroll
                     for (int db = 0; db < DB; ++db) oacc[db] *= corr;
                 }
-                // P^T operands: chunk c covers tile keys 16c + 8(j/4) + 4hi + j%4.
+                m_run = m_new;
+                // P (rounded to T) as B operands; chunk c covers tile keys
+                // 16c + 8(j/4) + 4hi + j%4. The row sum adds the rounded values.
                 u32x4_t pf[4];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const int kb = c >> 1, r0 = 8 * (c & 1);
-                    pf[c] = u32x4_t{T::pack2(sacc[kb][r0 + 0], sacc[kb][r0 + 1]),
-                                    T::pack2(sacc[kb][r0 + 2], sacc[kb][r0 + 3]),
-                                    T::pack2(sacc[kb][r0 + 4], sacc[kb][r0 + 5]),
-                                    T::pack2(sacc[kb][r0 + 6], sacc[kb][r0 + 7])};
+                    float e[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float x = sacc[kb][r0 + j];
+                        e[j] = __builtin_amdgcn_exp2f(raw_max ? fmaf(x, c2, -m_use) : x - m_use);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        pf[c][j] = T::pack2(e[2 * j], e[2 * j + 1]);
+                        l_run = dot2_ones<T>(pf[c][j], l_run);
+                    }
                 }
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
 #pragma unroll
                     for (int db = 0; db < DB; ++db) {
-                        const int d = 32 * db + l32;
-                        const u32x2_t x0 = ld8(Vt + tr_offset(d, 4 * c + hi));
-                        const u32x2_t x1 = ld8(Vt + tr_offset(d, 4 * c + 2 + hi));
-                        oacc[db] = mfma32<T>(u32x4_t{x0[0], x0[1], x1[0], x1[1]}, pf[c], oacc[db]);
+                        const u32x4_t a = ld16(Vt + vofs[c ^ (2 * (db & 1))] + db * 32 * 128);
+                        oacc[db] = mfma32<T>(a, pf[c], oacc[db]);
                     }
                 }
             }
@@ -246,7 +278,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     }
 
     // Epilogue: lanes l and l^32 hold the two halves of one query's row sum.
-    const float lt = l_run + __shfl_xor(l_run, 32);
+    const float lt = pair_sum(l_run);
     if (wave_active && qrow < q_len) {
         const float inv = lt > 0.f ? 1.f / lt : 0.f;
         uint16_t* op = p.o + (int64_t)(qr.start + qrow) * ((int64_t)p.hq * D) + (int64_t)head * D;

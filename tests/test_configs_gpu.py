@@ -1,9 +1,9 @@
 """GPU parity at the five BASELINE configs' real shapes (C1-C5).
 
-Criterion (north star): max|err| / RMS(ref) <= 1e-5 (fp32) or 2e-2 (fp16/bf16)
-per output and gradient tensor, evaluated element-wise as
-|err| <= tol * RMS(ref) + half an ulp of the output type at |ref| (see
-tests/helpers.py); the literal metric and the output type's own rounding
+Criterion (north star): max|err| / RMS(ref) <= 1e-5 (fp32, asserted
+literally) or 2e-2 (fp16/bf16) per output and gradient tensor. For 16-bit
+outputs the literal bar is below the storage rounding floor, so the asserted
+form is the one documented in tests/helpers.py; the literal metric and the
 floor are printed beside it. Large configs are run in full on the GPU and
 compared on sampled sequences / kv-head groups with the memory-bounded oracle
 (per-sequence, per-head independence makes the sample exact).
@@ -25,8 +25,8 @@ torch.set_num_threads(min(16, os.cpu_count() or 1))
 
 def _report(name, pairs):
     for nm, st in pairs:
-        print(f"  {name} {nm}: rel={st['rel']:.3e} floor={st['floor']:.3e} max_abs={st['max_abs']:.3e} "
-              f"rms={st['rms_ref']:.3e} ok={st['ok_elem']}", flush=True)
+        print(f"  {name} {nm}: rel={st['rel']:.3e} floor={st['floor']:.3e} rms_rel={st['rms_rel']:.3e} "
+              f"max_abs={st['max_abs']:.3e} rms={st['rms_ref']:.3e} ok={st['ok_elem']}", flush=True)
     for nm, st in pairs:
         assert st["ok_elem"], f"{name} {nm} out of tolerance: {st}"
 
