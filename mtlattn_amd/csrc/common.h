@@ -192,6 +192,99 @@ __device__ inline float pair_sum(float x) {
 }
 
 // ---------------------------------------------------------------------------
+// Direct HBM -> LDS staging and transposed operand reads (gfx950).
+//
+// Row-major tile [rows][D] of 16-bit values with 16-byte chunks XOR-swizzled
+// by s(row) = ((row & 3) << 1) | ((row >> 2) & 1). Conflict free for
+//  * ds_read_b128 operand reads: 8 consecutive rows, one chunk;
+//  * ds_read_b64_tr_b16 transposed reads: 4 rows {4a..4a+3}, two adjacent
+//    chunks {2b, 2b+1} (see tr_operand);
+//  * global_load_lds_dwordx4 writes: 1 KB contiguous per instruction.
+// ---------------------------------------------------------------------------
+__device__ inline int row_swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+
+template <int D>
+__device__ inline uint32_t tile_offset(int row, int chunk) {   // bytes
+    return (uint32_t)(row * (2 * D) + ((chunk ^ row_swz(row)) << 4));
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
+// Stage rows [row0, row0 + ROWS) of a [*, D] 16-bit matrix (row stride rs
+// elements) into a swizzled LDS tile with global_load_lds_dwordx4: each
+// instruction moves 1 KB and lands lane l's 16 bytes at tile + 16 l, so the
+// lane loads the global chunk that the swizzle maps to that LDS position.
+// Rows >= row_end read row row_end - 1 (finite data the kernels mask out).
+// NW waves share the ROWS * D * 2 / 1024 instructions; w must be uniform.
+template <int D, int ROWS, int NW>
+__device__ inline void stage_tile(char* tile, const uint16_t* base, int64_t rs, int row0, int row_end, int w,
+                                  int lane) {
+    constexpr int PER = ROWS * D * 2 / 1024;
+    static_assert(ROWS * D * 2 % 1024 == 0, "tile must be a multiple of 1 KB");
+#pragma unroll
+    for (int i = w; i < PER; i += NW) {
+        const int byte = i * 1024 + lane * 16;
+        const int row = byte / (2 * D);
+        const int chunk = ((byte % (2 * D)) >> 4) ^ row_swz(row);
+        const int grow = min(row0 + row, row_end - 1);
+        __builtin_amdgcn_global_load_lds(base + (int64_t)grow * rs + chunk * 8, (lds_void_t*)(tile + i * 1024), 16,
+                                         0, 0);
+    }
+}
+
+// Wait until at most N of this wave's vector memory operations are pending
+// (s_waitcnt vmcnt(N), other counters untouched); N <= 15.
+template <int N>
+__device__ inline void wait_vmcnt() {
+    static_assert(N >= 0 && N < 16, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8));
+}
+
+// 32x32x16 MFMA operand whose M index runs along the D columns of a
+// row-major tile and whose K index runs along its rows: M = columns
+// dcol0 .. dcol0 + 31, K slots j of lane half h = rows
+// krow0 + 8 (j / 4) + 4 h + j % 4 (krow0 a multiple of 16, dcol0 of 32). Two
+// ds_read_b64_tr_b16: in each 16-lane group, lane 4e + q addresses row e of
+// the group's 4 rows at columns 4q .. 4q + 3, and lane i receives column i of
+// all 4 rows.
+//
+// The swizzle of rows krow0 + 4h + e depends only on (e, h), and dcol0 only
+// flips chunk bit 2 (dcol0 / 32 odd) or adds whole 128-byte groups, so every
+// address is one of two per-lane bases (tr_base(lane, parity)) plus
+// compile-time offsets: krow0 * 2D + (dcol0 / 64) * 128.
+template <int D>
+__device__ inline uint32_t tr_base(int lane, int parity) {
+    const int g = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
+    const int col = 32 * parity + 16 * (g & 1) + 4 * q;
+    const int row = 4 * (g >> 1) + e;
+    return tile_offset<D>(row, col >> 3) + (col & 7) * 2;
+}
+// Keeps a per-iteration address opaque to the optimiser, so constant offsets
+// fold into the LDS instructions' offset fields instead of being hoisted
+// out of the loop as extra live registers.
+__device__ inline const char* opaque(const char* p) {
+    uint32_t v = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+    asm volatile("" : "+v"(v));
+    return (const char*)(const __attribute__((address_space(3))) char*)(uintptr_t)v;
+}
+
+template <int D>
+__device__ inline u32x4_t tr_operand_at(const char* p) {
+    const v4i16_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p);
+    const v4i16_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p + 8 * 2 * D));
+    const u32x2_t a2 = __builtin_bit_cast(u32x2_t, a), b2 = __builtin_bit_cast(u32x2_t, b);
+    return u32x4_t{a2[0], a2[1], b2[0], b2[1]};
+}
+// operand for (krow0 = 16 c, dcol0 = 32 db) given the two lane bases
+// tb[p] = opaque(tile + tr_base(lane, p))
+template <int D>
+__device__ inline u32x4_t tr_operand(const char* const tb[2], int c, int db) {
+    return tr_operand_at<D>(tb[db & 1] + c * 16 * 2 * D + (db >> 1) * 128);
+}
+
+// ---------------------------------------------------------------------------
 // Wave reductions (64 lanes).
 // ---------------------------------------------------------------------------
 __device__ inline float wave_max(float v) {

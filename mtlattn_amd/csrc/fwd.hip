@@ -6,9 +6,10 @@
 //     query rows of one query head. The workgroup packs `hpw` = gcd(g, 8) query
 //     heads of one GQA group, so every K/V tile staged in LDS serves
 //     hpw * (8 / hpw) * 32 = 256 query-head rows.
-//   * Key tiles of 64 rows are double-buffered in LDS: K row-major (swizzled),
-//     V transposed to [D][64] in registers on the way in, so the P.V product
-//     reads V^T operands with contiguous 8-byte LDS loads.
+//   * Key tiles of 64 rows go straight from HBM into a 3-deep LDS ring with
+//     global_load_lds_dwordx4 (no register staging), K and V both row-major
+//     and swizzled; the P.V product reads V^T operands with
+//     ds_read_b64_tr_b16 transposed loads.
 //   * Per wave and key tile:  S^T = K Q^T  (v_mfma_f32_32x32x16, 2 x D/16
 //     instructions), online softmax in base 2 on the C registers (each lane
 //     holds one query column, so max/sum need one cross-half exchange), then
@@ -43,15 +44,19 @@ struct FwdKParams {
     int causal, window;
 };
 
-template <typename T, int D, bool BIAS>
+// GENERAL = explicit per-element logit scaling, with the optional bias; the
+// fast variant (no bias, scale > 0) reduces raw scores and folds the scale
+// into one FMA per element.
+template <typename T, int D, bool GENERAL>
 __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
+    constexpr bool BIAS = GENERAL;
     constexpr int DC = D / 16;               // MFMA k-chunks over D
     constexpr int DB = D / 32;               // 32-row output blocks over D
-    constexpr int KS_BYTES = kKT * D * 2;
-    constexpr int STAGE = 2 * KS_BYTES;      // K tile + V^T tile
-    constexpr int VUNITS = 2 * D;            // (4 keys x 8 d) units per V tile
-    constexpr int KCH = kKT * D / 8 / 256;   // 16-byte K chunks per loader thread
-    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+    constexpr int TILE = kKT * D * 2;        // bytes of one K or V tile
+    constexpr int STAGE = 2 * TILE;          // K tile + V tile, both row-major
+    constexpr int NBUF = 3;                  // ring of staged key tiles
+    constexpr int LOADS = STAGE / 1024 / kWaves;   // direct loads per wave per tile
+    __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
@@ -78,8 +83,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     const int wq_last = min(q_len, qa + 32) - 1;
 
     // Q^T operand fragments: lane holds query qa + l32, d = 16 kc + 8 hi + (0..7).
-    // Loads are branch-free: rows past the sequence end read its last row
-    // (finite data whose results are never stored).
+    // Rows past the sequence end read its last row (finite, never stored).
     u32x4_t qf[DC];
     {
         const int row = min(qa + l32, q_len - 1);
@@ -100,62 +104,20 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
 
     const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * D;
     const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * D;
-
-    // Loader roles: waves 0-3 stage V (transposed), waves 4-7 stage K.
-    u32x4_t pre[4];
-    auto load_tile = [&](int kt) {
-        if (w < 4) {
-            if (64 * w < VUNITS) {                // wave-uniform
-                const int dc = tid % (D / 8), kg = tid / (D / 8);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    // keys past the end read the last row: finite, and masked to P = 0
-                    const int key = min(kt + 4 * kg + i, kv_len - 1);
-                    pre[i] = ld16(vbase + (int64_t)key * p.v_rs + 8 * dc);
-                }
-            }
-        } else {
-            const int t2 = tid - 256;
-#pragma unroll
-            for (int i = 0; i < KCH; ++i) {
-                const int cid = t2 + 256 * i;
-                const int row = cid / (D / 8), c = cid % (D / 8);
-                const int key = min(kt + row, kv_len - 1);
-                pre[i] = ld16(kbase + (int64_t)key * p.k_rs + 8 * c);
-            }
-        }
-    };
-    auto store_tile = [&](int buf) {
-        char* Ks = smem + buf * STAGE;
-        char* Vt = Ks + KS_BYTES;
-        if (w < 4) {
-            if (64 * w < VUNITS) {
-                const int dc = tid % (D / 8), kg = tid / (D / 8);
-                u32x2_t tr[8];
-                transpose4x8(pre, tr);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) st8(Vt + tr_store_offset(8 * dc + i, kg), tr[i]);
-            }
-        } else {
-            const int t2 = tid - 256;
-#pragma unroll
-            for (int i = 0; i < KCH; ++i) {
-                const int cid = t2 + 256 * i;
-                st16(Ks + rm_offset<D>(cid / (D / 8), cid % (D / 8)), pre[i]);
-            }
-        }
+    // All 8 waves stage each tile straight from HBM into LDS (K then V).
+    auto stage = [&](int it) {
+        char* buf = smem + (it % NBUF) * STAGE;
+        const int kt = kv_lo + it * kKT;
+        stage_tile<D, kKT, kWaves>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
+        stage_tile<D, kKT, kWaves>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
     };
 
-    // Per-lane LDS read offsets, hoisted out of the key loop. K operand rows
-    // 32 kb + l32, chunk 2 kc + hi: the swizzle only touches the low 3 chunk
-    // bits, so 4 bases cover kc = 0..DC-1 (kc >= 4 adds 128 B). V^T operand
-    // rows 32 db + l32: odd db flips unit bit 2, i.e. selects chunk c ^ 2.
-    uint32_t kofs[4], vofs[4];
+    // K operand rows 32 kb + l32, chunk 2 kc + hi (hoisted per-lane offsets):
+    // the swizzle touches the low 3 chunk bits only, so kc >= 4 adds 128 B.
+    uint32_t kofs[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        kofs[c] = rm_offset<D>(l32, 2 * c + hi);
-        vofs[c] = tr_load_offset(l32, c, hi);
-    }
+    for (int c = 0; c < 4; ++c) kofs[c] = tile_offset<D>(l32, 2 * c + hi);
+    const uint32_t trb[2] = {tr_base<D>(lane, 0), tr_base<D>(lane, 1)};
 
     float m_run = kNegInf, l_run = 0.f;
     f32x16_t oacc[DB];
@@ -164,116 +126,115 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
 
     const int qrow = qa + l32;
     const float* brow = nullptr;
-    if (BIAS && qrow < q_len)
+    if (BIAS && p.bias != nullptr && qrow < q_len)
         brow = p.bias + (int64_t)(qr.start + qrow) * p.bias_qs + (int64_t)head * p.bias_hs;
     const float c2 = p.scale_log2;
-    const bool raw_max = !BIAS && c2 > 0.f;   // max(s * c) = c * max(s)
+    constexpr bool raw_max = !GENERAL;   // max(s * c) = c * max(s) needs c > 0 (host-checked)
     // Rescale O only when the running max grows by more than 2^8: unnormalised
     // weights stay <= 256, exact after the final division by the row sum.
     constexpr float kRescale = 8.f;
 
-    if (n_kv_tiles > 0) {
-        load_tile(kv_lo);
-        store_tile(0);
+    if (n_kv_tiles > 0) stage(0);
+    if (n_kv_tiles > 1) stage(1);
+    for (int it = 0; it < n_kv_tiles; ++it) {
+        // tile `it` landed (the next one may still be in flight), then publish
+        if (it + 1 < n_kv_tiles) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
         __syncthreads();
-        for (int it = 0; it < n_kv_tiles; ++it) {
-            const int kt = kv_lo + it * kKT;
-            const bool has_next = it + 1 < n_kv_tiles;
-            if (has_next) load_tile(kt + kKT);
+        // the buffer of tile it + 2 was last read in iteration it - 1
+        if (it + 2 < n_kv_tiles) stage(it + 2);
+        const int kt = kv_lo + it * kKT;
 
-            bool skip = !wave_active;
-            if (p.causal && kt > wq_last + coff) skip = true;
-            if (p.window > 0 && kt + kKT - 1 < qa + coff - p.window + 1) skip = true;
-            if (!skip) {
-                const char* Ks = smem + (it & 1) * STAGE;
-                const char* Vt = Ks + KS_BYTES;
-                f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
+        bool skip = !wave_active;
+        if (p.causal && kt > wq_last + coff) skip = true;
+        if (p.window > 0 && kt + kKT - 1 < qa + coff - p.window + 1) skip = true;
+        if (skip) continue;
+        const char* Ks = smem + (it % NBUF) * STAGE;
+        const char* const vtb[2] = {opaque(Ks + TILE + trb[0]), opaque(Ks + TILE + trb[1])};
+        f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
 #pragma unroll
-                for (int kc = 0; kc < DC; ++kc) {
+        for (int kc = 0; kc < DC; ++kc) {
 #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb) {
-                        const u32x4_t a = ld16(Ks + kofs[kc & 3] + (kc >> 2) * 128 + kb * 32 * 2 * D);
-                        sacc[kb] = mfma32<T>(a, qf[kc], sacc[kb]);
-                    }
-                }
-                const bool need_mask = (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
-                                       (p.window > 0 && kt < wq_last + coff - p.window + 1);
-                if (need_mask) {
+            for (int kb = 0; kb < 2; ++kb) {
+                const u32x4_t a = ld16(Ks + kofs[kc & 3] + (kc >> 2) * 128 + kb * 32 * 2 * D);
+                sacc[kb] = mfma32<T>(a, qf[kc], sacc[kb]);
+            }
+        }
+        // keep the V^T reads of the P.V phase from being hoisted above the
+        // softmax (they would pin 64 registers across it)
+        __builtin_amdgcn_sched_barrier(0);
+        const bool need_mask = (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
+                               (p.window > 0 && kt < wq_last + coff - p.window + 1);
+        if (need_mask) {
 #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
-                            bool ok = key < kv_len;
-                            if (p.causal) ok = ok && key <= qrow + coff;
-                            if (p.window > 0) ok = ok && key > qrow + coff - p.window;
-                            if (!ok) sacc[kb][r] = kNegInf;
-                        }
-                    }
-                }
-                float mx = kNegInf;
-                if (raw_max) {
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
-                    mx *= c2;
-                } else {
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const float sv = sacc[kb][r];
-                            float x = sv == kNegInf ? kNegInf : sv * c2;   // masked stays -inf for any sign of c2
-                            if (BIAS && brow != nullptr) {
-                                const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
-                                if (x != kNegInf && key < p.bias_cols) x = fmaf(brow[key], kLog2e, x);
-                            }
-                            sacc[kb][r] = x;
-                            mx = fmaxf(mx, x);
-                        }
-                    }
-                }
-                mx = pair_max(mx);
-                // m_run changes only when the tile max exceeds it by kRescale
-                const float m_new = mx > m_run + kRescale ? mx : m_run;
-                const float m_use = m_new == kNegInf ? 0.f : m_new;
-                if (__any(m_new != m_run)) {
-                    const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
-                    l_run *= corr;
-#pragma unroll
-                    for (int db = 0; db < DB; ++db) oacc[db] *= corr;
-                }
-                m_run = m_new;
-                // P (rounded to T) as B operands; chunk c covers tile keys
-                // 16c + 8(j/4) + 4hi + j%4. The row sum adds the rounded values.
-                u32x4_t pf[4];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int kb = c >> 1, r0 = 8 * (c & 1);
-                    float e[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const float x = sacc[kb][r0 + j];
-                        e[j] = __builtin_amdgcn_exp2f(raw_max ? fmaf(x, c2, -m_use) : x - m_use);
-                    }
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        pf[c][j] = T::pack2(e[2 * j], e[2 * j + 1]);
-                        l_run = dot2_ones<T>(pf[c][j], l_run);
-                    }
-                }
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-#pragma unroll
-                    for (int db = 0; db < DB; ++db) {
-                        const u32x4_t a = ld16(Vt + vofs[c ^ (2 * (db & 1))] + db * 32 * 128);
-                        oacc[db] = mfma32<T>(a, pf[c], oacc[db]);
-                    }
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
+                    bool ok = key < kv_len;
+                    if (p.causal) ok = ok && key <= qrow + coff;
+                    if (p.window > 0) ok = ok && key > qrow + coff - p.window;
+                    if (!ok) sacc[kb][r] = kNegInf;
                 }
             }
-            if (has_next) store_tile((it + 1) & 1);
-            __syncthreads();
+        }
+        float mx = kNegInf;
+        if (raw_max) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+            mx *= c2;
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float sv = sacc[kb][r];
+                    float x = sv == kNegInf ? kNegInf : sv * c2;   // masked stays -inf for any sign of c2
+                    if (BIAS && brow != nullptr) {
+                        const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
+                        if (x != kNegInf && key < p.bias_cols) x = fmaf(brow[key], kLog2e, x);
+                    }
+                    sacc[kb][r] = x;
+                    mx = fmaxf(mx, x);
+                }
+            }
+        }
+        mx = pair_max(mx);
+        // m_run changes only when the tile max exceeds it by kRescale
+        const float m_new = mx > m_run + kRescale ? mx : m_run;
+        const float m_use = m_new == kNegInf ? 0.f : m_new;
+        if (__any(m_new != m_run)) {
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+            l_run *= corr;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) oacc[db] *= corr;
+        }
+        m_run = m_new;
+        // P (rounded to T) as B operands; chunk c covers tile keys
+        // 16c + 8(j/4) + 4hi + j%4. The row sum adds the rounded values.
+        u32x4_t pf[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int kb = c >> 1, r0 = 8 * (c & 1);
+            float e[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = sacc[kb][r0 + j];
+                e[j] = __builtin_amdgcn_exp2f(raw_max ? fmaf(x, c2, -m_use) : x - m_use);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                pf[c][j] = T::pack2(e[2 * j], e[2 * j + 1]);
+                l_run = dot2_ones<T>(pf[c][j], l_run);
+            }
+        }
+        // O^T += V^T P^T; V^T operands are transposed reads of the row-major V tile
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+                oacc[db] = mfma32<T>(tr_operand<D>(vtb, c, db), pf[c], oacc[db]);
         }
     }
 
@@ -318,7 +279,7 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     const int64_t blocks = (int64_t)p.n_tiles * p.n_hg;
     if (blocks <= 0) return hipSuccess;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    if (g.bias != nullptr)
+    if (g.bias != nullptr || !(p.scale_log2 > 0.f))
         hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true>), dim3((unsigned)blocks), dim3(kThreads), 0, st, p);
     else
         hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false>), dim3((unsigned)blocks), dim3(kThreads), 0, st, p);
