@@ -5,19 +5,25 @@
 Headline (BASELINE.json metric): fwd+bwd TFLOP/s of causal GQA prefill,
 8 x 4096 tokens, Hq=32, Hkv=8, D=128, bf16 (config C3). One step = the forward
 with LSE plus the backward (delta preprocess, dQ, dK/dV) -- the work of one
-autograd step of the op. FLOPs count attended pairs only (the reference's
-convention, mtlattn/bench.py:25-32): fwd 4*D*Hq*pairs, bwd 2.5x that,
-fwd+bwd 14*D*Hq*pairs. Inputs are synthetic N(0,1) and resident in HBM before
-timing. The secondary line item is split-KV decode HBM GB/s (config C5).
+autograd step of the op, through the same `_C` calls autograd makes. FLOPs
+count attended pairs only (the reference's convention, mtlattn/bench.py:25-32):
+fwd 4*D*Hq*pairs, bwd 2.5x that, fwd+bwd 14*D*Hq*pairs. Inputs are synthetic
+N(0,1) and resident in HBM before timing. The secondary line item is split-KV
+decode HBM GB/s (config C5).
 
-Per-kernel times come from HIP events recorded on the stream the kernels run
-on (torch's current stream, which the extension launches on).
+Per-kernel times: each kernel is launched alone through the C ABI
+(mtlattn_amd/capi.py) on torch's current stream, K times back to back between
+two HIP events recorded on that same stream; the average launch duration is
+the figure. Algorithmic FLOPs per kernel split the 14*D*Hq*pairs of a step by
+the products each kernel must do: forward 4 (S, P.V), dK/dV 8 (S, dP, dV, dK),
+dQ 2 (dQ; its S and dP recomputation is not algorithmic work), preprocess 0.
 """
 
 import argparse
 import json
 import math
 import os
+import platform
 import sys
 import time
 
@@ -26,6 +32,11 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA (spec)
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E (spec)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+C3 = dict(B=8, L=4096, Hq=32, Hkv=8, D=128)
+C3_WORKLOAD = "C3 causal GQA prefill fwd+bwd: 8 seqs x 4096, Hq=32, Hkv=8, D=128, bf16"
+C5_WORKLOAD = "C5 split-KV decode: 64 seqs q_len=1, kv U[8192,65536] (seeded), Hq=64, Hkv=8, D=128, bf16"
 
 
 def parse():
@@ -36,8 +47,9 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["c3", "c5"], default=None,
-                    help="run one workload and print nothing but its timing (for profilers)")
+    ap.add_argument("--only", choices=["c3", "c5", "copy"], default=None,
+                    help="run one workload (or the 1 GiB copy used to calibrate HBM byte counters) "
+                         "and print only its timing: the short program profilers wrap")
     return ap.parse_args()
 
 
@@ -45,47 +57,47 @@ def c3_pairs(L=4096, B=8):
     return B * L * (L + 1) // 2
 
 
-def time_events(fn, steps, stream):
+def avg_launch_ms(fn, n, stream):
+    """Average duration of `fn` (one kernel launch) over n back-to-back
+    launches, from two HIP events recorded on `stream`."""
     import torch
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    for i in range(steps):
-        starts[i].record(stream)
-        fn()
-        ends[i].record(stream)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    start.record(stream)
+    for _ in range(n):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / n
+
+
+def c3_inputs(seed):
+    import torch
+    B, L, Hq, Hkv, D = (C3[x] for x in ("B", "L", "Hq", "Hkv", "D"))
+    g = torch.Generator().manual_seed(seed)
+    M = B * L
+    mk = lambda h: torch.randn(M, h, D, generator=g).to(torch.bfloat16)
+    q, k, v, do = mk(Hq), mk(Hkv), mk(Hkv), mk(Hq)
+    cu = torch.arange(0, M + 1, L, dtype=torch.int32)
+    return q, k, v, do, cu
 
 
 def bench_c3(args):
     import torch
     import mtlattn
+    from mtlattn_amd import capi
     C = mtlattn._C
-    dev = "cuda"
-    B, L, Hq, Hkv, D = 8, 4096, 32, 8, 128
-    g = torch.Generator().manual_seed(args.seed)
+    B, L, Hq, Hkv, D = (C3[x] for x in ("B", "L", "Hq", "Hkv", "D"))
+    q, k, v, do, cu = (t.cuda() for t in c3_inputs(args.seed))
     M = B * L
-    q = torch.randn(M, Hq, D, generator=g).to(torch.bfloat16).to(dev)
-    k = torch.randn(M, Hkv, D, generator=g).to(torch.bfloat16).to(dev)
-    v = torch.randn(M, Hkv, D, generator=g).to(torch.bfloat16).to(dev)
-    do = torch.randn(M, Hq, D, generator=g).to(torch.bfloat16).to(dev)
-    cu = torch.arange(0, M + 1, L, dtype=torch.int32, device=dev)
     scale = 1.0 / math.sqrt(D)
-    lse = torch.empty(M, Hq, dtype=torch.float32, device=dev)
-    delta = torch.empty(M, Hq, dtype=torch.float32, device=dev)
+    lse = torch.empty(M, Hq, dtype=torch.float32, device="cuda")
     state = {}
 
-    def fwd():
+    def step():
         state["o"] = C.varlen_attention(q, k, v, cu, cu, L, scale, True, 0, lse, None)
-
-    def bwd():
         state["g"] = C.varlen_attention_bwd(q, k, v, state["o"], do, lse, cu, cu, scale, True, 0, None)
 
-    def step():
-        fwd()
-        bwd()
-
-    stream = torch.cuda.current_stream()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -94,43 +106,71 @@ def bench_c3(args):
         step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-
-    # per-kernel split (same inputs, events on the launch stream)
-    fwd_ms = time_events(fwd, args.steps, stream)
     o = state["o"]
-    bwd_ms = time_events(bwd, args.steps, stream)
-    med = lambda xs: sorted(xs)[len(xs) // 2]
-    pairs = c3_pairs(L, B)
-    flops = 14.0 * D * Hq * pairs
-    tflops = flops / (wall_ms * 1e-3) / 1e12
     fin = bool(torch.isfinite(o.float()).all().item()) and all(
         bool(torch.isfinite(t.float()).all().item()) for t in state["g"])
-    return {
-        "ms_per_step": wall_ms, "tflops": tflops, "pairs": pairs, "flops": flops,
-        "fwd_ms": med(fwd_ms), "bwd_ms": med(bwd_ms), "finite": fin,
-        "fwd_tflops": 4.0 * D * Hq * pairs / (med(fwd_ms) * 1e-3) / 1e12,
-        "bwd_tflops": 10.0 * D * Hq * pairs / (med(bwd_ms) * 1e-3) / 1e12,
-    }, (q, k, v, do, cu, lse, delta, o, scale)
+
+    # one kernel per launch through the C ABI, on torch's current stream
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    p = capi.problem_for(q, k, cu, cu, L, scale, causal=True)
+    rs = Hq * D
+    rk = Hkv * D
+    delta = torch.empty(M, Hq, dtype=torch.float32, device="cuda")
+    dq = torch.empty_like(q)
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    out2 = torch.empty_like(q)
+    bf = capi.DTYPE_BF16
+    calls = {
+        "fwd_mfma": lambda: capi.call("mtlattn_varlen_fwd", p, q.data_ptr(), rs, k.data_ptr(), rk, v.data_ptr(), rk,
+                                      out2.data_ptr(), lse.data_ptr(), None, 0, sh),
+        "bwd_preprocess": lambda: capi.call("mtlattn_bwd_preprocess", p, o.data_ptr(), rs, do.data_ptr(), rs,
+                                            delta.data_ptr(), sh),
+        "bwd_dq": lambda: capi.call("mtlattn_bwd_dq", p, q.data_ptr(), rs, k.data_ptr(), rk, v.data_ptr(), rk,
+                                    do.data_ptr(), rs, lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), bf, sh),
+        "bwd_dkv": lambda: capi.call("mtlattn_bwd_dkv", p, q.data_ptr(), rs, k.data_ptr(), rk, v.data_ptr(), rk,
+                                     do.data_ptr(), rs, lse.data_ptr(), delta.data_ptr(), dk.data_ptr(),
+                                     dv.data_ptr(), bf, sh),
+    }
+    calls["fwd_mfma"]()
+    calls["bwd_preprocess"]()
+    n = max(5, args.steps // 2)
+    kern_ms = {}
+    for name, fn in calls.items():
+        fn()
+        kern_ms[name] = avg_launch_ms(fn, n, stream)
+    pairs = c3_pairs(L, B)
+    unit = D * Hq * pairs
+    algo = {"fwd_mfma": 4.0 * unit, "bwd_preprocess": 0.0, "bwd_dq": 2.0 * unit, "bwd_dkv": 8.0 * unit}
+    flops = 14.0 * unit
+    return {"ms_per_step": wall_ms, "tflops": flops / (wall_ms * 1e-3) / 1e12, "pairs": pairs, "flops": flops,
+            "kern_ms": kern_ms, "algo_flop": algo, "launches_timed": n, "finite": fin}
+
+
+def c5_inputs(seed):
+    import torch
+    B = 64
+    gl = torch.Generator().manual_seed(seed)
+    kv_lens = torch.randint(8192, 65537, (B,), generator=gl).tolist()
+    return kv_lens
 
 
 def bench_c5(args):
     import torch
     import mtlattn
     C = mtlattn._C
-    dev = "cuda"
     B, Hq, Hkv, D = 64, 64, 8, 128
-    gl = torch.Generator().manual_seed(args.seed)
-    kv_lens = torch.randint(8192, 65537, (B,), generator=gl).tolist()
+    kv_lens = c5_inputs(args.seed)
     g = torch.Generator().manual_seed(args.seed + 1)
     Mk = sum(kv_lens)
-    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16).to(dev)
-    k = torch.empty(Mk, Hkv, D, dtype=torch.bfloat16, device=dev)
-    v = torch.empty(Mk, Hkv, D, dtype=torch.bfloat16, device=dev)
-    gd = torch.Generator(device=dev).manual_seed(args.seed + 2)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16).cuda()
+    k = torch.empty(Mk, Hkv, D, dtype=torch.bfloat16, device="cuda")
+    v = torch.empty(Mk, Hkv, D, dtype=torch.bfloat16, device="cuda")
+    gd = torch.Generator(device="cuda").manual_seed(args.seed + 2)
     k.normal_(generator=gd)
     v.normal_(generator=gd)
-    cu_q = torch.arange(0, B + 1, dtype=torch.int32, device=dev)
-    cu_kv = torch.tensor([0] + list(torch.tensor(kv_lens).cumsum(0).tolist()), dtype=torch.int32, device=dev)
+    cu_q = torch.arange(0, B + 1, dtype=torch.int32, device="cuda")
+    cu_kv = torch.tensor([0] + list(torch.tensor(kv_lens).cumsum(0).tolist()), dtype=torch.int32, device="cuda")
     scale = 1.0 / math.sqrt(D)
 
     def run():
@@ -138,63 +178,97 @@ def bench_c5(args):
 
     for _ in range(max(3, args.warmup)):
         run()
-    torch.cuda.synchronize()
-    ms = time_events(run, max(10, args.steps), torch.cuda.current_stream())
-    t = sorted(ms)[len(ms) // 2]
+    ms = avg_launch_ms(run, max(10, args.steps), torch.cuda.current_stream())
     nbytes = Mk * Hkv * D * 2 * 2 + B * Hq * D * 2 * 2
     out = run()
     torch.cuda.synchronize()
-    return {"ms": t, "GBps": nbytes / (t * 1e-3) / 1e9, "bytes": nbytes, "sum_kv": Mk,
+    return {"ms": ms, "GBps": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "sum_kv": Mk,
             "finite": bool(torch.isfinite(out.float()).all().item())}
 
 
-def cpu_baseline(seed):
-    """The oracle (torch CPU fp32, explicit fwd+bwd formulas) on a bounded
-    sample of C3: sequence 0, kv heads 0-1 (query heads 0-7)."""
+def copy_calibration(args):
+    """A plain 1 GiB device-to-device copy: the known-size kernel the HBM byte
+    counters (FETCH_SIZE / WRITE_SIZE) are scaled by."""
+    import torch
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(max(1, args.steps)):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return n
+
+
+def cpu_baseline(seed, budget_s=12.0):
+    """The oracle (torch CPU fp32, explicit fwd+bwd formulas) on C3, one
+    sequence (all 8 kv heads, 32 query heads) at a time until `budget_s` of
+    CPU time is spent: a bounded sample of the same workload."""
     import torch
     import oracle
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    B, L, Hq, Hkv, D = 8, 4096, 32, 8, 128
-    g = torch.Generator().manual_seed(seed)
-    M = L   # one sequence is enough for the sample; same shapes per head
-    q = torch.randn(M, Hq, D, generator=g).to(torch.bfloat16)
-    k = torch.randn(M, Hkv, D, generator=g).to(torch.bfloat16)
-    v = torch.randn(M, Hkv, D, generator=g).to(torch.bfloat16)
-    do = torch.randn(M, Hq, D, generator=g).to(torch.bfloat16)
-    cu = torch.tensor([0, L], dtype=torch.int32)
-    heads = [0, 1]
+    B, L, Hq, Hkv, D = (C3[x] for x in ("B", "L", "Hq", "Hkv", "D"))
+    q, k, v, do, cu = c3_inputs(seed)
+    done = 0
     t0 = time.perf_counter()
-    oracle.varlen_forward_backward_blocked(q, k, v, do, cu, cu, causal=True, heads=heads, q_block=512)
+    for s in range(B):
+        oracle.varlen_forward_backward_blocked(q, k, v, do, cu, cu, causal=True, seqs=[s], q_block=512)
+        done += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
     dt = time.perf_counter() - t0
-    sample_pairs = L * (L + 1) // 2 * len(heads) * (Hq // Hkv)
-    flops = 14.0 * D * sample_pairs
-    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"C3 sequence 0 of 8, kv heads 0-1 (8 of 32 query heads), fwd+bwd, "
-                      f"{sample_pairs} attended pairs, {dt:.2f} s",
-            "seconds": dt}
+    sample_pairs = L * (L + 1) // 2 * done
+    flops = 14.0 * D * Hq * sample_pairs
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"C3 fwd+bwd, {done} of {B} sequences (all 32 query heads), "
+                      f"{sample_pairs * Hq} attended pairs, {dt:.1f} s; oracle "
+                      f"varlen_forward_backward_blocked fp32, torch {threads} threads on {cpu}"}
+
+
+def load_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE, WRITE_SIZE scaled by the copy calibration)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t["kernels"][kernel]["hbm_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU design is documented, not run.", file=sys.stderr)
+              "how the path shards over GPUs is documented, not run.", file=sys.stderr)
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    if args.only == "copy":
+        n = copy_calibration(args)
+        print(json.dumps({"copy_bytes": n, "launches": max(1, args.steps)}), flush=True)
+        return
     if args.only == "c3":
-        c3, _ = bench_c3(args)
-        print(json.dumps({"c3_ms_per_step": c3["ms_per_step"], "tflops": c3["tflops"]}), flush=True)
+        c3 = bench_c3(args)
+        print(json.dumps({"c3_ms_per_step": c3["ms_per_step"], "tflops": c3["tflops"],
+                          "kern_ms": c3["kern_ms"]}), flush=True)
         return
     if args.only == "c5":
         dec = bench_c5(args)
         print(json.dumps({"c5_ms": dec["ms"], "GBps": dec["GBps"]}), flush=True)
         return
-    c3, _ = bench_c3(args)
+    c3 = bench_c3(args)
     dec = None if args.no_decode else bench_c5(args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.seed)
-    dom = max((("fwd_mfma", c3["fwd_ms"], c3["fwd_tflops"]),), key=lambda x: x[1])
+    km, algo = c3["kern_ms"], c3["algo_flop"]
+    dom = max(km, key=km.get)
+    ach = algo[dom] / (km[dom] * 1e-3) / 1e12
     line = {
         "metric": "fwd+bwd TFLOP/s causal GQA 8x4096 D128 bf16; split-KV decode HBM GB/s",
         "value": round(c3["tflops"], 2),
@@ -208,21 +282,22 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic N(0,1), seeded",
-        "config": {"workload": "C3 causal GQA prefill fwd+bwd: 8 seqs x 4096, Hq=32, Hkv=8, D=128, bf16",
-                   "global_batch": 8, "seq_len": 4096, "parallelism": "single GPU",
-                   "attended_pairs_per_head": c3["pairs"], "flop_per_step": c3["flops"]},
-        "breakdown": {"fwd_ms": round(c3["fwd_ms"], 4), "bwd_ms": round(c3["bwd_ms"], 4),
-                      "fwd_tflops": round(c3["fwd_tflops"], 2), "bwd_tflops": round(c3["bwd_tflops"], 2),
-                      "outputs_finite": c3["finite"]},
-        "roofline": {"bound": "mfma", "achieved": round(c3["fwd_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(c3["fwd_tflops"] / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "kernel": dom[0]},
+        "config": {"workload": C3_WORKLOAD, "global_batch": C3["B"], "seq_len": C3["L"],
+                   "parallelism": "single GPU", "attended_pairs_per_head": c3["pairs"],
+                   "flop_per_step": c3["flops"]},
+        "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": load_traffic(dom), "kernel": dom,
+                     "kernel_ms": round(km[dom], 4), "algorithmic_flop": algo[dom]},
+        "kernels": {n: {"ms": round(t, 4),
+                        "tflops": round(algo[n] / (t * 1e-3) / 1e12, 2) if algo[n] else None}
+                    for n, t in km.items()},
         "decode": None if dec is None else {
-            "workload": "C5 split-KV decode: 64 seqs q_len=1, kv U[8192,65536], Hq=64, Hkv=8, D=128, bf16",
+            "workload": C5_WORKLOAD,
             "ms": round(dec["ms"], 4), "GBps": round(dec["GBps"], 1), "bytes": dec["bytes"],
             "roofline": {"bound": "hbm", "achieved": round(dec["GBps"], 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(dec["GBps"] / PEAK_HBM_GBS, 4)},
             "outputs_finite": dec["finite"]},
+        "outputs_finite": c3["finite"],
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -14,6 +14,13 @@ Two criteria are used:
     criterion is therefore: RMS(err) / RMS(ref) <= tol, and
     max|err| / RMS(ref) <= 2 * floor + tol; both the literal metric and the
     floor are reported from the same run.
+
+For fp32, C1 (the config the bar is stated for) is asserted literally. Other
+fp32 cases with heavy-tailed rows (few-key rows whose |out| is many times the
+RMS) can sit at the level of fp32 arithmetic itself: there the fp32 CPU
+oracle's own max|err| / RMS against the fp64 oracle (`floor32`, measured in
+the same test) is passed in, and the kernels must stay within
+tol + 2 * floor32 of the fp64 oracle.
 """
 
 import math
@@ -22,6 +29,10 @@ import torch
 
 TOL_RMS = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 2e-2}
 REF_ATOL = {torch.float32: 1e-4, torch.float16: 5e-3, torch.bfloat16: 3e-2}
+# LSE (natural log) absolute bound. The 16-bit kernels sum P after rounding it
+# to the input type (the values the P.V product consumes); each term carries a
+# relative error <= 2^-9 (bf16) / 2^-12 (fp16), so log(l) is off by <= ~2^-9.
+LSE_TOL = {torch.float32: 2e-5, torch.float16: 2e-3, torch.bfloat16: 2e-3}
 
 
 def cu_of(lens, device="cpu"):
@@ -35,7 +46,7 @@ def randn(shape, dtype, gen):
     return torch.randn(shape, generator=gen, dtype=torch.float32).to(dtype)
 
 
-def err_stats(out, ref, dtype):
+def err_stats(out, ref, dtype, floor32=0.0):
     """Returns dict: max_abs, rms_ref, rel (literal max|err| / RMS(ref)),
     rms_rel (RMS(err) / RMS(ref)), floor (the literal metric of the exactly
     rounded reference) and ok (the criterion described in the module doc)."""
@@ -56,7 +67,7 @@ def err_stats(out, ref, dtype):
     rms_rel = rms_err / rms if rms > 0 else (0.0 if rms_err == 0 else math.inf)
     tol = TOL_RMS[dtype]
     if dtype == torch.float32:
-        ok = rel <= tol
+        ok = rel <= tol + 2.0 * floor32
     else:
         ok = rms_rel <= tol and rel <= 2.0 * floor + tol
     ok = ok and bool(torch.isfinite(o).all()) and bool(torch.equal(torch.isfinite(out), finite))

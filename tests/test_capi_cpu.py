@@ -169,3 +169,17 @@ def test_dq_dtype_checked(lib):
     p = problem()
     rc = lib.mtlattn_bwd_dq(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, 0, FAKE, FAKE, FAKE, F16, None)
     assert rc == ERR_INVALID and b"dq dtype" in lib.mtlattn_last_error()
+
+
+def test_ctypes_binding_covers_header():
+    """mtlattn_amd/capi.py declares every function of the header, with the
+    header's parameter count."""
+    from mtlattn_amd import capi
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decl = dict(re.findall(r"\b(mtlattn_\w+)\s*\(([^)]*)\)\s*;", text))
+    assert set(decl) == set(capi.SIGNATURES)
+    for name, params in decl.items():
+        n = 0 if params.strip() in ("", "void") else params.count(",") + 1
+        assert len(capi.SIGNATURES[name][1]) == n, name
+    assert capi.lib().mtlattn_abi_version() == capi.ABI_VERSION
