@@ -10,16 +10,18 @@
 // P and dS are rounded to the input type before the second products, as the
 // forward rounds P before P.V.
 //
-// dQ kernel: workgroup of 8 waves, 32 query rows x 1 head per wave, GQA heads
-//   packed like the forward. Per 64-key tile staged in LDS (K row-major, V
-//   row-major, K^T): S^T = K Q^T and dP^T = V dO^T (C layout: lane = query),
-//   dS^T in registers, dQ^T += K^T dS^T.
-// dK/dV kernel: workgroup of 8 waves, 32 keys per wave (256 keys of one kv
-//   head). Loops over the g query heads of the group and over 64-query tiles
-//   staged in LDS (Q, Q^T, dO, dO^T, lse, delta): S = Q K^T and dP = dO V^T
-//   (C layout: lane = key), dV^T += dO^T P, dK^T += Q^T dS. Causal and window
-//   bands skip whole query tiles (the reference skips causal only,
-//   src/attn_mpp.metal:591).
+// dQ kernel: workgroup of 8 waves (2 per SIMD), 32 query rows x 1 head per
+//   wave, GQA heads packed like the forward. Per 64-key tile staged in LDS by
+//   direct loads (K, V row-major, swizzled): S^T = K Q^T and dP^T = V dO^T
+//   (C layout: lane = query), dS^T in registers, dQ^T += K^T dS^T with K^T
+//   read through transposing LDS loads.
+// dK/dV kernel: workgroup of 4 wave pairs, 32 keys per pair (128 keys of one
+//   kv head). Loops over the g query heads of the group and over 64-query
+//   stages staged by direct loads (Q, dO, lse, delta). Wave A of a pair:
+//   S = Q K^T, P, dV^T += dO^T P; wave B, one stage behind: dP = dO V^T,
+//   dS = P (dP - delta) with P handed over through LDS, dK^T += Q^T dS.
+//   Causal and window bands skip whole query blocks (the reference skips
+//   causal only, src/attn_mpp.metal:591).
 #include "common.h"
 #include "kernels.h"
 #include "../../include/mtlattn_capi.h"
@@ -65,30 +67,27 @@ __device__ inline void store4(void* base, int64_t off, float a, float b, float c
 }
 
 // ---------------------------------------------------------------------------
-// dQ
+// dQ.  8 waves (2 per SIMD), 32 query rows x 1 head per wave, the heads of a
+// GQA group packed as in the forward. Key tiles of 64 rows go straight from
+// HBM into a 3-deep LDS ring (K and V row-major, swizzled); K^T operands of
+// the dQ product are transposed LDS reads of the same K tile.
 // ---------------------------------------------------------------------------
-// 8 waves at D = 64; 4 waves (one per SIMD, 512-register budget) at D = 128.
-template <int D> struct DqCfg { static constexpr int NW = D >= 128 ? 4 : 8; };
-
 template <typename T, int D, bool BIAS, bool OUT_F32>
-__global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams p) {
-    constexpr int NW = DqCfg<D>::NW;
-    constexpr int HALF = NW * 32;             // loader threads per role
+__global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     constexpr int DC = D / 16, DB = D / 32;
-    constexpr int TILE_BYTES = kKT * D * 2;
-    constexpr int STAGE = 3 * TILE_BYTES;     // K, V (row-major), K^T
-    constexpr int KUNITS = 2 * D;             // (4 keys x 8 d) units
-    constexpr int KUPT = (KUNITS + HALF - 1) / HALF;   // K units per loader thread
-    constexpr int VCH = kKT * D / 8 / HALF;   // 16-byte V chunks per loader thread
-    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+    constexpr int TILE = kKT * D * 2;
+    constexpr int STAGE = 2 * TILE;           // K, V
+    constexpr int NBUF = 3;
+    constexpr int LOADS = STAGE / 1024 / kWaves;
+    __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
     const int l32 = lane & 31, hi = lane >> 5;
-    const int QT = 32 * (NW / p.hpw);
+    const int QT = 32 * (kWaves / p.hpw);
     const int L = xcd_remap(blockIdx.x, p.n_tiles * p.n_hg);
     const int hg = L / p.n_tiles;
-    const int t = p.n_tiles - 1 - (L - hg * p.n_tiles);
+    const int t = p.n_tiles - 1 - (L - hg * p.n_tiles);   // late (heavier) tiles first
     const int s = find_seq_for_tile(p.cu_q, p.num_seqs, QT, t, p.total_q);
     const int tb = tile_base(p.cu_q, s, QT, p.total_q);
     if (t < tb) return;
@@ -98,7 +97,7 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
     const int q0 = (t - tb) * QT;
     if (q0 >= q_len) return;
 
-    const int wph = NW / p.hpw;
+    const int wph = kWaves / p.hpw;
     const int head = hg * p.hpw + w / wph;
     const int hk = head / p.g;
     const int qa = q0 + 32 * (w % wph);
@@ -140,131 +139,66 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
     const int n_kv_tiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kKT - 1) / kKT : 0;
     const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * D;
     const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * D;
-
-    // Loader roles: the first half of the threads stage K (row-major and
-    // transposed), the second half V (row-major).
-    const bool role_k = w < NW / 2;               // wave-uniform roles
-    const int rt = role_k ? tid : tid - HALF;
-    const int rt0 = role_k ? 64 * w : 64 * w - HALF;  // rt of lane 0 (unit counts are multiples of 64)
-    constexpr int NPRE = KUPT * 4 > VCH ? KUPT * 4 : VCH;
-    u32x4_t pre[NPRE];
-    auto load_tile = [&](int kt) {
-        if (role_k) {
-#pragma unroll
-            for (int uu = 0; uu < KUPT; ++uu) {
-                const int u = rt + HALF * uu;
-                if (rt0 + HALF * uu < KUNITS) {
-                    const int dc = u % (D / 8), kg = u / (D / 8);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int key = min(kt + 4 * kg + i, kv_len - 1);   // masked past the end
-                        pre[4 * uu + i] = ld16(kbase + (int64_t)key * p.k_rs + 8 * dc);
-                    }
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < VCH; ++i) {
-                const int cid = rt + HALF * i;
-                const int key = min(kt + cid / (D / 8), kv_len - 1);
-                pre[i] = ld16(vbase + (int64_t)key * p.v_rs + 8 * (cid % (D / 8)));
-            }
-        }
-    };
-    auto store_tile = [&](int buf) {
-        char* Ks = smem + buf * STAGE;
-        char* Vs = Ks + TILE_BYTES;
-        char* Kt = Vs + TILE_BYTES;
-        if (role_k) {
-#pragma unroll
-            for (int uu = 0; uu < KUPT; ++uu) {
-                const int u = rt + HALF * uu;
-                if (rt0 + HALF * uu < KUNITS) {
-                    const int dc = u % (D / 8), kg = u / (D / 8);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) st16(Ks + rm_offset<D>(4 * kg + i, dc), pre[4 * uu + i]);
-                    u32x2_t tr[8];
-                    transpose4x8(&pre[4 * uu], tr);
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) st8(Kt + tr_store_offset(8 * dc + i, kg), tr[i]);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < VCH; ++i) {
-                const int cid = rt + HALF * i;
-                st16(Vs + rm_offset<D>(cid / (D / 8), cid % (D / 8)), pre[i]);
-            }
-        }
+    auto stage = [&](int it) {
+        char* buf = smem + (it % NBUF) * STAGE;
+        const int kt = kv_lo + it * kKT;
+        stage_tile<D, kKT, kWaves>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
+        stage_tile<D, kKT, kWaves>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
     };
 
-    // Per-lane LDS read offsets (see the forward kernel): row-major operands
-    // for rows 32 kb + l32, transposed K^T operands for rows 32 db + l32.
-    uint32_t rofs[4], tofs[4];
+    uint32_t kofs[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        rofs[c] = rm_offset<D>(l32, 2 * c + hi);
-        tofs[c] = tr_load_offset(l32, c, hi);
-    }
+    for (int c = 0; c < 4; ++c) kofs[c] = tile_offset<D>(l32, 2 * c + hi);
+    const uint32_t trb[2] = {tr_base<D>(lane, 0), tr_base<D>(lane, 1)};
+    const float c2 = p.scale_log2;
 
     f32x16_t dqacc[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) dqacc[db] = f32x16_t{};
 
-    if (n_kv_tiles > 0) {
-        load_tile(kv_lo);
-        store_tile(0);
+    if (n_kv_tiles > 0) stage(0);
+    if (n_kv_tiles > 1) stage(1);
+    for (int it = 0; it < n_kv_tiles; ++it) {
+        if (it + 1 < n_kv_tiles) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
         __syncthreads();
-        for (int it = 0; it < n_kv_tiles; ++it) {
-            const int kt = kv_lo + it * kKT;
-            const bool has_next = it + 1 < n_kv_tiles;
-            if (has_next) load_tile(kt + kKT);
-
-            bool skip = !wave_active;
-            if (p.causal && kt > wq_last + coff) skip = true;
-            if (p.window > 0 && kt + kKT - 1 < qa + coff - p.window + 1) skip = true;
-            if (!skip) {
-                const char* Ks = smem + (it & 1) * STAGE;
-                const char* Vs = Ks + TILE_BYTES;
-                const char* Kt = Vs + TILE_BYTES;
-                const bool need_mask = (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
-                                       (p.window > 0 && kt < wq_last + coff - p.window + 1);
-                // Two independent 32-key halves: P = exp(S - lse) needs no running max.
+        if (it + 2 < n_kv_tiles) stage(it + 2);
+        const int kt = kv_lo + it * kKT;
+        bool skip = !wave_active;
+        if (p.causal && kt > wq_last + coff) skip = true;
+        if (p.window > 0 && kt + kKT - 1 < qa + coff - p.window + 1) skip = true;
+        if (skip) continue;
+        const char* Ks = smem + (it % NBUF) * STAGE;
+        const char* Vs = Ks + TILE;
+        const char* const ktb[2] = {opaque(Ks + trb[0]), opaque(Ks + trb[1])};
+        const bool need_mask = (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
+                               (p.window > 0 && kt < wq_last + coff - p.window + 1);
+        // two independent 32-key halves: P = exp2(S - lse) needs no running max
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    f32x16_t sacc = f32x16_t{}, pacc = f32x16_t{};
+        for (int kb = 0; kb < 2; ++kb) {
+            f32x16_t sacc = f32x16_t{}, pacc = f32x16_t{};
 #pragma unroll
-                    for (int kc = 0; kc < DC; ++kc) {
-                        const uint32_t o = rofs[kc & 3] + (kc >> 2) * 128 + kb * 32 * 2 * D;
-                        sacc = mfma32<T>(ld16(Ks + o), qf[kc], sacc);
-                        pacc = mfma32<T>(ld16(Vs + o), df[kc], pacc);
-                    }
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
-                        const bool ok = !need_mask || allowed(qrow, key, coff, kv_len, p.causal, p.window);
-                        float x = sacc[r] * p.scale_log2;
-                        if (BIAS && ok && brow != nullptr && key < p.bias_cols) x += brow[key] * kLog2e;
-                        const float pr = ok ? __builtin_amdgcn_exp2f(x - lse2) : 0.f;
-                        sacc[r] = pr * (pacc[r] - dlt);        // dS^T
-                    }
-#pragma unroll
-                    for (int cc = 0; cc < 2; ++cc) {
-                        const int c = 2 * kb + cc, r0 = 8 * cc;
-                        const u32x4_t bs = u32x4_t{T::pack2(sacc[r0 + 0], sacc[r0 + 1]),
-                                                   T::pack2(sacc[r0 + 2], sacc[r0 + 3]),
-                                                   T::pack2(sacc[r0 + 4], sacc[r0 + 5]),
-                                                   T::pack2(sacc[r0 + 6], sacc[r0 + 7])};
-#pragma unroll
-                        for (int db = 0; db < DB; ++db) {
-                            const u32x4_t a = ld16(Kt + tofs[c ^ (2 * (db & 1))] + db * 32 * 128);
-                            dqacc[db] = mfma32<T>(a, bs, dqacc[db]);
-                        }
-                    }
-                }
+            for (int kc = 0; kc < DC; ++kc) {
+                const uint32_t o = kofs[kc & 3] + (kc >> 2) * 128 + kb * 32 * 2 * D;
+                sacc = mfma32<T>(ld16(Ks + o), qf[kc], sacc);
+                pacc = mfma32<T>(ld16(Vs + o), df[kc], pacc);
             }
-            if (has_next) store_tile((it + 1) & 1);
-            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
+                const bool ok = !need_mask || allowed(qrow, key, coff, kv_len, p.causal, p.window);
+                float x = sacc[r] * c2;
+                if (BIAS && ok && brow != nullptr && key < p.bias_cols) x = fmaf(brow[key], kLog2e, x);
+                const float pr = ok ? __builtin_amdgcn_exp2f(x - lse2) : 0.f;
+                sacc[r] = pr * (pacc[r] - dlt);        // dS^T
+            }
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                const int c = 2 * kb + cc, r0 = 8 * cc;
+                const u32x4_t bs = u32x4_t{T::pack2(sacc[r0 + 0], sacc[r0 + 1]), T::pack2(sacc[r0 + 2], sacc[r0 + 3]),
+                                           T::pack2(sacc[r0 + 4], sacc[r0 + 5]), T::pack2(sacc[r0 + 6], sacc[r0 + 7])};
+#pragma unroll
+                for (int db = 0; db < DB; ++db) dqacc[db] = mfma32<T>(tr_operand<D>(ktb, c, db), bs, dqacc[db]);
+            }
         }
     }
 
@@ -283,31 +217,40 @@ __global__ __launch_bounds__(DqCfg<D>::NW * 64, 1) void bwd_dq_kernel(BwdKParams
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV.  NW waves of 32 keys each: 8 waves at D = 64; at D = 128 the
-// per-wave state (K, V operands + two D x 32 fp32 accumulators) needs the
-// full 512-register budget, so 4 waves (one per SIMD).
+// dK / dV.  8 waves = 4 pairs; pair i is waves i and i + 4 (the same SIMD)
+// and owns 32 keys of one kv head, so a workgroup owns 128 keys. The pair
+// splits the four products between its two waves:
+//   wave A (i):     S = Q K^T,  P = exp2(S c - lse2),  dV^T += dO^T P
+//   wave B (i + 4): dP = dO V^T, dS = P (dP - delta),   dK^T += Q^T dS
+// A hands P (rounded to the input type, C layout) to B through LDS; B runs
+// one stage behind A, so one barrier per stage orders everything. Each wave
+// holds one operand (K or V) and one accumulator set in registers, which keeps
+// both waves of a SIMD resident: one's softmax overlaps the other's MFMAs.
+// A stage is (query head h of the group, 64-query tile): Q, dO, lse and delta
+// go straight from HBM into a 3-deep LDS ring (row-major, swizzled); Q^T and
+// dO^T operands are transposed LDS reads. The loop covers the g heads of the
+// group, so the GQA reduction of dK/dV happens in registers.
 // ---------------------------------------------------------------------------
-template <int D> struct DkvCfg { static constexpr int NW = D >= 128 ? 4 : 8; };
-
 template <typename T, int D, bool BIAS, bool OUT_F32>
-__global__ __launch_bounds__(DkvCfg<D>::NW * 64, 1) void bwd_dkv_kernel(BwdKParams p) {
-    constexpr int NW = DkvCfg<D>::NW;
-    constexpr int NT = NW * 64;
-    constexpr int HALF = NT / 2;                           // loader threads per role
+__global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     constexpr int DC = D / 16, DB = D / 32;
-    constexpr int TILE_BYTES = kQT * D * 2;
-    constexpr int STAGE = 4 * TILE_BYTES + 2 * kQT * 4;  // Q, Q^T, dO, dO^T, lse2, delta
-    constexpr int UNITS = 2 * D;                           // (4 rows x 8 d) units per tile
-    constexpr int UPT = (UNITS + HALF - 1) / HALF;         // units per loader thread
-    constexpr int KB = NW * kKW;                           // keys per workgroup
-    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+    constexpr int NP = kWaves / 2;                      // wave pairs
+    constexpr int KB = NP * kKW;                        // keys per workgroup
+    constexpr int TILE = kQT * D * 2;
+    constexpr int STAGE = 2 * TILE + 2 * kQT * 4;       // Q, dO, lse, delta
+    constexpr int NBUF = 3;
+    constexpr int PBLK = 2 * 1024;                      // packed P of one 32x32 block
+    constexpr int PSTAGE = NP * 2 * PBLK;               // one stage, all pairs
+    __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE + 2 * PSTAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
     const int l32 = lane & 31, hi = lane >> 5;
+    const bool role_a = w < NP;
+    const int pair = w & (NP - 1);
     const int L = xcd_remap(blockIdx.x, p.n_tiles * p.hkv);
     const int hk = L / p.n_tiles;
-    const int t = L - hk * p.n_tiles;                      // early key blocks (heavier when causal) first
+    const int t = L - hk * p.n_tiles;                  // early key blocks (heavier when causal) first
     const int s = find_seq_for_tile(p.cu_kv, p.num_seqs, KB, t, p.total_kv);
     const int tb = tile_base(p.cu_kv, s, KB, p.total_kv);
     if (t < tb) return;
@@ -318,23 +261,21 @@ __global__ __launch_bounds__(DkvCfg<D>::NW * 64, 1) void bwd_dkv_kernel(BwdKPara
     if (k0 >= kv_len) return;
     const int coff = kv_len - q_len;
 
-    const int kw = k0 + kKW * w;                 // first key of this wave (seq-local)
-    const bool wave_active = kw < kv_len;
+    const int kw = k0 + kKW * pair;              // first key of this pair (seq-local)
+    const bool pair_active = kw < kv_len;
     const int wk_last = min(kv_len, kw + kKW) - 1;
     const int key = kw + l32;                    // this lane's key column
     const bool key_ok = key < kv_len;
 
-    // K^T / V^T B operands: lane = key, d = 16 kc + 8 hi + j.
-    u32x4_t kf[DC], vf[DC];
+    // B operand of this wave's first product: K^T (wave A) or V^T (wave B),
+    // lane = key, d = 16 kc + 8 hi + j.
+    u32x4_t kvf[DC];
     {
         const int64_t grow = kr.start + min(key, kv_len - 1);     // masked past the end
-        const uint16_t* kp = p.k + grow * p.k_rs + (int64_t)hk * D + 8 * hi;
-        const uint16_t* vp = p.v + grow * p.v_rs + (int64_t)hk * D + 8 * hi;
+        const uint16_t* kp = role_a ? p.k + grow * p.k_rs : p.v + grow * p.v_rs;
+        kp += (int64_t)hk * D + 8 * hi;
 #pragma unroll
-        for (int kc = 0; kc < DC; ++kc) {
-            kf[kc] = ld16(kp + 16 * kc);
-            vf[kc] = ld16(vp + 16 * kc);
-        }
+        for (int kc = 0; kc < DC; ++kc) kvf[kc] = ld16(kp + 16 * kc);
     }
 
     // Query range that can see any key of this workgroup.
@@ -344,167 +285,156 @@ __global__ __launch_bounds__(DkvCfg<D>::NW * 64, 1) void bwd_dkv_kernel(BwdKPara
     const int n_q_tiles = q_hi > q_lo ? (q_hi - q_lo + kQT - 1) / kQT : 0;
     const int n_stages = n_q_tiles * p.g;
 
-    // Loader roles: the first half of the threads stage Q (row-major +
-    // transposed) and lse, the second half dO (row-major + transposed) and delta.
-    const bool role_q = w < NW / 2;               // wave-uniform roles
-    const int rt = role_q ? tid : tid - HALF;
-    const int rt0 = role_q ? 64 * w : 64 * w - HALF;  // rt of lane 0 (unit counts are multiples of 64)
-    u32x4_t pre[UPT][4];
-    float pre_s = 0.f;
-    auto load_stage = [&](int st) {
+    // Direct loads of stage `st`: Q and dO tiles by all waves, lse by wave 0,
+    // delta by wave 1 (4 bytes per lane, lane l -> row l).
+    auto stage = [&](int st) {
+        char* buf = smem + (st % NBUF) * STAGE;
         const int h = hk * p.g + st / n_q_tiles;
         const int qt = q_lo + (st % n_q_tiles) * kQT;
-        const uint16_t* base = role_q ? p.q : p.dout;
-        const int64_t rs = role_q ? p.q_rs : p.do_rs;
-#pragma unroll
-        for (int uu = 0; uu < UPT; ++uu) {
-            const int u = rt + HALF * uu;
-            if (rt0 + HALF * uu < UNITS) {
-                const int dc = u % (D / 8), qg = u / (D / 8);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    // rows past the end read the last row; their lse is +inf, so P = dS = 0
-                    const int q = min(qt + 4 * qg + i, q_len - 1);
-                    pre[uu][i] = ld16(base + (int64_t)(qr.start + q) * rs + (int64_t)h * D + 8 * dc);
-                }
-            }
-        }
-        if (rt0 == 0) {                          // first wave of each role: 64 rows
-            const int q = qt + rt;
-            if (role_q) {
-                float l2 = kPosInf;
-                if (q < q_len) {
-                    const float l = p.lse[(int64_t)(qr.start + q) * p.hq + h];
-                    l2 = l == kNegInf ? kPosInf : l * kLog2e;
-                }
-                pre_s = l2;
-            } else {
-                pre_s = q < q_len ? p.delta[(int64_t)(qr.start + q) * p.hq + h] : 0.f;
-            }
+        const int64_t hoff = (int64_t)qr.start * p.q_rs + (int64_t)h * D;
+        stage_tile<D, kQT, kWaves>(buf, p.q + hoff, p.q_rs, qt, q_len, w, lane);
+        stage_tile<D, kQT, kWaves>(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * D, p.do_rs, qt,
+                                   q_len, w, lane);
+        if (w < 2) {
+            const int q = min(qt + lane, q_len - 1);        // rows past the end are masked
+            const float* src = (w == 0 ? p.lse : p.delta) + (int64_t)(qr.start + q) * p.hq + h;
+            __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(buf + 2 * TILE + w * kQT * 4), 4, 0, 0);
         }
     };
-    auto store_stage = [&](int buf) {
-        char* Qs = smem + buf * STAGE;
-        char* Qt = Qs + TILE_BYTES;
-        char* Ds = Qt + TILE_BYTES;
-        char* Dt = Ds + TILE_BYTES;
-        float* ls = reinterpret_cast<float*>(Dt + TILE_BYTES);
-        float* ds = ls + kQT;
-        char* rm = role_q ? Qs : Ds;
-        char* tr = role_q ? Qt : Dt;
+
+    uint32_t rofs[4];
 #pragma unroll
-        for (int uu = 0; uu < UPT; ++uu) {
-            const int u = rt + HALF * uu;
-            if (rt0 + HALF * uu < UNITS) {
-                const int dc = u % (D / 8), qg = u / (D / 8);
+    for (int c = 0; c < 4; ++c) rofs[c] = tile_offset<D>(l32, 2 * c + hi);
+    const uint32_t trb[2] = {tr_base<D>(lane, 0), tr_base<D>(lane, 1)};
+    const float c2 = p.scale_log2;
+
+    f32x16_t acc[DB];                            // dV^T (wave A) or dK^T (wave B)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) st16(rm + rm_offset<D>(4 * qg + i, dc), pre[uu][i]);
-                u32x2_t trv[8];
-                transpose4x8(pre[uu], trv);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) st8(tr + tr_store_offset(8 * dc + i, qg), trv[i]);
-            }
-        }
-        if (rt0 == 0) (role_q ? ls : ds)[rt] = pre_s;
+    for (int db = 0; db < DB; ++db) acc[db] = f32x16_t{};
+
+    // Is the 32x32 block (queries qf0.., this pair's keys) of stage st empty
+    // or does it need per-element masking? Identical in both waves of a pair.
+    auto block_state = [&](int st, int qb, bool& need_mask) {
+        const int qf0 = q_lo + (st % n_q_tiles) * kQT + 32 * qb;
+        const int qf1 = min(q_len, qf0 + 32) - 1;
+        bool skip = !pair_active || qf0 >= q_len;
+        if (p.causal && kw > qf1 + coff) skip = true;
+        if (p.window > 0 && wk_last < qf0 + coff - p.window + 1) skip = true;
+        need_mask = (kw + kKW > kv_len) || (qf0 + 32 > q_len) || (p.causal && wk_last > qf0 + coff) ||
+                    (p.window > 0 && kw < qf1 + coff - p.window + 1);
+        return !skip;
     };
-
-    uint32_t rofs[4], tofs[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        rofs[c] = rm_offset<D>(l32, 2 * c + hi);
-        tofs[c] = tr_load_offset(l32, c, hi);
-    }
-
-    f32x16_t dkacc[DB], dvacc[DB];
-#pragma unroll
-    for (int db = 0; db < DB; ++db) { dkacc[db] = f32x16_t{}; dvacc[db] = f32x16_t{}; }
 
     if (n_stages > 0) {
-        load_stage(0);
-        store_stage(0);
+        stage(0);
+        wait_vmcnt<0>();
         __syncthreads();
-        for (int st = 0; st < n_stages; ++st) {
-            const bool has_next = st + 1 < n_stages;
-            if (has_next) load_stage(st + 1);
+    }
+    for (int st = 0; n_stages > 0 && st <= n_stages; ++st) {
+        if (st + 1 < n_stages) stage(st + 1);
+        if (role_a && st < n_stages) {
+            const char* Qs = smem + (st % NBUF) * STAGE;
+            const char* Ds = Qs + TILE;
+            const float* ls = reinterpret_cast<const float*>(Qs + 2 * TILE);
+            const char* const dtb[2] = {opaque(Ds + trb[0]), opaque(Ds + trb[1])};
+            char* pb = smem + NBUF * STAGE + (st & 1) * PSTAGE + pair * 2 * PBLK;
             const int h = hk * p.g + st / n_q_tiles;
             const int qt = q_lo + (st % n_q_tiles) * kQT;
-            const char* Qs = smem + (st & 1) * STAGE;
-            const char* Qt = Qs + TILE_BYTES;
-            const char* Ds = Qt + TILE_BYTES;
-            const char* Dt = Ds + TILE_BYTES;
-            const float* ls = reinterpret_cast<const float*>(Dt + TILE_BYTES);
-            const float* dls = ls + kQT;
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
-                const int qf0 = qt + 32 * qb;            // first query of this block
-                const int qf1 = min(q_len, qf0 + 32) - 1;
-                bool skip = !wave_active || qf0 >= q_len;
-                if (p.causal && kw > qf1 + coff) skip = true;
-                if (p.window > 0 && wk_last < qf0 + coff - p.window + 1) skip = true;
-                if (skip) continue;
-                const bool need_mask = (kw + kKW > kv_len) || (qf0 + 32 > q_len) ||
-                                       (p.causal && wk_last > qf0 + coff) ||
-                                       (p.window > 0 && kw < qf1 + coff - p.window + 1);
-                f32x16_t sacc = f32x16_t{}, pacc = f32x16_t{};
+                bool need_mask;
+                if (!block_state(st, qb, need_mask)) continue;
+                f32x16_t sacc = f32x16_t{};
 #pragma unroll
-                for (int kc = 0; kc < DC; ++kc) {
-                    const uint32_t o = rofs[kc & 3] + (kc >> 2) * 128 + qb * 32 * 2 * D;
-                    sacc = mfma32<T>(ld16(Qs + o), kf[kc], sacc);
-                    pacc = mfma32<T>(ld16(Ds + o), vf[kc], pacc);
-                }
+                for (int kc = 0; kc < DC; ++kc)
+                    sacc = mfma32<T>(ld16(Qs + rofs[kc & 3] + (kc >> 2) * 128 + qb * 32 * 2 * D), kvf[kc], sacc);
+                __builtin_amdgcn_sched_barrier(0);
                 const float* brow0 = nullptr;
                 if (BIAS) brow0 = p.bias + (int64_t)h * p.bias_hs + key;
 #pragma unroll
                 for (int rg = 0; rg < 4; ++rg) {
-                    const int qi = 32 * qb + 8 * rg + 4 * hi;   // stage-local query of r = 4 rg
+                    const int qi = 32 * qb + 8 * rg + 4 * hi;    // stage-local query of r = 4 rg
                     const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(ls + qi);
-                    const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(dls + qi);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int r = 4 * rg + e;
                         const int qrow = qt + qi + e;
                         const bool ok = !need_mask ||
                                         (qrow < q_len && allowed(qrow, key, coff, kv_len, p.causal, p.window));
-                        float x = sacc[r] * p.scale_log2;
+                        float x = sacc[r] * c2;
                         if (BIAS && ok && key < p.bias_cols)
-                            x += brow0[(int64_t)(qr.start + qrow) * p.bias_qs] * kLog2e;
-                        const float pr = ok ? __builtin_amdgcn_exp2f(x - l4[e]) : 0.f;
-                        sacc[r] = pr;                               // P
-                        pacc[r] = pr * (pacc[r] - d4[e]);           // dS
+                            x = fmaf(brow0[(int64_t)(qr.start + qrow) * p.bias_qs], kLog2e, x);
+                        // rows whose every logit is -inf (bias) have lse = -inf: P = 0
+                        const bool live = ok && (!BIAS || x != kNegInf);
+                        sacc[r] = live ? __builtin_amdgcn_exp2f(x - l4[e] * kLog2e) : 0.f;
                     }
                 }
 #pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const int r0 = 8 * c;
+                for (int cc = 0; cc < 2; ++cc) {
+                    const int r0 = 8 * cc;
                     const u32x4_t bp = u32x4_t{T::pack2(sacc[r0 + 0], sacc[r0 + 1]), T::pack2(sacc[r0 + 2], sacc[r0 + 3]),
                                                T::pack2(sacc[r0 + 4], sacc[r0 + 5]), T::pack2(sacc[r0 + 6], sacc[r0 + 7])};
-                    const u32x4_t bs = u32x4_t{T::pack2(pacc[r0 + 0], pacc[r0 + 1]), T::pack2(pacc[r0 + 2], pacc[r0 + 3]),
-                                               T::pack2(pacc[r0 + 4], pacc[r0 + 5]), T::pack2(pacc[r0 + 6], pacc[r0 + 7])};
-                    const int cc = 2 * qb + c;                 // 16-query chunk within the stage
+                    st16(pb + qb * PBLK + cc * 1024 + lane * 16, bp);
 #pragma unroll
-                    for (int db = 0; db < DB; ++db) {
-                        const uint32_t o = tofs[cc ^ (2 * (db & 1))] + db * 32 * 128;
-                        dvacc[db] = mfma32<T>(ld16(Dt + o), bp, dvacc[db]);
-                        dkacc[db] = mfma32<T>(ld16(Qt + o), bs, dkacc[db]);
-                    }
+                    for (int db = 0; db < DB; ++db)
+                        acc[db] = mfma32<T>(tr_operand<D>(dtb, 2 * qb + cc, db), bp, acc[db]);
                 }
             }
-            if (has_next) store_stage((st + 1) & 1);
-            __syncthreads();
         }
+        if (!role_a && st > 0) {
+            const int sp = st - 1;                    // wave B works one stage behind
+            const char* Qs = smem + (sp % NBUF) * STAGE;
+            const char* Ds = Qs + TILE;
+            const float* dls = reinterpret_cast<const float*>(Qs + 2 * TILE) + kQT;
+            const char* const qtb[2] = {opaque(Qs + trb[0]), opaque(Qs + trb[1])};
+            const char* pb = smem + NBUF * STAGE + (sp & 1) * PSTAGE + pair * 2 * PBLK;
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                bool need_mask;
+                if (!block_state(sp, qb, need_mask)) continue;
+                f32x16_t pacc = f32x16_t{};
+#pragma unroll
+                for (int kc = 0; kc < DC; ++kc)
+                    pacc = mfma32<T>(ld16(Ds + rofs[kc & 3] + (kc >> 2) * 128 + qb * 32 * 2 * D), kvf[kc], pacc);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int cc = 0; cc < 2; ++cc) {
+                    const u32x4_t pp = ld16(pb + qb * PBLK + cc * 1024 + lane * 16);
+                    float dsv[8];
+#pragma unroll
+                    for (int rg2 = 0; rg2 < 2; ++rg2) {
+                        const int qi = 32 * qb + 8 * (2 * cc + rg2) + 4 * hi;
+                        const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(dls + qi);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int j = 4 * rg2 + e;              // r = 8 cc + j
+                            const float pr = (j & 1) ? hi16<T>(pp[j >> 1]) : lo16<T>(pp[j >> 1]);
+                            dsv[j] = pr * (pacc[8 * cc + j] - d4[e]);
+                        }
+                    }
+                    const u32x4_t bs = u32x4_t{T::pack2(dsv[0], dsv[1]), T::pack2(dsv[2], dsv[3]),
+                                               T::pack2(dsv[4], dsv[5]), T::pack2(dsv[6], dsv[7])};
+#pragma unroll
+                    for (int db = 0; db < DB; ++db)
+                        acc[db] = mfma32<T>(tr_operand<D>(qtb, 2 * qb + cc, db), bs, acc[db]);
+                }
+            }
+        }
+        wait_vmcnt<0>();
+        __syncthreads();
     }
 
-    if (wave_active && key_ok) {
+    if (pair_active && key_ok) {
         const int64_t off = (int64_t)(kr.start + key) * ((int64_t)p.hkv * D) + (int64_t)hk * D;
+        void* dst = role_a ? p.dv : p.dk;
+        const float sc = role_a ? 1.f : p.scale;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
                 const int d = 32 * db + 8 * rg + 4 * hi;
-                store4<T, OUT_F32>(p.dk, off + d, dkacc[db][4 * rg] * p.scale, dkacc[db][4 * rg + 1] * p.scale,
-                                   dkacc[db][4 * rg + 2] * p.scale, dkacc[db][4 * rg + 3] * p.scale);
-                store4<T, OUT_F32>(p.dv, off + d, dvacc[db][4 * rg], dvacc[db][4 * rg + 1],
-                                   dvacc[db][4 * rg + 2], dvacc[db][4 * rg + 3]);
+                store4<T, OUT_F32>(dst, off + d, acc[db][4 * rg] * sc, acc[db][4 * rg + 1] * sc,
+                                   acc[db][4 * rg + 2] * sc, acc[db][4 * rg + 3] * sc);
             }
         }
     }
@@ -593,7 +523,7 @@ BwdKParams make_params(const BwdArgs& a) {
 
 template <typename T, int D, bool OUT_F32>
 hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
-    constexpr int NW = DqCfg<D>::NW;
+    constexpr int NW = kWaves;
     BwdKParams p = make_params(a);
     p.hpw = gcd_int(a.geo.g, NW);
     const int QT = 32 * (NW / p.hpw);
@@ -611,8 +541,8 @@ hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
 template <typename T, int D, bool OUT_F32>
 hipError_t launch_dkv_typed(const BwdArgs& a, hipStream_t st) {
     BwdKParams p = make_params(a);
-    constexpr int NW = DkvCfg<D>::NW;
-    p.n_tiles = (int)(a.geo.total_kv / (NW * kKW)) + a.geo.num_seqs + 1;
+    constexpr int NW = kWaves;
+    p.n_tiles = (int)(a.geo.total_kv / (NW / 2 * kKW)) + a.geo.num_seqs + 1;
     const int64_t blocks = (int64_t)p.n_tiles * a.geo.hkv;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (a.geo.bias != nullptr)
