@@ -50,13 +50,6 @@ struct BwdKParams {
     int causal, window;
 };
 
-__device__ inline bool allowed(int qrow, int key, int coff, int kv_len, int causal, int window) {
-    bool ok = key < kv_len;
-    if (causal) ok = ok && key <= qrow + coff;
-    if (window > 0) ok = ok && key > qrow + coff - window;
-    return ok;
-}
-
 template <typename T, bool OUT_F32>
 __device__ inline void store4(void* base, int64_t off, float a, float b, float c, float d) {
     if (OUT_F32) {
@@ -106,6 +99,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     const int wq_last = min(q_len, qa + 32) - 1;
     const int qrow = qa + l32;
     const bool row_ok = qrow < q_len;
+    const Band band = key_band(qrow, coff, kv_len, p.causal, p.window);
     // rows past the sequence end read its last row (finite, never stored)
     const int64_t grow = qr.start + min(qrow, q_len - 1);
 
@@ -146,10 +140,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         stage_tile<D, kKT, kWaves>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
     };
 
-    uint32_t kofs[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) kofs[c] = tile_offset<D>(l32, 2 * c + hi);
-    const uint32_t trb[2] = {tr_base<D>(lane, 0), tr_base<D>(lane, 1)};
+    const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
     const float c2 = p.scale_log2;
 
     f32x16_t dqacc[DB];
@@ -163,41 +154,55 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         __syncthreads();
         if (it + 2 < n_kv_tiles) stage(it + 2);
         const int kt = kv_lo + it * kKT;
+        // tiles outside this wave's band are computed fully masked, not
+        // skipped (a branch around the MFMAs costs accumulator copies)
         bool skip = !wave_active;
         if (p.causal && kt > wq_last + coff) skip = true;
         if (p.window > 0 && kt + kKT - 1 < qa + coff - p.window + 1) skip = true;
-        if (skip) continue;
         const char* Ks = smem + (it % NBUF) * STAGE;
-        const char* Vs = Ks + TILE;
-        const char* const ktb[2] = {opaque(Ks + trb[0]), opaque(Ks + trb[1])};
-        const bool need_mask = (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
+        const char* krb = opaque(Ks + rbase);
+        const char* ktb = opaque(Ks + tbase);
+        const bool need_mask = skip || (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
                                (p.window > 0 && kt < wq_last + coff - p.window + 1);
+        const int d0 = kt + 4 * hi - band.lo;
+        const uint32_t wdt = skip ? 0u : band.width;
         // two independent 32-key halves: P = exp2(S - lse) needs no running max
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
+            // fresh bases per half: the XORed addresses are rebuilt, not kept live
+            const char* krh = opaque(krb);
+            const char* kth = opaque(ktb);
             f32x16_t sacc = f32x16_t{}, pacc = f32x16_t{};
 #pragma unroll
             for (int kc = 0; kc < DC; ++kc) {
-                const uint32_t o = kofs[kc & 3] + (kc >> 2) * 128 + kb * 32 * 2 * D;
-                sacc = mfma32<T>(ld16(Ks + o), qf[kc], sacc);
-                pacc = mfma32<T>(ld16(Vs + o), df[kc], pacc);
+                const char* a = lds_xor(krh, 32 * kc) + kb * 32 * 2 * D;
+                sacc = mfma32<T>(ld16(a), qf[kc], sacc);
+                pacc = mfma32<T>(ld16(a + TILE), df[kc], pacc);
             }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
-                const bool ok = !need_mask || allowed(qrow, key, coff, kv_len, p.causal, p.window);
-                float x = sacc[r] * c2;
-                if (BIAS && ok && brow != nullptr && key < p.bias_cols) x = fmaf(brow[key], kLog2e, x);
-                const float pr = ok ? __builtin_amdgcn_exp2f(x - lse2) : 0.f;
-                sacc[r] = pr * (pacc[r] - dlt);        // dS^T
+                const int c = 32 * kb + 8 * (r >> 2) + (r & 3);     // key - (kt + 4 hi)
+                float x = fmaf(sacc[r], c2, -lse2);
+                if (BIAS && brow != nullptr && kt + 4 * hi + c < p.bias_cols)
+                    x = fmaf(brow[kt + 4 * hi + c], kLog2e, x);
+                sacc[r] = x;
             }
+            if (need_mask) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
+                    sacc[r] = (uint32_t)(d0 + c) < wdt ? sacc[r] : kNegInf;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[r] = __builtin_amdgcn_exp2f(sacc[r]) * (pacc[r] - dlt);   // dS^T
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 const int c = 2 * kb + cc, r0 = 8 * cc;
                 const u32x4_t bs = u32x4_t{T::pack2(sacc[r0 + 0], sacc[r0 + 1]), T::pack2(sacc[r0 + 2], sacc[r0 + 3]),
                                            T::pack2(sacc[r0 + 4], sacc[r0 + 5]), T::pack2(sacc[r0 + 6], sacc[r0 + 7])};
 #pragma unroll
-                for (int db = 0; db < DB; ++db) dqacc[db] = mfma32<T>(tr_operand<D>(ktb, c, db), bs, dqacc[db]);
+                for (int db = 0; db < DB; ++db) dqacc[db] = mfma32<T>(tr_operand<D>(kth, c, db), bs, dqacc[db]);
             }
         }
     }
@@ -302,10 +307,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         }
     };
 
-    uint32_t rofs[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) rofs[c] = tile_offset<D>(l32, 2 * c + hi);
-    const uint32_t trb[2] = {tr_base<D>(lane, 0), tr_base<D>(lane, 1)};
+    const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
     const float c2 = p.scale_log2;
 
     f32x16_t acc[DB];                            // dV^T (wave A) or dK^T (wave B)
@@ -314,16 +316,17 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 
     // Is the 32x32 block (queries qf0.., this pair's keys) of stage st empty
     // or does it need per-element masking? Identical in both waves of a pair.
-    auto block_state = [&](int st, int qb, bool& need_mask) {
+    // Does the 32x32 block (queries qf0.., this pair's keys) need per-element
+    // masking? Blocks entirely outside the band (nothing to add) are also
+    // "masked": they are computed with P = 0 rather than skipped, because a
+    // branch around the MFMAs costs accumulator copies.
+    auto block_needs_mask = [&](int st, int qb) {
         const int qf0 = q_lo + (st % n_q_tiles) * kQT + 32 * qb;
         const int qf1 = min(q_len, qf0 + 32) - 1;
-        bool skip = !pair_active || qf0 >= q_len;
-        if (p.causal && kw > qf1 + coff) skip = true;
-        if (p.window > 0 && wk_last < qf0 + coff - p.window + 1) skip = true;
-        need_mask = (kw + kKW > kv_len) || (qf0 + 32 > q_len) || (p.causal && wk_last > qf0 + coff) ||
-                    (p.window > 0 && kw < qf1 + coff - p.window + 1);
-        return !skip;
+        return (kw + kKW > kv_len) || (qf0 + 32 > q_len) || (p.causal && wk_last > qf0 + coff) ||
+               (p.window > 0 && kw < qf1 + coff - p.window + 1);
     };
+    const Band band = query_band(key, coff, q_len, kv_len, p.causal, p.window);
 
     if (n_stages > 0) {
         stage(0);
@@ -336,18 +339,19 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             const char* Qs = smem + (st % NBUF) * STAGE;
             const char* Ds = Qs + TILE;
             const float* ls = reinterpret_cast<const float*>(Qs + 2 * TILE);
-            const char* const dtb[2] = {opaque(Ds + trb[0]), opaque(Ds + trb[1])};
+            const char* qrb = opaque(Qs + rbase);
+            const char* dtb = opaque(Ds + tbase);
             char* pb = smem + NBUF * STAGE + (st & 1) * PSTAGE + pair * 2 * PBLK;
             const int h = hk * p.g + st / n_q_tiles;
             const int qt = q_lo + (st % n_q_tiles) * kQT;
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
-                bool need_mask;
-                if (!block_state(st, qb, need_mask)) continue;
+                const bool need_mask = block_needs_mask(st, qb);
+                const int d0 = qt + 32 * qb + 4 * hi - band.lo;       // query - band.lo at r = 0
                 f32x16_t sacc = f32x16_t{};
 #pragma unroll
                 for (int kc = 0; kc < DC; ++kc)
-                    sacc = mfma32<T>(ld16(Qs + rofs[kc & 3] + (kc >> 2) * 128 + qb * 32 * 2 * D), kvf[kc], sacc);
+                    sacc = mfma32<T>(row_operand<D>(qrb, kc, 32 * qb), kvf[kc], sacc);
                 __builtin_amdgcn_sched_barrier(0);
                 const float* brow0 = nullptr;
                 if (BIAS) brow0 = p.bias + (int64_t)h * p.bias_hs + key;
@@ -358,15 +362,16 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int r = 4 * rg + e;
-                        const int qrow = qt + qi + e;
-                        const bool ok = !need_mask ||
-                                        (qrow < q_len && allowed(qrow, key, coff, kv_len, p.causal, p.window));
                         float x = sacc[r] * c2;
-                        if (BIAS && ok && key < p.bias_cols)
-                            x = fmaf(brow0[(int64_t)(qr.start + qrow) * p.bias_qs], kLog2e, x);
+                        if (BIAS) {
+                            const int qrow = min(qt + qi + e, q_len - 1);
+                            if (key < p.bias_cols) x = fmaf(brow0[(int64_t)(qr.start + qrow) * p.bias_qs], kLog2e, x);
+                        }
+                        float arg = fmaf(l4[e], -kLog2e, x);
                         // rows whose every logit is -inf (bias) have lse = -inf: P = 0
-                        const bool live = ok && (!BIAS || x != kNegInf);
-                        sacc[r] = live ? __builtin_amdgcn_exp2f(x - l4[e] * kLog2e) : 0.f;
+                        if (BIAS) arg = x == kNegInf ? kNegInf : arg;
+                        if (need_mask) arg = (uint32_t)(d0 + 8 * rg + e) < band.width ? arg : kNegInf;
+                        sacc[r] = __builtin_amdgcn_exp2f(arg);
                     }
                 }
 #pragma unroll
@@ -386,16 +391,15 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             const char* Qs = smem + (sp % NBUF) * STAGE;
             const char* Ds = Qs + TILE;
             const float* dls = reinterpret_cast<const float*>(Qs + 2 * TILE) + kQT;
-            const char* const qtb[2] = {opaque(Qs + trb[0]), opaque(Qs + trb[1])};
+            const char* drb = opaque(Ds + rbase);
+            const char* qtb = opaque(Qs + tbase);
             const char* pb = smem + NBUF * STAGE + (sp & 1) * PSTAGE + pair * 2 * PBLK;
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
-                bool need_mask;
-                if (!block_state(sp, qb, need_mask)) continue;
                 f32x16_t pacc = f32x16_t{};
 #pragma unroll
                 for (int kc = 0; kc < DC; ++kc)
-                    pacc = mfma32<T>(ld16(Ds + rofs[kc & 3] + (kc >> 2) * 128 + qb * 32 * 2 * D), kvf[kc], pacc);
+                    pacc = mfma32<T>(row_operand<D>(drb, kc, 32 * qb), kvf[kc], pacc);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {

@@ -131,43 +131,6 @@ __device__ inline void transpose4x8(const u32x4_t r[4], u32x2_t out[8]) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// LDS layouts.
-// Row-major tile [rows][D] of 16-bit values, 16-byte chunks XOR-swizzled by
-// (row & 7): a 32-lane MFMA operand read (32 rows, one chunk) and a coalesced
-// 16-lane row write are both bank-conflict free.
-// ---------------------------------------------------------------------------
-template <int D>
-__device__ inline uint32_t rm_offset(int row, int chunk) {   // bytes
-    return (uint32_t)(row * (2 * D) + ((chunk ^ (row & 7)) << 4));
-}
-
-// Transposed tile [D][64] (64 columns of 16-bit, 128 B per row), 8-byte groups
-// of 4 columns XOR-swizzled by f(row) = (row & 15) ^ ((row >> 4) & 7): the
-// MFMA operand read (32 consecutive rows, one group) and the transposing write
-// (16 rows 8 apart, one group) are both conflict free.
-__device__ inline uint32_t tr_offset(int row, int group) {   // bytes
-    const int f = (row & 15) ^ ((row >> 4) & 7);
-    return (uint32_t)(row * 128 + ((group ^ f) << 3));
-}
-
-// Transposed tile [rows][64] in 16-byte units: unit U = 2c + h of a row holds
-// columns {16c + 4h + 0..3, 16c + 8 + 4h + 0..3}, exactly the eight k-slots
-// that lane half h feeds to a 32x32x16 MFMA operand for k-chunk c, so an
-// operand is one 16-byte LDS read. Units are XOR-swizzled by
-// (row ^ (row >> 3)) & 7: operand reads (32 consecutive rows, one unit) are
-// conflict free, transposing writes (16 rows 8 apart) at most 2-way.
-__device__ inline int tr_swz(int row) { return (row ^ (row >> 3)) & 7; }
-// write offset of 4 consecutive columns 4*g4 .. 4*g4+3 (g4 = 0..15)
-__device__ inline uint32_t tr_store_offset(int row, int g4) {
-    const int c = g4 >> 2, gl = g4 & 3;
-    return (uint32_t)(row * 128 + (((2 * c + (gl & 1)) ^ tr_swz(row)) << 4) + ((gl >> 1) << 3));
-}
-// read offset of the operand unit for k-chunk c (0..3), lane half h
-__device__ inline uint32_t tr_load_offset(int row, int c, int h) {
-    return (uint32_t)(row * 128 + (((2 * c + h) ^ tr_swz(row)) << 4));
-}
-
 // Sum of two packed 16-bit values, accumulated in fp32 (v_dot2 with 1.0).
 template <typename T> __device__ inline float dot2_ones(uint32_t w, float acc);
 template <> __device__ inline float dot2_ones<BF16>(uint32_t w, float acc) {
@@ -194,18 +157,31 @@ __device__ inline float pair_sum(float x) {
 // ---------------------------------------------------------------------------
 // Direct HBM -> LDS staging and transposed operand reads (gfx950).
 //
-// Row-major tile [rows][D] of 16-bit values with 16-byte chunks XOR-swizzled
-// by s(row) = ((row & 3) << 1) | ((row >> 2) & 1). Conflict free for
-//  * ds_read_b128 operand reads: 8 consecutive rows, one chunk;
-//  * ds_read_b64_tr_b16 transposed reads: 4 rows {4a..4a+3}, two adjacent
-//    chunks {2b, 2b+1} (see tr_operand);
-//  * global_load_lds_dwordx4 writes: 1 KB contiguous per instruction.
+// The gfx950 LDS serves 256 bytes per clock from 64 four-byte banks: a
+// ds_read_b128 is served 16 lanes at a time, a ds_read_b64(_tr_b16) 32 lanes
+// at a time, and an access is conflict free when those lanes hit 16 (resp.
+// 32) distinct bank groups. A row-major tile [rows][D] of 16-bit values keeps
+// its 16-byte chunks XOR-swizzled per row so that both operand patterns are:
+//  * row reads (ds_read_b128, MFMA operand rows): 16 consecutive rows, one
+//    chunk -> the swizzle must be a bijection on 16 consecutive rows;
+//  * transposed reads (ds_read_b64_tr_b16, see tr_operand): 4 rows
+//    {4a..4a+3} x 4 chunks {4p..4p+3} -> the swizzle's chunk bits 2-3 must
+//    separate rows 4a..4a+3.
+// D = 128 (one row = 256 B = all banks): s(row) = (row & 3) << 2 | (row >> 2) & 3.
+// D = 64 (two rows per 256 B, the odd row in the upper half):
+//   s(row) = ((row >> 1) & 1) << 2 | (row >> 2) & 3.
+// Direct-load writes (global_load_lds_dwordx4) are 1 KB contiguous per
+// instruction and conflict free under any swizzle.
 // ---------------------------------------------------------------------------
-__device__ inline int row_swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+template <int D>
+__device__ inline int row_swz(int row) {
+    static_assert(D == 64 || D == 128, "swizzled tiles are defined for D = 64 and 128");
+    return D == 128 ? (((row & 3) << 2) | ((row >> 2) & 3)) : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
+}
 
 template <int D>
 __device__ inline uint32_t tile_offset(int row, int chunk) {   // bytes
-    return (uint32_t)(row * (2 * D) + ((chunk ^ row_swz(row)) << 4));
+    return (uint32_t)(row * (2 * D) + ((chunk ^ row_swz<D>(row)) << 4));
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -227,7 +203,7 @@ __device__ inline void stage_tile(char* tile, const uint16_t* base, int64_t rs, 
     for (int i = w; i < PER; i += NW) {
         const int byte = i * 1024 + lane * 16;
         const int row = byte / (2 * D);
-        const int chunk = ((byte % (2 * D)) >> 4) ^ row_swz(row);
+        const int chunk = ((byte % (2 * D)) >> 4) ^ row_swz<D>(row);
         const int grow = min(row0 + row, row_end - 1);
         __builtin_amdgcn_global_load_lds(base + (int64_t)grow * rs + chunk * 8, (lds_void_t*)(tile + i * 1024), 16,
                                          0, 0);
@@ -242,46 +218,83 @@ __device__ inline void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8));
 }
 
-// 32x32x16 MFMA operand whose M index runs along the D columns of a
-// row-major tile and whose K index runs along its rows: M = columns
-// dcol0 .. dcol0 + 31, K slots j of lane half h = rows
-// krow0 + 8 (j / 4) + 4 h + j % 4 (krow0 a multiple of 16, dcol0 of 32). Two
-// ds_read_b64_tr_b16: in each 16-lane group, lane 4e + q addresses row e of
-// the group's 4 rows at columns 4q .. 4q + 3, and lane i receives column i of
-// all 4 rows.
-//
-// The swizzle of rows krow0 + 4h + e depends only on (e, h), and dcol0 only
-// flips chunk bit 2 (dcol0 / 32 odd) or adds whole 128-byte groups, so every
-// address is one of two per-lane bases (tr_base(lane, parity)) plus
-// compile-time offsets: krow0 * 2D + (dcol0 / 64) * 128.
-template <int D>
-__device__ inline uint32_t tr_base(int lane, int parity) {
-    const int g = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
-    const int col = 32 * parity + 16 * (g & 1) + 4 * q;
-    const int row = 4 * (g >> 1) + e;
-    return tile_offset<D>(row, col >> 3) + (col & 7) * 2;
-}
 // Keeps a per-iteration address opaque to the optimiser, so constant offsets
-// fold into the LDS instructions' offset fields instead of being hoisted
-// out of the loop as extra live registers.
+// fold into the LDS instructions' offset fields and per-lane XOR variants are
+// formed per use instead of being hoisted out of the loop as live registers.
 __device__ inline const char* opaque(const char* p) {
     uint32_t v = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
     asm volatile("" : "+v"(v));
     return (const char*)(const __attribute__((address_space(3))) char*)(uintptr_t)v;
 }
+// p ^ x on an LDS address (x < 256; tiles start on 256-byte boundaries, so
+// this XORs the within-row byte offset).
+__device__ inline const char* lds_xor(const char* p, uint32_t x) {
+    const uint32_t v = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+    return (const char*)(const __attribute__((address_space(3))) char*)(uintptr_t)(v ^ x);
+}
 
+// Row operand reads. Lane (l32, hi) of a 32x32x16 MFMA operand reads row
+// l32 (+ any multiple of 16 rows) at chunk 2 kc + hi. Since 2 kc + hi =
+// 2 kc ^ hi and the swizzle is an XOR, chunk 2 kc + hi of row l32 sits at
+// row_base ^ (32 kc): one per-lane base per tile, one v_xor per k-chunk.
 template <int D>
-__device__ inline u32x4_t tr_operand_at(const char* p) {
-    const v4i16_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p);
-    const v4i16_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p + 8 * 2 * D));
+__device__ inline uint32_t row_base(int l32, int hi) { return tile_offset<D>(l32, hi); }
+template <int D>
+__device__ inline u32x4_t row_operand(const char* rb, int kc, int row_off) {
+    return ld16(lds_xor(rb, 32 * kc) + row_off * 2 * D);
+}
+
+// 32x32x16 MFMA operand whose M index runs along the D columns of a
+// row-major tile and whose K index runs along its rows: M = columns
+// 32 db .. 32 db + 31, K slots j of lane half h = rows
+// 16 c + 8 (j / 4) + 4 h + j % 4. Two ds_read_b64_tr_b16 (K slots 0-3, then
+// 4-7 eight rows down): in each 16-lane group, lane 4e + q addresses row e
+// of the group's 4 rows at columns 4q .. 4q + 3, and lane i receives column
+// i of all 4 rows.
+//
+// Addresses: the swizzle depends on row & 15 only, so 16 c rows are a plain
+// offset; column block db XORs swizzled chunk bits 2-3 (byte 64 db) and the
+// second read (+8 rows) XORs chunk bit 1 (byte 32), so every read is
+// tr_base ^ const + const.
+template <int D>
+__device__ inline uint32_t tr_base(int lane) {
+    const int g = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
+    const int col = 16 * (g & 1) + 4 * q;
+    const int row = 4 * (g >> 1) + e;
+    return tile_offset<D>(row, col >> 3) + (col & 7) * 2;
+}
+template <int D>
+__device__ inline u32x4_t tr_operand(const char* tb, int c, int db) {
+    const char* p0 = lds_xor(tb, 64 * db) + c * 16 * 2 * D;
+    const char* p1 = lds_xor(tb, 64 * db + 32) + (c * 16 + 8) * 2 * D;
+    const v4i16_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p0);
+    const v4i16_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p1);
     const u32x2_t a2 = __builtin_bit_cast(u32x2_t, a), b2 = __builtin_bit_cast(u32x2_t, b);
     return u32x4_t{a2[0], a2[1], b2[0], b2[1]};
 }
-// operand for (krow0 = 16 c, dcol0 = 32 db) given the two lane bases
-// tb[p] = opaque(tile + tr_base(lane, p))
-template <int D>
-__device__ inline u32x4_t tr_operand(const char* const tb[2], int c, int db) {
-    return tr_operand_at<D>(tb[db & 1] + c * 16 * 2 * D + (db >> 1) * 128);
+
+// ---------------------------------------------------------------------------
+// Mask bands. With end-aligned causal masking (coff = kv_len - q_len) and a
+// sliding window W, query i may attend key j iff
+//   j < kv_len, (!causal || j <= i + coff), (W <= 0 || j > i + coff - W).
+// For one query row the allowed keys form [lo, lo + width); for one key the
+// allowed queries (also < q_len) form an interval too. A test is then one
+// unsigned compare: (unsigned)(k - lo) < width.
+// ---------------------------------------------------------------------------
+struct Band {
+    int lo;
+    uint32_t width;
+    __device__ inline bool has(int k) const { return (uint32_t)(k - lo) < width; }
+};
+__device__ inline Band key_band(int qrow, int coff, int kv_len, int causal, int window) {
+    const int lo = window > 0 ? max(0, qrow + coff - window + 1) : 0;
+    const int hi = causal ? min(kv_len, qrow + coff + 1) : kv_len;
+    return Band{lo, (uint32_t)max(0, hi - lo)};
+}
+__device__ inline Band query_band(int key, int coff, int q_len, int kv_len, int causal, int window) {
+    const int lo = causal ? max(0, key - coff) : 0;
+    const int hi = key >= kv_len ? lo : (window > 0 ? min(q_len, key - coff + window) : q_len);
+    return Band{lo, (uint32_t)max(0, hi - lo)};
 }
 
 // ---------------------------------------------------------------------------

@@ -112,12 +112,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         stage_tile<D, kKT, kWaves>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
     };
 
-    // K operand rows 32 kb + l32, chunk 2 kc + hi (hoisted per-lane offsets):
-    // the swizzle touches the low 3 chunk bits only, so kc >= 4 adds 128 B.
-    uint32_t kofs[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) kofs[c] = tile_offset<D>(l32, 2 * c + hi);
-    const uint32_t trb[2] = {tr_base<D>(lane, 0), tr_base<D>(lane, 1)};
+    // per-lane LDS offsets: K operand rows 32 kb + l32 (chunk 2 kc + hi) and
+    // the transposed V^T operand reads
+    const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
 
     float m_run = kNegInf, l_run = 0.f;
     f32x16_t oacc[DB];
@@ -125,6 +122,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     for (int db = 0; db < DB; ++db) oacc[db] = f32x16_t{};
 
     const int qrow = qa + l32;
+    const Band band = key_band(qrow, coff, kv_len, p.causal, p.window);
     const float* brow = nullptr;
     if (BIAS && p.bias != nullptr && qrow < q_len)
         brow = p.bias + (int64_t)(qr.start + qrow) * p.bias_qs + (int64_t)head * p.bias_hs;
@@ -144,36 +142,38 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         if (it + 2 < n_kv_tiles) stage(it + 2);
         const int kt = kv_lo + it * kKT;
 
+        // A tile outside this wave's band is computed fully masked (P = 0)
+        // rather than skipped: a branch around the MFMAs makes the compiler
+        // copy the 64 O accumulator registers twice per tile.
         bool skip = !wave_active;
         if (p.causal && kt > wq_last + coff) skip = true;
         if (p.window > 0 && kt + kKT - 1 < qa + coff - p.window + 1) skip = true;
-        if (skip) continue;
         const char* Ks = smem + (it % NBUF) * STAGE;
-        const char* const vtb[2] = {opaque(Ks + TILE + trb[0]), opaque(Ks + TILE + trb[1])};
+        const char* kb_ = opaque(Ks + rbase);
+        const char* vtb = opaque(Ks + TILE + tbase);
         f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
 #pragma unroll
         for (int kc = 0; kc < DC; ++kc) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                const u32x4_t a = ld16(Ks + kofs[kc & 3] + (kc >> 2) * 128 + kb * 32 * 2 * D);
+                const u32x4_t a = row_operand<D>(kb_, kc, 32 * kb);
                 sacc[kb] = mfma32<T>(a, qf[kc], sacc[kb]);
             }
         }
         // keep the V^T reads of the P.V phase from being hoisted above the
         // softmax (they would pin 64 registers across it)
         __builtin_amdgcn_sched_barrier(0);
-        const bool need_mask = (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
+        const bool need_mask = skip || (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
                                (p.window > 0 && kt < wq_last + coff - p.window + 1);
         if (need_mask) {
+            const int d0 = kt + 4 * hi - band.lo;
+            const uint32_t wdt = skip ? 0u : band.width;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
-                    bool ok = key < kv_len;
-                    if (p.causal) ok = ok && key <= qrow + coff;
-                    if (p.window > 0) ok = ok && key > qrow + coff - p.window;
-                    if (!ok) sacc[kb][r] = kNegInf;
+                    const int c = 32 * kb + 8 * (r >> 2) + (r & 3);    // key - (kt + 4 hi)
+                    sacc[kb][r] = (uint32_t)(d0 + c) < wdt ? sacc[kb][r] : kNegInf;
                 }
             }
         }
