@@ -285,17 +285,24 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 
     // Query range that can see any key of this workgroup.
     const int k_last_wg = min(kv_len, k0 + KB) - 1;
-    const int q_lo = p.causal ? max(0, k0 - coff) : 0;
+    // (tile grid aligned to kQT so workgroups of a sequence share tiles)
+    const int q_lo = p.causal ? max(0, k0 - coff) / kQT * kQT : 0;
     const int q_hi = p.window > 0 ? min(q_len, k_last_wg - coff + p.window) : q_len;
     const int n_q_tiles = q_hi > q_lo ? (q_hi - q_lo + kQT - 1) / kQT : 0;
     const int n_stages = n_q_tiles * p.g;
 
+    // Stage st covers query tile (n_q_tiles - 1 - st / g) of head hk g + st % g:
+    // tiles run top-down with the heads inner, so every workgroup of a
+    // sequence reads the same (tile, head) at the same time and the L2 serves
+    // the repeats (each workgroup stops at its own causal start q_lo).
+    auto stage_head = [&](int st) { return hk * p.g + st % p.g; };
+    auto stage_q0 = [&](int st) { return q_lo + (n_q_tiles - 1 - st / p.g) * kQT; };
     // Direct loads of stage `st`: Q and dO tiles by all waves, lse by wave 0,
     // delta by wave 1 (4 bytes per lane, lane l -> row l).
     auto stage = [&](int st) {
         char* buf = smem + (st % NBUF) * STAGE;
-        const int h = hk * p.g + st / n_q_tiles;
-        const int qt = q_lo + (st % n_q_tiles) * kQT;
+        const int h = stage_head(st);
+        const int qt = stage_q0(st);
         const int64_t hoff = (int64_t)qr.start * p.q_rs + (int64_t)h * D;
         stage_tile<D, kQT, kWaves>(buf, p.q + hoff, p.q_rs, qt, q_len, w, lane);
         stage_tile<D, kQT, kWaves>(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * D, p.do_rs, qt,
@@ -321,7 +328,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     // "masked": they are computed with P = 0 rather than skipped, because a
     // branch around the MFMAs costs accumulator copies.
     auto block_needs_mask = [&](int st, int qb) {
-        const int qf0 = q_lo + (st % n_q_tiles) * kQT + 32 * qb;
+        const int qf0 = stage_q0(st) + 32 * qb;
         const int qf1 = min(q_len, qf0 + 32) - 1;
         return (kw + kKW > kv_len) || (qf0 + 32 > q_len) || (p.causal && wk_last > qf0 + coff) ||
                (p.window > 0 && kw < qf1 + coff - p.window + 1);
@@ -331,6 +338,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     if (n_stages > 0) {
         stage(0);
         wait_vmcnt<0>();
+        if (w == 0) reinterpret_cast<float*>(smem + 2 * TILE)[lane] *= -kLog2e;
         __syncthreads();
     }
     for (int st = 0; n_stages > 0 && st <= n_stages; ++st) {
@@ -338,21 +346,23 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         if (role_a && st < n_stages) {
             const char* Qs = smem + (st % NBUF) * STAGE;
             const char* Ds = Qs + TILE;
-            const float* ls = reinterpret_cast<const float*>(Qs + 2 * TILE);
+            const float* ls = reinterpret_cast<const float*>(Qs + 2 * TILE);   // -lse log2(e)
             const char* qrb = opaque(Qs + rbase);
             const char* dtb = opaque(Ds + tbase);
             char* pb = smem + NBUF * STAGE + (st & 1) * PSTAGE + pair * 2 * PBLK;
-            const int h = hk * p.g + st / n_q_tiles;
-            const int qt = q_lo + (st % n_q_tiles) * kQT;
+            const int h = stage_head(st);
+            const int qt = stage_q0(st);
+            // S of both 32-query blocks on the matrix cores; block 0's
+            // exponentials then overlap block 1's MFMAs, and block 1's
+            // exponentials overlap block 0's dV products.
+            f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
+#pragma unroll
+            for (int kc = 0; kc < DC; ++kc)
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb)
+                    sacc[qb] = mfma32<T>(row_operand<D>(qrb, kc, 32 * qb), kvf[kc], sacc[qb]);
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
-                const bool need_mask = block_needs_mask(st, qb);
-                const int d0 = qt + 32 * qb + 4 * hi - band.lo;       // query - band.lo at r = 0
-                f32x16_t sacc = f32x16_t{};
-#pragma unroll
-                for (int kc = 0; kc < DC; ++kc)
-                    sacc = mfma32<T>(row_operand<D>(qrb, kc, 32 * qb), kvf[kc], sacc);
-                __builtin_amdgcn_sched_barrier(0);
                 const float* brow0 = nullptr;
                 if (BIAS) brow0 = p.bias + (int64_t)h * p.bias_hs + key;
 #pragma unroll
@@ -362,23 +372,33 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int r = 4 * rg + e;
-                        float x = sacc[r] * c2;
+                        float arg;
                         if (BIAS) {
+                            float x = sacc[qb][r] * c2;
                             const int qrow = min(qt + qi + e, q_len - 1);
                             if (key < p.bias_cols) x = fmaf(brow0[(int64_t)(qr.start + qrow) * p.bias_qs], kLog2e, x);
+                            // rows whose every logit is -inf (bias) have lse = -inf: P = 0
+                            arg = x == kNegInf ? kNegInf : x + l4[e];
+                        } else {
+                            arg = fmaf(sacc[qb][r], c2, l4[e]);
                         }
-                        float arg = fmaf(l4[e], -kLog2e, x);
-                        // rows whose every logit is -inf (bias) have lse = -inf: P = 0
-                        if (BIAS) arg = x == kNegInf ? kNegInf : arg;
-                        if (need_mask) arg = (uint32_t)(d0 + 8 * rg + e) < band.width ? arg : kNegInf;
-                        sacc[r] = __builtin_amdgcn_exp2f(arg);
+                        sacc[qb][r] = __builtin_amdgcn_exp2f(arg);
                     }
+                }
+                // out-of-band elements (and rows with no allowed key) -> P = 0
+                if (block_needs_mask(st, qb)) {
+                    const int d0 = qt + 32 * qb + 4 * hi - band.lo;   // query - band.lo at r = 0
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        sacc[qb][r] = (uint32_t)(d0 + 8 * (r >> 2) + (r & 3)) < band.width ? sacc[qb][r] : 0.f;
                 }
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {
                     const int r0 = 8 * cc;
-                    const u32x4_t bp = u32x4_t{T::pack2(sacc[r0 + 0], sacc[r0 + 1]), T::pack2(sacc[r0 + 2], sacc[r0 + 3]),
-                                               T::pack2(sacc[r0 + 4], sacc[r0 + 5]), T::pack2(sacc[r0 + 6], sacc[r0 + 7])};
+                    const u32x4_t bp = u32x4_t{T::pack2(sacc[qb][r0 + 0], sacc[qb][r0 + 1]),
+                                               T::pack2(sacc[qb][r0 + 2], sacc[qb][r0 + 3]),
+                                               T::pack2(sacc[qb][r0 + 4], sacc[qb][r0 + 5]),
+                                               T::pack2(sacc[qb][r0 + 6], sacc[qb][r0 + 7])};
                     st16(pb + qb * PBLK + cc * 1024 + lane * 16, bp);
 #pragma unroll
                     for (int db = 0; db < DB; ++db)
@@ -394,13 +414,15 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             const char* drb = opaque(Ds + rbase);
             const char* qtb = opaque(Qs + tbase);
             const char* pb = smem + NBUF * STAGE + (sp & 1) * PSTAGE + pair * 2 * PBLK;
+            // dP of both blocks first; block 0's dS overlaps block 1's MFMAs
+            f32x16_t pacc[2] = {f32x16_t{}, f32x16_t{}};
+#pragma unroll
+            for (int kc = 0; kc < DC; ++kc)
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb)
+                    pacc[qb] = mfma32<T>(row_operand<D>(drb, kc, 32 * qb), kvf[kc], pacc[qb]);
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
-                f32x16_t pacc = f32x16_t{};
-#pragma unroll
-                for (int kc = 0; kc < DC; ++kc)
-                    pacc = mfma32<T>(row_operand<D>(drb, kc, 32 * qb), kvf[kc], pacc);
-                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {
                     const u32x4_t pp = ld16(pb + qb * PBLK + cc * 1024 + lane * 16);
@@ -413,7 +435,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                         for (int e = 0; e < 4; ++e) {
                             const int j = 4 * rg2 + e;              // r = 8 cc + j
                             const float pr = (j & 1) ? hi16<T>(pp[j >> 1]) : lo16<T>(pp[j >> 1]);
-                            dsv[j] = pr * (pacc[8 * cc + j] - d4[e]);
+                            dsv[j] = pr * (pacc[qb][8 * cc + j] - d4[e]);
                         }
                     }
                     const u32x4_t bs = u32x4_t{T::pack2(dsv[0], dsv[1]), T::pack2(dsv[2], dsv[3]),
@@ -424,7 +446,13 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                 }
             }
         }
+        // stage st + 1 landed for this wave; wave 0 pre-scales its lse column
+        // (-lse log2 e) before the barrier publishes the stage
         wait_vmcnt<0>();
+        if (w == 0 && st + 1 < n_stages) {
+            float* l = reinterpret_cast<float*>(smem + ((st + 1) % NBUF) * STAGE + 2 * TILE);
+            l[lane] *= -kLog2e;
+        }
         __syncthreads();
     }
 
