@@ -166,43 +166,47 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
                                (p.window > 0 && kt < wq_last + coff - p.window + 1);
         const int d0 = kt + 4 * hi - band.lo;
         const uint32_t wdt = skip ? 0u : band.width;
-        // two independent 32-key halves: P = exp2(S - lse) needs no running max
+        // S^T and dP^T of both 32-key halves on the matrix cores first; half
+        // 0's elementwise work overlaps half 1's MFMAs, half 1's overlaps
+        // half 0's dQ products. P = exp2(S - lse) needs no running max.
+        f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}}, pacc[2] = {f32x16_t{}, f32x16_t{}};
+#pragma unroll
+        for (int kc = 0; kc < DC; ++kc) {
+            const char* a = lds_xor(krb, 32 * kc);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                sacc[kb] = mfma32<T>(ld16(a + kb * 32 * 2 * D), qf[kc], sacc[kb]);
+                pacc[kb] = mfma32<T>(ld16(a + kb * 32 * 2 * D + TILE), df[kc], pacc[kb]);
+            }
+        }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-            // fresh bases per half: the XORed addresses are rebuilt, not kept live
-            const char* krh = opaque(krb);
-            const char* kth = opaque(ktb);
-            f32x16_t sacc = f32x16_t{}, pacc = f32x16_t{};
-#pragma unroll
-            for (int kc = 0; kc < DC; ++kc) {
-                const char* a = lds_xor(krh, 32 * kc) + kb * 32 * 2 * D;
-                sacc = mfma32<T>(ld16(a), qf[kc], sacc);
-                pacc = mfma32<T>(ld16(a + TILE), df[kc], pacc);
-            }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int c = 32 * kb + 8 * (r >> 2) + (r & 3);     // key - (kt + 4 hi)
-                float x = fmaf(sacc[r], c2, -lse2);
+                float x = fmaf(sacc[kb][r], c2, -lse2);
                 if (BIAS && brow != nullptr && kt + 4 * hi + c < p.bias_cols)
                     x = fmaf(brow[kt + 4 * hi + c], kLog2e, x);
-                sacc[r] = x;
+                sacc[kb][r] = __builtin_amdgcn_exp2f(x);
             }
-            if (need_mask) {
+            if (need_mask) {     // out-of-band keys -> P = 0
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
-                    sacc[r] = (uint32_t)(d0 + c) < wdt ? sacc[r] : kNegInf;
+                    sacc[kb][r] = (uint32_t)(d0 + c) < wdt ? sacc[kb][r] : 0.f;
                 }
             }
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[r] = __builtin_amdgcn_exp2f(sacc[r]) * (pacc[r] - dlt);   // dS^T
+            for (int r = 0; r < 16; ++r) sacc[kb][r] *= pacc[kb][r] - dlt;   // dS^T
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 const int c = 2 * kb + cc, r0 = 8 * cc;
-                const u32x4_t bs = u32x4_t{T::pack2(sacc[r0 + 0], sacc[r0 + 1]), T::pack2(sacc[r0 + 2], sacc[r0 + 3]),
-                                           T::pack2(sacc[r0 + 4], sacc[r0 + 5]), T::pack2(sacc[r0 + 6], sacc[r0 + 7])};
+                const u32x4_t bs = u32x4_t{T::pack2(sacc[kb][r0 + 0], sacc[kb][r0 + 1]),
+                                           T::pack2(sacc[kb][r0 + 2], sacc[kb][r0 + 3]),
+                                           T::pack2(sacc[kb][r0 + 4], sacc[kb][r0 + 5]),
+                                           T::pack2(sacc[kb][r0 + 6], sacc[kb][r0 + 7])};
 #pragma unroll
-                for (int db = 0; db < DB; ++db) dqacc[db] = mfma32<T>(tr_operand<D>(kth, c, db), bs, dqacc[db]);
+                for (int db = 0; db < DB; ++db) dqacc[db] = mfma32<T>(tr_operand<D>(ktb, c, db), bs, dqacc[db]);
             }
         }
     }
