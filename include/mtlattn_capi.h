@@ -165,7 +165,9 @@ int mtlattn_bwd_dkv(const mtlattn_problem* p,
  * final LSE when `lse` is non-NULL. num_splits == 1 is a plain forward.
  * Replaces _C.attn_splitkv (src/ext.mm:716-773; kernels
  * src/attn_mpp.metal:384-535). Requires fp16/bf16, D in {64, 128}, no bias,
- * no window, max_seqlen_q * (Hq / Hkv) rows per kv head handled in groups of 16.
+ * no window, max_seqlen_q * (Hq / Hkv) rows per kv head handled in groups of
+ * 16. Workspace: fp32 partial rows of D values plus one LSE each, 16 rows per
+ * (kv head, head group, sequence, split).
  */
 size_t mtlattn_attn_splitkv_workspace_size(const mtlattn_problem* p, int32_t num_splits);
 int mtlattn_attn_splitkv(const mtlattn_problem* p,
@@ -176,8 +178,11 @@ int mtlattn_attn_splitkv(const mtlattn_problem* p,
                          void* workspace, size_t workspace_bytes,
                          void* stream);
 
-/* Split count the forward's decode routing would choose for `p` (0 = the
- * call is not routed to split-KV). Retunes src/ext.mm:372-388 for 256 CUs. */
+/* Number of split-KV work-item slots per (kv head, head group) the forward's
+ * decode routing would use for `p` (0 = the call is not routed to split-KV).
+ * The automatic path cuts each sequence's KV into fixed-length chunks (about
+ * 18 work items per CU) rather than a fixed number of splits per sequence,
+ * so ragged KV lengths stay balanced. Retunes src/ext.mm:372-388. */
 int32_t mtlattn_decode_num_splits(const mtlattn_problem* p);
 
 #ifdef __cplusplus

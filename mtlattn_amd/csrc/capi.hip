@@ -128,29 +128,63 @@ bool splitkv_supported(const mtlattn_problem* p) {
            p->max_seqlen_q >= 1 && p->max_seqlen_q <= 16;
 }
 
-size_t splitkv_bytes(const mtlattn_problem* p, int ns) {
-    const size_t rows = (size_t)p->total_q * (size_t)p->num_heads_q;
-    const size_t o = rows * (size_t)p->head_dim * sizeof(float) * (size_t)ns;
-    const size_t l = rows * sizeof(float) * (size_t)ns;
-    return ((o + 255) & ~(size_t)255) + l;
+// Partial rows of the split-KV workspace for ns equal splits per sequence
+// (chunk == 0) or fixed KV chunks of `chunk` keys.
+int64_t splitkv_rows(const mtlattn_problem* p, int ns, int chunk) {
+    const int g = p->num_heads_q / p->num_heads_kv;
+    const int n_hg = g / decode_heads_per_group(g, p->max_seqlen_q);
+    return decode_workspace_rows(p->total_kv, p->num_seqs, p->num_heads_kv, n_hg, chunk, ns);
+}
+
+size_t splitkv_bytes(const mtlattn_problem* p, int ns, int chunk) {
+    const size_t rows = (size_t)splitkv_rows(p, ns, chunk);
+    const size_t o = rows * (size_t)p->head_dim * sizeof(float);
+    return ((o + 255) & ~(size_t)255) + rows * sizeof(float);
 }
 
 int run_splitkv(const mtlattn_problem* p, const void* q, int64_t qrs, const void* k, int64_t krs, const void* v,
-                int64_t vrs, void* out, float* lse, int ns, void* ws, size_t ws_bytes, hipStream_t st) {
-    if (ws_bytes < splitkv_bytes(p, ns) || (ws == nullptr && splitkv_bytes(p, ns) > 0))
+                int64_t vrs, void* out, float* lse, int ns, int chunk, void* ws, size_t ws_bytes, hipStream_t st) {
+    const size_t need = splitkv_bytes(p, ns, chunk);
+    if (ws_bytes < need || (ws == nullptr && need > 0))
         return fail(MTLATTN_ERR_WORKSPACE, "mtlattn: split-KV workspace too small (%zu < %zu bytes)", ws_bytes,
-                    splitkv_bytes(p, ns));
+                    need);
     DecodeArgs a;
     a.geo = make_geo(p);
     a.q = q; a.q_rs = qrs; a.k = k; a.k_rs = krs; a.v = v; a.v_rs = vrs;
     a.o = out; a.lse = lse;
-    const size_t rows = (size_t)p->total_q * (size_t)p->num_heads_q;
-    const size_t obytes = rows * (size_t)p->head_dim * sizeof(float) * (size_t)ns;
+    const size_t obytes = (size_t)splitkv_rows(p, ns, chunk) * (size_t)p->head_dim * sizeof(float);
     a.o_part = (float*)ws;
     a.lse_part = (float*)((char*)ws + ((obytes + 255) & ~(size_t)255));
     a.num_splits = ns;
+    a.chunk = chunk;
     a.max_q = p->max_seqlen_q;
     return launch_status(launch_decode(p->dtype, a, st), "split-KV decode");
+}
+
+// KV chunk length (keys, a multiple of 32) of the automatic decode path, or
+// 0 when the call is not routed there. Reference gate (src/ext.mm:372-376):
+// few queries, long KV, no bias/window. Chunks are sized so that about 18
+// work items per CU exist (measured on MI355X: fewer leave a ragged last
+// round, more add per-item start-up and partial-row traffic); every wave
+// then streams the same number of bytes whatever the spread of KV lengths.
+constexpr int64_t kItemsPerCu = 18;
+
+int decode_chunk(const mtlattn_problem* p) {
+    if (check_problem(p) != MTLATTN_OK) return 0;
+    if (p->total_q <= 0 || env_set("MTLATTN_NO_SPLITKV") || force_generic() || !splitkv_supported(p)) return 0;
+    const int64_t avg_kv = p->total_kv / (p->num_seqs > 0 ? p->num_seqs : 1);
+    if (avg_kv < 2048) return 0;
+    const int g = p->num_heads_q / p->num_heads_kv;
+    const int64_t groups = (int64_t)p->num_heads_kv * (g / decode_heads_per_group(g, p->max_seqlen_q));
+    int64_t c = (p->total_kv * groups + (int64_t)device_cus() * kItemsPerCu - 1) / ((int64_t)device_cus() * kItemsPerCu);
+    if (const char* e = std::getenv("MTLATTN_DECODE_CHUNK")) {   // tuning override (keys)
+        const long v = std::strtol(e, nullptr, 10);
+        if (v > 0) c = v;
+    }
+    c = (c + 128) / 256 * 256;      // nearest multiple of 256 keys
+    if (c < 256) c = 256;
+    if (c > 8192) c = 8192;
+    return (int)c;
 }
 
 }  // namespace
@@ -171,26 +205,15 @@ int mtlattn_gpu_core_count(int device) {
 }
 
 int32_t mtlattn_decode_num_splits(const mtlattn_problem* p) {
-    if (check_problem(p) != MTLATTN_OK) return 0;
-    // Reference gate (src/ext.mm:372-376): few queries, long KV, no bias/window.
-    if (p->total_q <= 0 || env_set("MTLATTN_NO_SPLITKV") || force_generic() || !splitkv_supported(p)) return 0;
-    const int64_t avg_kv = p->total_kv / (p->num_seqs > 0 ? p->num_seqs : 1);
-    if (avg_kv < 2048) return 0;
-    // Splits: enough waves to fill every CU ~64 deep (waves are independent and
-    // short, so oversubscription balances ragged lengths), but >= 256 keys each.
-    const int g = p->num_heads_q / p->num_heads_kv;
-    const int64_t units = (int64_t)p->num_seqs * p->num_heads_kv * (g / decode_heads_per_group(g, p->max_seqlen_q));
-    int64_t ns = ((int64_t)device_cus() * 64 + units - 1) / units;
-    const int64_t cap = avg_kv / 256 > 1 ? avg_kv / 256 : 1;
-    if (ns > cap) ns = cap;
-    if (ns > 256) ns = 256;
-    if (ns < 1) ns = 1;
-    return (int32_t)ns;
+    const int c = decode_chunk(p);
+    if (c <= 0) return 0;
+    const int64_t slots = p->total_kv / c + p->num_seqs + 1;
+    return slots > 0x7fffffff ? 0x7fffffff : (int32_t)slots;
 }
 
 size_t mtlattn_varlen_fwd_workspace_size(const mtlattn_problem* p) {
-    const int32_t ns = mtlattn_decode_num_splits(p);
-    return ns > 0 ? splitkv_bytes(p, ns) : 0;
+    const int c = decode_chunk(p);
+    return c > 0 ? splitkv_bytes(p, 0, c) : 0;
 }
 
 int mtlattn_varlen_fwd(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
@@ -202,11 +225,11 @@ int mtlattn_varlen_fwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
     if (q == nullptr || out == nullptr || (p->total_kv > 0 && (k == nullptr || v == nullptr)))
         return fail(MTLATTN_ERR_INVALID, "mtlattn: null q/k/v/out pointer");
     hipStream_t st = (hipStream_t)stream;
-    const int32_t ns = mtlattn_decode_num_splits(p);
+    const int chunk = decode_chunk(p);
     const bool vec_ok = aligned16(q, q_row_stride, p->dtype) && aligned16(k, k_row_stride, p->dtype) &&
                         aligned16(v, v_row_stride, p->dtype) && ((uintptr_t)out & 15u) == 0;
-    if (ns > 0 && vec_ok)
-        return run_splitkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, ns, workspace,
+    if (chunk > 0 && vec_ok)
+        return run_splitkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, 0, chunk, workspace,
                            workspace_bytes, st);
     FwdArgs a;
     a.geo = make_geo(p);
@@ -331,7 +354,7 @@ int mtlattn_varlen_bwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
 
 size_t mtlattn_attn_splitkv_workspace_size(const mtlattn_problem* p, int32_t num_splits) {
     if (check_problem(p) != MTLATTN_OK || num_splits < 1) return 0;
-    return splitkv_bytes(p, num_splits);
+    return splitkv_bytes(p, num_splits, 0);
 }
 
 int mtlattn_attn_splitkv(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
@@ -352,7 +375,7 @@ int mtlattn_attn_splitkv(const mtlattn_problem* p, const void* q, int64_t q_row_
     if (!aligned16(q, q_row_stride, p->dtype) || !aligned16(k, k_row_stride, p->dtype) ||
         !aligned16(v, v_row_stride, p->dtype) || ((uintptr_t)out & 15u) != 0)
         return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: q/k/v rows must be 16-byte aligned");
-    return run_splitkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, num_splits, workspace,
+    return run_splitkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, num_splits, 0, workspace,
                        workspace_bytes, (hipStream_t)stream);
 }
 

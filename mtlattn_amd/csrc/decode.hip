@@ -6,15 +6,21 @@
 //     a kv head form the N dimension (16) of v_mfma_f32_16x16x32, so each K/V
 //     row is read once per kv head instead of once per query head (the
 //     reference's grid z = Hq re-reads it g times, src/ext.mm:760-761).
-//   * One wave = one split of one (sequence, kv head, head group). Waves never
+//   * One wave = one work item: a KV range of one (sequence, kv head, head
+//     group). The automatic path cuts every sequence into fixed-length KV
+//     chunks numbered without a host sync (slot = cu_kv[s] / C + s + chunk
+//     index, as the prefill tiles are), so every wave streams the same number
+//     of bytes whatever the spread of KV lengths; the explicit num_splits entry
+//     cuts each sequence into that many equal parts instead. Waves never
 //     synchronise with each other, so a workgroup is just 4 independent waves.
 //   * Per 32-key tile: K goes straight from HBM into MFMA A-operand registers
 //     (16 B per lane); V is loaded coalesced and transposed through a per-wave
 //     LDS buffer for the P.V product. The next tile's loads are issued before
 //     the current tile is computed.
-//   * Each split writes a normalised fp32 partial O and its LSE; the combine
-//     kernel merges splits with LSE weights and, unlike the reference's
-//     (src/attn_mpp.metal:498-521), also writes the final LSE.
+//   * Each work item writes a normalised fp32 partial O and its LSE (16 rows
+//     of its group); the combine kernel merges a sequence's items with LSE
+//     weights and, unlike the reference's (src/attn_mpp.metal:498-521), also
+//     writes the final LSE.
 #include "common.h"
 #include "kernels.h"
 #include "../../include/mtlattn_capi.h"
@@ -26,16 +32,43 @@ namespace {
 constexpr int kDecWaves = 4;
 constexpr int kDecKT = 32;      // keys per tile
 
+// Work items: chunk > 0 -> fixed KV chunks, slot = cu_kv[s] / chunk + s + c
+// (n_slots = total_kv / chunk + num_seqs + 1); chunk == 0 -> ns equal splits
+// per sequence, slot = s * ns + split (n_slots = num_seqs * ns). Partials of
+// item `slot` for kv head hk and head group hgi live at row
+// ((hk * n_hg + hgi) * n_slots + slot) * 16 + n (n = 16-row group row).
 struct DecKParams {
     const uint16_t* q; const uint16_t* k; const uint16_t* v;
     float* o_part; float* lse_part;
     const int* cu_q; const int* cu_kv;
     int64_t q_rs, k_rs, v_rs;
     int64_t total_q, total_kv;
-    int num_seqs, hq, hkv, g, hpb, n_hg, ns;
+    int num_seqs, hq, hkv, g, hpb, n_hg, ns, chunk, n_slots;
     float scale_log2;
     int causal;
 };
+
+// KV range [ks, ke) of work item `slot` of sequence s (false: no keys).
+__device__ inline bool item_range(const DecKParams& p, int slot, int& s, int& ks, int& ke) {
+    int kv_len;
+    if (p.chunk > 0) {
+        s = find_seq_for_tile(p.cu_kv, p.num_seqs, p.chunk, slot, p.total_kv);
+        const SeqRange kr = seq_range(p.cu_kv, s, p.total_kv);
+        kv_len = kr.end - kr.start;
+        ks = (slot - tile_base(p.cu_kv, s, p.chunk, p.total_kv)) * p.chunk;
+        ke = min(kv_len, ks + p.chunk);
+    } else {
+        s = slot / p.ns;
+        const int split = slot - s * p.ns;
+        const SeqRange kr = seq_range(p.cu_kv, s, p.total_kv);
+        kv_len = kr.end - kr.start;
+        int c = (kv_len + p.ns - 1) / p.ns;
+        c = (c + kDecKT - 1) / kDecKT * kDecKT;
+        ks = split * c;
+        ke = min(kv_len, ks + c);
+    }
+    return ke > ks;
+}
 
 // V^T tile [D][32] (64 B per row); 8-byte groups XOR-swizzled by row.
 __device__ inline uint32_t dec_tr_offset(int row, int group) {
@@ -55,11 +88,14 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
     char* vt = smem + w * (D * kDecKT * 2);
 
     int wid = blockIdx.x * kDecWaves + w;
-    const int split = wid % p.ns; wid /= p.ns;
-    const int hgi = wid % p.n_hg; wid /= p.n_hg;
-    const int hk = wid % p.hkv;
-    const int s = wid / p.hkv;
-    if (s >= p.num_seqs) return;
+    const int slot = wid % p.n_slots; wid /= p.n_slots;
+    const int hgi = wid % p.n_hg;
+    const int hk = wid / p.n_hg;
+    if (hk >= p.hkv) return;
+    int s, ks, ke;
+    const bool has_keys = item_range(p, slot, s, ks, ke);
+    // fixed chunks past a sequence's end are not read by the combine
+    if (!has_keys && p.chunk > 0) return;
     const SeqRange qr = seq_range(p.cu_q, s, p.total_q);
     const SeqRange kr = seq_range(p.cu_kv, s, p.total_kv);
     const int q_len = qr.end - qr.start, kv_len = kr.end - kr.start;
@@ -81,11 +117,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
         for (int kc = 0; kc < KC; ++kc) qf[kc] = ld16(qp + 32 * kc);
     }
 
-    int chunk = (kv_len + p.ns - 1) / p.ns;
-    chunk = (chunk + kDecKT - 1) / kDecKT * kDecKT;
-    const int ks = split * chunk;
-    const int ke = min(kv_len, ks + chunk);
-    const int n_tiles = ke > ks ? (ke - ks + kDecKT - 1) / kDecKT : 0;
+    const int n_tiles = has_keys ? (ke - ks + kDecKT - 1) / kDecKT : 0;
 
     const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * D;
     const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * D;
@@ -118,8 +150,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    if (n_tiles > 0) load(ks, ka, vr);
-    for (int it = 0; it < n_tiles; ++it) {
+    // Two register sets alternate: tile it is computed from set it % 2 while
+    // the loads of tiles it + 1 and it + 2 are in flight.
+    u32x4_t ka2[2][KC], vr2[VU][4];
+    auto step = [&](int it, u32x4_t (&ka)[2][KC], u32x4_t (&vr)[VU][4]) __attribute__((always_inline)) {
         const int kt = ks + it * kDecKT;
         // stage V^T of this tile in the wave's LDS buffer
         __builtin_amdgcn_wave_barrier();
@@ -139,8 +173,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) sc[mb] = mfma16<T>(ka[mb][kc], qf[kc], sc[mb]);
         }
-        // prefetch the next tile while the softmax and P.V run
-        if (it + 1 < n_tiles) load(kt + kDecKT, ka, vr);
+        // refill this register set with tile it + 2 (two tiles of latency cover)
+        if (it + 2 < n_tiles) load(kt + 2 * kDecKT, ka, vr);
 
         const bool need_mask = (kt + kDecKT > ke) || (p.causal && kt + kDecKT - 1 > coff);
         float mx = kNegInf;
@@ -189,6 +223,12 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
             const u32x2_t x1 = ld8(vt + dec_tr_offset(d, 4 + lg));
             oacc[db] = mfma16<T>(u32x4_t{x0[0], x0[1], x1[0], x1[1]}, pf, oacc[db]);
         }
+    };
+    if (n_tiles > 0) load(ks, ka, vr);
+    if (n_tiles > 1) load(ks + kDecKT, ka2, vr2);
+    for (int it = 0; it < n_tiles; it += 2) {
+        step(it, ka, vr);
+        if (it + 1 < n_tiles) step(it + 1, ka2, vr2);
     }
 
     // l_run is split over the 4 lane groups holding a row's keys.
@@ -196,52 +236,77 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
     lt += __shfl_xor(lt, 32);
     if (row_ok) {
         const float inv = lt > 0.f ? 1.f / lt : 0.f;
-        float* op = p.o_part + (((int64_t)split * p.total_q + grow) * p.hq + head) * D;
+        const int64_t prow = ((int64_t)(hk * p.n_hg + hgi) * p.n_slots + slot) * 16 + n16;
+        float* op = p.o_part + prow * D;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
             const int d = 16 * db + 4 * lg;
             *reinterpret_cast<f32x4_t*>(op + d) = oacc[db] * inv;
         }
-        if (lg == 0)
-            p.lse_part[((int64_t)split * p.total_q + grow) * p.hq + head] =
-                lt > 0.f ? m_run * kLn2 + logf(lt) : kNegInf;
+        if (lg == 0) p.lse_part[prow] = lt > 0.f ? m_run * kLn2 + logf(lt) : kNegInf;
     }
 }
 
-// One wave per (row, head): O = sum_s w_s O_s / sum_s w_s with w_s = exp(lse_s - max lse).
+// One wave per (row, head): O = sum_i w_i O_i / sum_i w_i over the work items
+// of the row's sequence, w_i = exp(lse_i - max lse). Rows outside every
+// sequence, or beyond the 16-row group (max_seqlen_q too small), are left
+// untouched as the flash forward leaves them.
 template <typename T>
-__global__ __launch_bounds__(256) void decode_combine_kernel(const float* __restrict__ o_part,
-                                                             const float* __restrict__ lse_part,
-                                                             typename T::raw* __restrict__ out,
-                                                             float* __restrict__ lse_out, int64_t total_q,
-                                                             int hq, int d, int ns) {
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecKParams p, typename T::raw* __restrict__ out,
+                                                             float* __restrict__ lse_out, int d) {
     const int64_t rh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (rh >= total_q * hq) return;
-    const int64_t stride = total_q * hq;
+    if (rh >= p.total_q * p.hq) return;
+    const int64_t row = rh / p.hq;
+    const int head = (int)(rh - row * p.hq);
+    // sequence of this row (largest s with cu_q[s] <= row)
+    int lo = 0, hi = p.num_seqs - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (p.cu_q[mid] <= row) lo = mid; else hi = mid - 1;
+    }
+    const int s = lo;
+    const SeqRange qr = seq_range(p.cu_q, s, p.total_q);
+    if (row < qr.start || row >= qr.end) return;
+    const int q_len = qr.end - qr.start, qi = (int)(row - qr.start);
+    const int hk = head / p.g, hh_full = head - hk * p.g;
+    const int hgi = hh_full / p.hpb, n = (hh_full - hgi * p.hpb) * q_len + qi;
+    if (n >= 16) return;
+    const SeqRange kr = seq_range(p.cu_kv, s, p.total_kv);
+    const int kv_len = kr.end - kr.start;
+    int first, count;
+    if (p.chunk > 0) {
+        first = tile_base(p.cu_kv, s, p.chunk, p.total_kv);
+        count = (kv_len + p.chunk - 1) / p.chunk;
+    } else {
+        first = s * p.ns;
+        count = p.ns;
+    }
+    const int64_t base = (int64_t)(hk * p.n_hg + hgi) * p.n_slots;
     float m = kNegInf;
-    for (int s = 0; s < ns; ++s) m = fmaxf(m, lse_part[s * stride + rh]);
+    for (int i = 0; i < count; ++i) m = fmaxf(m, p.lse_part[(base + first + i) * 16 + n]);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     float wsum = 0.f;
     if (m != kNegInf) {
-        for (int s = 0; s < ns; ++s) {
-            const float l = lse_part[s * stride + rh];
+        for (int i = 0; i < count; ++i) {
+            const int64_t prow = (base + first + i) * 16 + n;
+            const float l = p.lse_part[prow];
             if (l == kNegInf) continue;
             const float wgt = __expf(l - m);
             wsum += wgt;
-            const float* op = o_part + (s * stride + rh) * d;
+            const float* op = p.o_part + prow * d;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int dd = lane + 64 * i;
-                if (dd < d) acc[i] += wgt * op[dd];
+            for (int j = 0; j < 4; ++j) {
+                const int dd = lane + 64 * j;
+                if (dd < d) acc[j] += wgt * op[dd];
             }
         }
     }
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int dd = lane + 64 * i;
-        if (dd < d) out[rh * d + dd] = T::from_float(acc[i] * inv);
+    for (int j = 0; j < 4; ++j) {
+        const int dd = lane + 64 * j;
+        if (dd < d) out[rh * d + dd] = T::from_float(acc[j] * inv);
     }
     if (lse_out != nullptr && lane == 0) lse_out[rh] = wsum > 0.f ? m + logf(wsum) : kNegInf;
 }
@@ -264,9 +329,13 @@ hipError_t launch_typed(const DecodeArgs& a, hipStream_t st) {
     p.hpb = hpb;
     p.n_hg = g.g / hpb;
     p.ns = a.num_splits;
+    p.chunk = a.chunk;
+    const int64_t slots = a.chunk > 0 ? g.total_kv / a.chunk + g.num_seqs + 1 : (int64_t)g.num_seqs * a.num_splits;
+    if (slots > 0x3fffffff) return hipErrorInvalidValue;
+    p.n_slots = (int)slots;
     p.scale_log2 = g.scale * kLog2e;
     p.causal = g.causal;
-    const int64_t waves = (int64_t)g.num_seqs * g.hkv * p.n_hg * p.ns;
+    const int64_t waves = (int64_t)g.hkv * p.n_hg * p.n_slots;
     const int64_t blocks = (waves + kDecWaves - 1) / kDecWaves;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (blocks > 0)
@@ -275,9 +344,8 @@ hipError_t launch_typed(const DecodeArgs& a, hipStream_t st) {
     if (e != hipSuccess) return e;
     const int64_t rh = g.total_q * g.hq;
     if (rh > 0)
-        hipLaunchKernelGGL(decode_combine_kernel<T>, dim3((unsigned)((rh + 3) / 4)), dim3(256), 0, st,
-                           (const float*)a.o_part, (const float*)a.lse_part, (typename T::raw*)a.o, a.lse,
-                           g.total_q, g.hq, D, p.ns);
+        hipLaunchKernelGGL(decode_combine_kernel<T>, dim3((unsigned)((rh + 3) / 4)), dim3(256), 0, st, p,
+                           (typename T::raw*)a.o, a.lse, D);
     return hipGetLastError();
 }
 

@@ -50,9 +50,10 @@ struct DecodeArgs {
     const void* v; int64_t v_rs;
     void* o;                      // contiguous [total_q, hq, d]
     float* lse;                   // nullable
-    float* o_part;                // [ns, total_q, hq, d]
-    float* lse_part;              // [ns, total_q, hq]
-    int num_splits;
+    float* o_part;                // [hkv * head groups * slots * 16, d] (decode_workspace_rows)
+    float* lse_part;              // [hkv * head groups * slots * 16]
+    int num_splits;               // equal splits per sequence (used when chunk == 0)
+    int chunk;                    // > 0: fixed KV chunk length (multiple of 32)
     int max_q;                    // bound on q lengths; heads_per_group * max_q <= 16
 };
 
@@ -68,6 +69,13 @@ hipError_t launch_bwd_dkv_generic(int dtype, const BwdArgs& a, hipStream_t st);
 hipError_t launch_zero_outside(void* ptr, int64_t row_bytes, int64_t total_rows, const int* cu, int num_seqs,
                                hipStream_t st);
 hipError_t launch_decode(int dtype, const DecodeArgs& a, hipStream_t st);
+
+// Partial rows of the split-KV workspace (fp32 O rows of D values plus one
+// LSE each): kv heads x head groups x work-item slots x 16.
+inline int64_t decode_workspace_rows(int64_t total_kv, int num_seqs, int hkv, int n_hg, int chunk, int ns) {
+    const int64_t slots = chunk > 0 ? total_kv / chunk + num_seqs + 1 : (int64_t)num_seqs * ns;
+    return (int64_t)hkv * n_hg * slots * 16;
+}
 
 // Which head dims have MFMA kernels.
 inline bool mfma_head_dim(int d) { return d == 64 || d == 128; }

@@ -113,12 +113,18 @@ def test_null_tensor_pointer(lib):
     assert rc == ERR_INVALID and b"null" in lib.mtlattn_last_error()
 
 
+def _splitkv_bytes(rows, d):
+    o = rows * d * 4
+    return ((o + 255) // 256) * 256 + rows * 4
+
+
 def test_workspace_sizes(lib):
     p = problem(total_q=1000, num_heads_q=32, num_heads_kv=8)
     assert lib.mtlattn_varlen_bwd_workspace_size(ctypes.byref(p)) == 1000 * 32 * 4
+    # explicit splits: 16 partial rows per (kv head, head group, sequence, split);
+    # max_seqlen_q = 32 leaves one head per 16-row group, so g = 4 groups
     n = lib.mtlattn_attn_splitkv_workspace_size(ctypes.byref(p), 4)
-    o = 1000 * 32 * 128 * 4 * 4
-    assert n == ((o + 255) // 256) * 256 + 1000 * 32 * 4 * 4
+    assert n == _splitkv_bytes(8 * 4 * (2 * 4) * 16, 128)
     assert lib.mtlattn_attn_splitkv_workspace_size(ctypes.byref(p), 0) == 0
 
 
@@ -142,10 +148,16 @@ def test_decode_routing(lib, monkeypatch):
     monkeypatch.delenv("MTLATTN_NO_SPLITKV", raising=False)
     monkeypatch.delenv("MTLATTN_NO_MPP", raising=False)
     monkeypatch.delenv("MTLATTN_NO_MFMA", raising=False)
-    ns = lib.mtlattn_decode_num_splits(ctypes.byref(_c5_like()))
-    assert 1 <= ns <= 256
-    assert lib.mtlattn_varlen_fwd_workspace_size(ctypes.byref(_c5_like())) == \
-        lib.mtlattn_attn_splitkv_workspace_size(ctypes.byref(_c5_like()), ns)
+    slots = lib.mtlattn_decode_num_splits(ctypes.byref(_c5_like()))
+    # fixed KV chunks: slots = total_kv / chunk + num_seqs + 1 with a chunk of
+    # >= 256 keys sized for ~18 work items per CU (256 CUs without a device),
+    # rounded to the nearest multiple of 256
+    total_kv = 64 * 36864
+    chunk = -(-(total_kv * 8) // (256 * 18))
+    chunk = (chunk + 128) // 256 * 256
+    assert slots == total_kv // chunk + 64 + 1
+    # 8 kv heads x 1 head group (8 heads x q_len 1 fill a 16-row group)
+    assert lib.mtlattn_varlen_fwd_workspace_size(ctypes.byref(_c5_like())) == _splitkv_bytes(8 * slots * 16, 128)
     for kw in (dict(dtype=F32), dict(head_dim=96), dict(window=128), dict(max_seqlen_q=17),
                dict(total_kv=64 * 2000), dict(bias=FAKE, bias_kv_cols=10)):
         assert lib.mtlattn_decode_num_splits(ctypes.byref(_c5_like(**kw))) == 0, kw
