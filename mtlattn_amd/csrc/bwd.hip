@@ -156,14 +156,15 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         const int kt = kv_lo + it * kKT;
         // tiles outside this wave's band are computed fully masked, not
         // skipped (a branch around the MFMAs costs accumulator copies)
-        bool skip = !wave_active;
-        if (p.causal && kt > wq_last + coff) skip = true;
-        if (p.window > 0 && kt + kKT - 1 < qa + coff - p.window + 1) skip = true;
+        // (bitwise | and &: these uniform tests must not become branches,
+        // which would split the loop body into separately scheduled blocks)
+        const bool skip = !wave_active | ((p.causal != 0) & (kt > wq_last + coff)) |
+                          ((p.window > 0) & (kt + kKT - 1 < qa + coff - p.window + 1));
         const char* Ks = smem + (it % NBUF) * STAGE;
         const char* krb = opaque(Ks + rbase);
         const char* ktb = opaque(Ks + tbase);
-        const bool need_mask = skip || (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
-                               (p.window > 0 && kt < wq_last + coff - p.window + 1);
+        const bool need_mask = skip | (kt + kKT > kv_len) | ((p.causal != 0) & (kt + kKT - 1 > qa + coff)) |
+                               ((p.window > 0) & (kt < wq_last + coff - p.window + 1));
         const int d0 = kt + 4 * hi - band.lo;
         const uint32_t wdt = skip ? 0u : band.width;
         // S^T and dP^T of both 32-key halves on the matrix cores first; half
@@ -190,6 +191,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
                 sacc[kb][r] = __builtin_amdgcn_exp2f(x);
             }
             if (need_mask) {     // out-of-band keys -> P = 0
+                asm volatile("");   // keep a real branch (no speculated selects on every tile)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
@@ -334,8 +336,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     auto block_needs_mask = [&](int st, int qb) {
         const int qf0 = stage_q0(st) + 32 * qb;
         const int qf1 = min(q_len, qf0 + 32) - 1;
-        return (kw + kKW > kv_len) || (qf0 + 32 > q_len) || (p.causal && wk_last > qf0 + coff) ||
-               (p.window > 0 && kw < qf1 + coff - p.window + 1);
+        return (kw + kKW > kv_len) | (qf0 + 32 > q_len) | ((p.causal != 0) & (wk_last > qf0 + coff)) |
+               ((p.window > 0) & (kw < qf1 + coff - p.window + 1));
     };
     const Band band = query_band(key, coff, q_len, kv_len, p.causal, p.window);
 
@@ -365,6 +367,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 #pragma unroll
                 for (int qb = 0; qb < 2; ++qb)
                     sacc[qb] = mfma32<T>(row_operand<D>(qrb, kc, 32 * qb), kvf[kc], sacc[qb]);
+            // exponentials of both blocks (overlapping the S MFMAs in flight),
+            // then the rarely needed masks, then the dV products
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
                 const float* brow0 = nullptr;
@@ -389,13 +393,20 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                         sacc[qb][r] = __builtin_amdgcn_exp2f(arg);
                     }
                 }
+            }
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
                 // out-of-band elements (and rows with no allowed key) -> P = 0
                 if (block_needs_mask(st, qb)) {
+                    asm volatile("");   // keep a real branch (no speculated selects on every block)
                     const int d0 = qt + 32 * qb + 4 * hi - band.lo;   // query - band.lo at r = 0
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
                         sacc[qb][r] = (uint32_t)(d0 + 8 * (r >> 2) + (r & 3)) < band.width ? sacc[qb][r] : 0.f;
                 }
+            }
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {
                     const int r0 = 8 * cc;

@@ -145,9 +145,10 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         // A tile outside this wave's band is computed fully masked (P = 0)
         // rather than skipped: a branch around the MFMAs makes the compiler
         // copy the 64 O accumulator registers twice per tile.
-        bool skip = !wave_active;
-        if (p.causal && kt > wq_last + coff) skip = true;
-        if (p.window > 0 && kt + kKT - 1 < qa + coff - p.window + 1) skip = true;
+        // (bitwise | and &: these uniform tests must not become branches,
+        // which would split the loop body into separately scheduled blocks)
+        const bool skip = !wave_active | ((p.causal != 0) & (kt > wq_last + coff)) |
+                          ((p.window > 0) & (kt + kKT - 1 < qa + coff - p.window + 1));
         const char* Ks = smem + (it % NBUF) * STAGE;
         const char* kb_ = opaque(Ks + rbase);
         const char* vtb = opaque(Ks + TILE + tbase);
@@ -163,9 +164,12 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         // keep the V^T reads of the P.V phase from being hoisted above the
         // softmax (they would pin 64 registers across it)
         __builtin_amdgcn_sched_barrier(0);
-        const bool need_mask = skip || (kt + kKT > kv_len) || (p.causal && kt + kKT - 1 > qa + coff) ||
-                               (p.window > 0 && kt < wq_last + coff - p.window + 1);
+        const bool need_mask = skip | (kt + kKT > kv_len) | ((p.causal != 0) & (kt + kKT - 1 > qa + coff)) |
+                               ((p.window > 0) & (kt < wq_last + coff - p.window + 1));
         if (need_mask) {
+            // (the empty asm keeps this a real branch: speculating the selects
+            // into every tile would cost ~100 VALU per tile)
+            asm volatile("");
             const int d0 = kt + 4 * hi - band.lo;
             const uint32_t wdt = skip ? 0u : band.width;
 #pragma unroll

@@ -207,6 +207,23 @@ def test_decode_cases(mt):
     _fwd(mt, "decode GQA 64/8 few-q", [3, 2], [9000, 4100], 64, 8, 128, torch.bfloat16, causal=True)
 
 
+def test_decode_small_chunks(mt, monkeypatch):
+    """The automatic split-KV path with 256-key chunks: many chunks per
+    sequence, a partial last chunk, KV lengths below one chunk, an empty
+    sequence, and speculative (q_len > 1) rows, all against the oracle."""
+    from mtlattn_amd import capi
+    monkeypatch.setenv("MTLATTN_DECODE_CHUNK", "256")
+    q_lens, kv_lens = [1, 1, 1, 1, 1], [2048, 300, 0, 4097, 5800]
+    q, k, v = _inputs(q_lens, kv_lens, 8, 2, 128, torch.bfloat16, seed=11)
+    p = capi.problem_for(q.cuda(), k.cuda(), cu_of(q_lens, "cuda"), cu_of(kv_lens, "cuda"), 1, 0.1, causal=True)
+    assert capi.lib().mtlattn_decode_num_splits(p) == sum(kv_lens) // 256 + len(kv_lens) + 1   # routed, chunked
+    _fwd(mt, "decode 256-key chunks, ragged + empty", q_lens, kv_lens, 8, 2, 128, torch.bfloat16, causal=True,
+         seed=11)
+    _fwd(mt, "decode 256-key chunks, q_len 1-3 GQA 16/2", [2, 3, 1], [3000, 2600, 4100], 16, 2, 128,
+         torch.float16, causal=True, seed=12)
+    _fwd(mt, "decode 256-key chunks, non-causal D=64", [1, 1], [2304, 2560], 8, 8, 64, torch.bfloat16, seed=13)
+
+
 # causal (tests/test_correctness.py:367-371)
 def test_causal_cases(mt):
     _fwd(mt, "causal self D=128", [1024], [1024], 12, 12, 128, torch.float16, causal=True)
