@@ -122,6 +122,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     }
     const float* brow = nullptr;
     if (BIAS && row_ok) brow = p.bias + grow * p.bias_qs + (int64_t)head * p.bias_hs;
+    // settle these loads here: the key loop's own wait counts cover only the
+    // staging loads
+    wait_vmcnt<0>();
 
     const int q_last_wg = min(q_len, q0 + QT) - 1;
     const int kv_hi = p.causal ? min(kv_len, q_last_wg + coff + 1) : kv_len;
@@ -316,7 +319,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         if (w < 2) {
             const int q = min(qt + lane, q_len - 1);        // rows past the end are masked
             const float* src = (w == 0 ? p.lse : p.delta) + (int64_t)(qr.start + q) * p.hq + h;
-            __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(buf + 2 * TILE + w * kQT * 4), 4, 0, 0);
+            lds_dma4(src, buf + 2 * TILE + w * kQT * 4);
         }
     };
 

@@ -188,6 +188,26 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
+// One global_load_lds_dwordx4: each lane's 16 bytes at gptr land at LDS
+// lds + 16 * lane. Issued as inline asm so the compiler's wait-count
+// bookkeeping does not see it: the compiler conservatively waits for every
+// outstanding direct load before any transposed LDS read (ds_read_b64_tr)
+// and before barriers, which would drain the staging pipeline each tile.
+// Callers therefore order these loads themselves (wait_vmcnt, then a barrier)
+// before LDS reads of the staged data. `lds` (passed in M0) must be
+// wave-uniform. The s_nop covers the one wait state required between an M0
+// write and an LDS direct load.
+__device__ inline void lds_dma16(const void* gptr, const char* lds) {
+    const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "{m0}"(a) : "memory");
+}
+// Same for 4 bytes per lane (global_load_lds_dword): lane data lands at
+// lds + 4 * lane.
+__device__ inline void lds_dma4(const void* gptr, const char* lds) {
+    const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(gptr), "{m0}"(a) : "memory");
+}
+
 // Stage rows [row0, row0 + ROWS) of a [*, D] 16-bit matrix (row stride rs
 // elements) into a swizzled LDS tile with global_load_lds_dwordx4: each
 // instruction moves 1 KB and lands lane l's 16 bytes at tile + 16 l, so the
@@ -205,8 +225,7 @@ __device__ inline void stage_tile(char* tile, const uint16_t* base, int64_t rs, 
         const int row = byte / (2 * D);
         const int chunk = ((byte % (2 * D)) >> 4) ^ row_swz<D>(row);
         const int grow = min(row0 + row, row_end - 1);
-        __builtin_amdgcn_global_load_lds(base + (int64_t)grow * rs + chunk * 8, (lds_void_t*)(tile + i * 1024), 16,
-                                         0, 0);
+        lds_dma16(base + (int64_t)grow * rs + chunk * 8, tile + i * 1024);
     }
 }
 

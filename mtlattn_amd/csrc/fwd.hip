@@ -90,6 +90,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         const uint16_t* qp = p.q + (int64_t)(qr.start + row) * p.q_rs + (int64_t)head * D + 8 * hi;
 #pragma unroll
         for (int kc = 0; kc < DC; ++kc) qf[kc] = ld16(qp + 16 * kc);
+        // settle the fragments here: the key loop's own wait counts cover
+        // only the staging loads
+        wait_vmcnt<0>();
     }
 
     // Key range of the whole workgroup.
