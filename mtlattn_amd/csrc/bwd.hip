@@ -183,6 +183,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
                 pacc[kb] = mfma32<T>(ld16(a + kb * 32 * 2 * D + TILE), df[kc], pacc[kb]);
             }
         }
+        pipe_reads<1, 4 * DC, 4>();
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -306,16 +307,20 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     // the repeats (each workgroup stops at its own causal start q_lo).
     auto stage_head = [&](int st) { return hk * p.g + st % p.g; };
     auto stage_q0 = [&](int st) { return q_lo + (n_q_tiles - 1 - st / p.g) * kQT; };
-    // Direct loads of stage `st`: Q and dO tiles by all waves, lse by wave 0,
-    // delta by wave 1 (4 bytes per lane, lane l -> row l).
+    // Direct loads of stage `st`: Q and dO tiles by the four A waves, lse by
+    // wave 0, delta by wave 1 (4 bytes per lane, lane l -> row l).
     auto stage = [&](int st) {
         char* buf = smem + (st % NBUF) * STAGE;
         const int h = stage_head(st);
         const int qt = stage_q0(st);
         const int64_t hoff = (int64_t)qr.start * p.q_rs + (int64_t)h * D;
-        stage_tile<D, kQT, kWaves>(buf, p.q + hoff, p.q_rs, qt, q_len, w, lane);
-        stage_tile<D, kQT, kWaves>(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * D, p.do_rs, qt,
+        // (wave A of each pair issues the tile loads: wave B, one stage
+        // behind, is the longer of the two and should not stall on issue)
+        if (role_a) {
+            stage_tile<D, kQT, NP>(buf, p.q + hoff, p.q_rs, qt, q_len, w, lane);
+            stage_tile<D, kQT, NP>(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * D, p.do_rs, qt,
                                    q_len, w, lane);
+        }
         if (w < 2) {
             const int q = min(qt + lane, q_len - 1);        // rows past the end are masked
             const float* src = (w == 0 ? p.lse : p.delta) + (int64_t)(qr.start + q) * p.hq + h;
@@ -329,6 +334,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     f32x16_t acc[DB];                            // dV^T (wave A) or dK^T (wave B)
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = f32x16_t{};
+    f32x16_t pacc[2] = {f32x16_t{}, f32x16_t{}};  // wave B: dP of the previous stage
 
     // Is the 32x32 block (queries qf0.., this pair's keys) of stage st empty
     // or does it need per-element masking? Identical in both waves of a pair.
@@ -424,44 +430,53 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                 }
             }
         }
-        if (!role_a && st > 0) {
-            const int sp = st - 1;                    // wave B works one stage behind
-            const char* Qs = smem + (sp % NBUF) * STAGE;
-            const char* Ds = Qs + TILE;
-            const float* dls = reinterpret_cast<const float*>(Qs + 2 * TILE) + kQT;
-            const char* drb = opaque(Ds + rbase);
-            const char* qtb = opaque(Qs + tbase);
-            const char* pb = smem + NBUF * STAGE + (sp & 1) * PSTAGE + pair * 2 * PBLK;
-            // dP of both blocks first; block 0's dS overlaps block 1's MFMAs
-            f32x16_t pacc[2] = {f32x16_t{}, f32x16_t{}};
+        if (!role_a) {
+            // Wave B runs a software pipeline one stage behind wave A: first
+            // dS and dK of stage st - 1 (dP of that stage is already in
+            // registers), then dP of stage st. Its VALU phase (dS) thus meets
+            // wave A's S products and its dK products meet wave A's
+            // exponentials, instead of both waves of a SIMD issuing matrix
+            // work and then VALU work at the same time.
+            if (st > 0) {
+                const int sp = st - 1;
+                const char* Qs = smem + (sp % NBUF) * STAGE;
+                const float* dls = reinterpret_cast<const float*>(Qs + 2 * TILE) + kQT;
+                const char* qtb = opaque(Qs + tbase);
+                const char* pb = smem + NBUF * STAGE + (sp & 1) * PSTAGE + pair * 2 * PBLK;
 #pragma unroll
-            for (int kc = 0; kc < DC; ++kc)
+                for (int qb = 0; qb < 2; ++qb) {
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb)
-                    pacc[qb] = mfma32<T>(row_operand<D>(drb, kc, 32 * qb), kvf[kc], pacc[qb]);
+                    for (int cc = 0; cc < 2; ++cc) {
+                        const u32x4_t pp = ld16(pb + qb * PBLK + cc * 1024 + lane * 16);
+                        float dsv[8];
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
+                        for (int rg2 = 0; rg2 < 2; ++rg2) {
+                            const int qi = 32 * qb + 8 * (2 * cc + rg2) + 4 * hi;
+                            const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(dls + qi);
 #pragma unroll
-                for (int cc = 0; cc < 2; ++cc) {
-                    const u32x4_t pp = ld16(pb + qb * PBLK + cc * 1024 + lane * 16);
-                    float dsv[8];
-#pragma unroll
-                    for (int rg2 = 0; rg2 < 2; ++rg2) {
-                        const int qi = 32 * qb + 8 * (2 * cc + rg2) + 4 * hi;
-                        const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(dls + qi);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int j = 4 * rg2 + e;              // r = 8 cc + j
-                            const float pr = (j & 1) ? hi16<T>(pp[j >> 1]) : lo16<T>(pp[j >> 1]);
-                            dsv[j] = pr * (pacc[qb][8 * cc + j] - d4[e]);
+                            for (int e = 0; e < 4; ++e) {
+                                const int j = 4 * rg2 + e;              // r = 8 cc + j
+                                const float pr = (j & 1) ? hi16<T>(pp[j >> 1]) : lo16<T>(pp[j >> 1]);
+                                dsv[j] = pr * (pacc[qb][8 * cc + j] - d4[e]);
+                            }
                         }
-                    }
-                    const u32x4_t bs = u32x4_t{T::pack2(dsv[0], dsv[1]), T::pack2(dsv[2], dsv[3]),
-                                               T::pack2(dsv[4], dsv[5]), T::pack2(dsv[6], dsv[7])};
+                        const u32x4_t bs = u32x4_t{T::pack2(dsv[0], dsv[1]), T::pack2(dsv[2], dsv[3]),
+                                                   T::pack2(dsv[4], dsv[5]), T::pack2(dsv[6], dsv[7])};
 #pragma unroll
-                    for (int db = 0; db < DB; ++db)
-                        acc[db] = mfma32<T>(tr_operand<D>(qtb, 2 * qb + cc, db), bs, acc[db]);
+                        for (int db = 0; db < DB; ++db)
+                            acc[db] = mfma32<T>(tr_operand<D>(qtb, 2 * qb + cc, db), bs, acc[db]);
+                    }
                 }
+            }
+            if (st < n_stages) {
+                const char* drb = opaque(smem + (st % NBUF) * STAGE + TILE + rbase);
+                pacc[0] = f32x16_t{};
+                pacc[1] = f32x16_t{};
+#pragma unroll
+                for (int kc = 0; kc < DC; ++kc)
+#pragma unroll
+                    for (int qb = 0; qb < 2; ++qb)
+                        pacc[qb] = mfma32<T>(row_operand<D>(drb, kc, 32 * qb), kvf[kc], pacc[qb]);
             }
         }
         // stage st + 1 landed for this wave; wave 0 pre-scales its lse column

@@ -237,6 +237,21 @@ __device__ inline void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8));
 }
 
+// Scheduling hint for the region just emitted: N MFMAs that each consume R
+// LDS reads go out with the reads AHEAD operands in front of the MFMA that
+// uses them (the default schedule issues each operand's reads just before
+// its MFMA and waits for them there).
+template <int R, int N, int AHEAD>
+__device__ inline void pipe_reads() {
+    __builtin_amdgcn_sched_group_barrier(0x100, R * AHEAD, 0);   // LDS reads
+#pragma unroll
+    for (int i = 0; i < N - AHEAD; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, AHEAD, 0);
+}
+
 // Keeps a per-iteration address opaque to the optimiser, so constant offsets
 // fold into the LDS instructions' offset fields and per-lane XOR variants are
 // formed per use instead of being hoisted out of the loop as live registers.

@@ -164,6 +164,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
                 sacc[kb] = mfma32<T>(a, qf[kc], sacc[kb]);
             }
         }
+        pipe_reads<1, 2 * DC, 4>();
         // keep the V^T reads of the P.V phase from being hoisted above the
         // softmax (they would pin 64 registers across it)
         __builtin_amdgcn_sched_barrier(0);
