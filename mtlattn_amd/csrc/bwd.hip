@@ -48,6 +48,7 @@ struct BwdKParams {
     int num_seqs, hq, hkv, g, hpw, n_tiles, n_hg;
     float scale, scale_log2;
     int causal, window;
+    int bias_v4;      // bias rows 16-byte aligned (pointer and strides)
 };
 
 template <typename T, bool OUT_F32>
@@ -120,8 +121,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         lse2 = l == kNegInf ? kPosInf : l * kLog2e;   // empty rows: P = 0
         dlt = p.delta[grow * p.hq + head];
     }
+    // bias row of this lane's query (rows past the end read the last row);
+    // columns at or past bias_cols read as 0
     const float* brow = nullptr;
-    if (BIAS && row_ok) brow = p.bias + grow * p.bias_qs + (int64_t)head * p.bias_hs;
+    if (BIAS) brow = p.bias + grow * p.bias_qs + (int64_t)head * p.bias_hs;
     // settle these loads here: the key loop's own wait counts cover only the
     // staging loads
     wait_vmcnt<0>();
@@ -155,8 +158,29 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     for (int it = 0; it < n_kv_tiles; ++it) {
         if (it + 1 < n_kv_tiles) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
         __syncthreads();
-        if (it + 2 < n_kv_tiles) stage(it + 2);
+        // (with a bias, the tile loads go out after the bias is consumed: the
+        // bias loads' wait would otherwise also wait for them)
+        if (!BIAS && it + 2 < n_kv_tiles) stage(it + 2);
         const int kt = kv_lo + it * kKT;
+        // the bias of the whole tile, all loads in flight together (4-key
+        // groups at 32 kb + 8 g + 4 hi)
+        f32x4_t bv[8];
+        if (BIAS) {
+            if (kt + kKT <= p.bias_cols && p.bias_v4) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    bv[i] = *reinterpret_cast<const f32x4_t*>(brow + kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int key = kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi + j;
+                        const float b = brow[min(key, (int)p.bias_cols - 1)];
+                        bv[i][j] = key < p.bias_cols ? b : 0.f;
+                    }
+            }
+        }
         // tiles outside this wave's band are computed fully masked, not
         // skipped (a branch around the MFMAs costs accumulator copies)
         // (bitwise | and &: these uniform tests must not become branches,
@@ -188,12 +212,11 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int c = 32 * kb + 8 * (r >> 2) + (r & 3);     // key - (kt + 4 hi)
                 float x = fmaf(sacc[kb][r], c2, -lse2);
-                if (BIAS && brow != nullptr && kt + 4 * hi + c < p.bias_cols)
-                    x = fmaf(brow[kt + 4 * hi + c], kLog2e, x);
+                if (BIAS) x = fmaf(bv[4 * kb + (r >> 2)][r & 3], kLog2e, x);
                 sacc[kb][r] = __builtin_amdgcn_exp2f(x);
             }
+            if (BIAS && kb == 1 && it + 2 < n_kv_tiles) stage(it + 2);
             if (need_mask) {     // out-of-band keys -> P = 0
                 asm volatile("");   // keep a real branch (no speculated selects on every tile)
 #pragma unroll
@@ -307,24 +330,29 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     // the repeats (each workgroup stops at its own causal start q_lo).
     auto stage_head = [&](int st) { return hk * p.g + st % p.g; };
     auto stage_q0 = [&](int st) { return q_lo + (n_q_tiles - 1 - st / p.g) * kQT; };
-    // Direct loads of stage `st`: Q and dO tiles by the four A waves, lse by
-    // wave 0, delta by wave 1 (4 bytes per lane, lane l -> row l).
+    // Direct loads of stage `st`: Q and dO tiles by four loader waves
+    // (ldw = 0..3), lse by loader 0, delta by loader 1 (4 bytes per lane,
+    // lane l -> row l).
+    const int ldw = BIAS ? (role_a ? -1 : w - NP) : (role_a ? w : -1);
     auto stage = [&](int st) {
         char* buf = smem + (st % NBUF) * STAGE;
         const int h = stage_head(st);
         const int qt = stage_q0(st);
         const int64_t hoff = (int64_t)qr.start * p.q_rs + (int64_t)h * D;
-        // (wave A of each pair issues the tile loads: wave B, one stage
-        // behind, is the longer of the two and should not stall on issue)
-        if (role_a) {
-            stage_tile<D, kQT, NP>(buf, p.q + hoff, p.q_rs, qt, q_len, w, lane);
+        // Without a bias the A waves issue the tile loads: wave B, one stage
+        // behind, is the longer of the two and should not stall on issue.
+        // With a bias the A waves keep their own bias loads in flight, and
+        // the wait for those would also cover tile loads issued after them,
+        // so the B waves load the tiles.
+        if (ldw >= 0) {
+            stage_tile<D, kQT, NP>(buf, p.q + hoff, p.q_rs, qt, q_len, ldw, lane);
             stage_tile<D, kQT, NP>(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * D, p.do_rs, qt,
-                                   q_len, w, lane);
+                                   q_len, ldw, lane);
         }
-        if (w < 2) {
+        if (ldw == 0 || ldw == 1) {
             const int q = min(qt + lane, q_len - 1);        // rows past the end are masked
-            const float* src = (w == 0 ? p.lse : p.delta) + (int64_t)(qr.start + q) * p.hq + h;
-            lds_dma4(src, buf + 2 * TILE + w * kQT * 4);
+            const float* src = (ldw == 0 ? p.lse : p.delta) + (int64_t)(qr.start + q) * p.hq + h;
+            lds_dma4(src, buf + 2 * TILE + ldw * kQT * 4);
         }
     };
 
@@ -353,7 +381,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     if (n_stages > 0) {
         stage(0);
         wait_vmcnt<0>();
-        if (w == 0) reinterpret_cast<float*>(smem + 2 * TILE)[lane] *= -kLog2e;
+        if (ldw == 0) reinterpret_cast<float*>(smem + 2 * TILE)[lane] *= -kLog2e;
         __syncthreads();
     }
     for (int st = 0; n_stages > 0 && st <= n_stages; ++st) {
@@ -370,6 +398,20 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             // S of both 32-query blocks on the matrix cores; block 0's
             // exponentials then overlap block 1's MFMAs, and block 1's
             // exponentials overlap block 0's dV products.
+            // the stage's bias (this lane's key column, 32 query rows), all
+            // loads in flight together under the S products; columns at or
+            // past bias_cols read as 0, rows past the end read the last row
+            float bvals[2][16];
+            if (BIAS) {
+                const float* bcol = p.bias + (int64_t)h * p.bias_hs + min(key, (int)p.bias_cols - 1);
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int qrow = min(qt + 32 * qb + 8 * (r >> 2) + 4 * hi + (r & 3), q_len - 1);
+                        bvals[qb][r] = bcol[(int64_t)(qr.start + qrow) * p.bias_qs];
+                    }
+            }
             f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
 #pragma unroll
             for (int kc = 0; kc < DC; ++kc)
@@ -380,8 +422,6 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             // then the rarely needed masks, then the dV products
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
-                const float* brow0 = nullptr;
-                if (BIAS) brow0 = p.bias + (int64_t)h * p.bias_hs + key;
 #pragma unroll
                 for (int rg = 0; rg < 4; ++rg) {
                     const int qi = 32 * qb + 8 * rg + 4 * hi;    // stage-local query of r = 4 rg
@@ -391,9 +431,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                         const int r = 4 * rg + e;
                         float arg;
                         if (BIAS) {
-                            float x = sacc[qb][r] * c2;
-                            const int qrow = min(qt + qi + e, q_len - 1);
-                            if (key < p.bias_cols) x = fmaf(brow0[(int64_t)(qr.start + qrow) * p.bias_qs], kLog2e, x);
+                            const float x = fmaf(key < p.bias_cols ? bvals[qb][r] : 0.f, kLog2e, sacc[qb][r] * c2);
                             // rows whose every logit is -inf (bias) have lse = -inf: P = 0
                             arg = x == kNegInf ? kNegInf : x + l4[e];
                         } else {
@@ -479,10 +517,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                         pacc[qb] = mfma32<T>(row_operand<D>(drb, kc, 32 * qb), kvf[kc], pacc[qb]);
             }
         }
-        // stage st + 1 landed for this wave; wave 0 pre-scales its lse column
-        // (-lse log2 e) before the barrier publishes the stage
+        // stage st + 1 landed for this wave; loader 0 pre-scales its lse
+        // column (-lse log2 e) before the barrier publishes the stage
         wait_vmcnt<0>();
-        if (w == 0 && st + 1 < n_stages) {
+        if (ldw == 0 && st + 1 < n_stages) {
             float* l = reinterpret_cast<float*>(smem + ((st + 1) % NBUF) * STAGE + 2 * TILE);
             l[lane] *= -kLog2e;
         }
@@ -583,6 +621,7 @@ BwdKParams make_params(const BwdArgs& a) {
     p.n_tiles = 0; p.n_hg = 0;
     p.scale = g.scale; p.scale_log2 = g.scale * kLog2e;
     p.causal = g.causal; p.window = g.window > 0 ? g.window : 0;
+    p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0;
     return p;
 }
 

@@ -94,7 +94,8 @@ Geometry make_geo(const mtlattn_problem* p) {
     g.scale = p->scale;
     g.causal = p->causal ? 1 : 0;
     g.window = p->window > 0 ? p->window : 0;
-    g.bias = p->bias;
+    // a bias with no columns reads as 0 everywhere: the same as none
+    g.bias = p->bias_kv_cols > 0 ? p->bias : nullptr;
     g.bias_qs = p->bias_q_stride;
     g.bias_hs = p->bias_h_stride;
     g.bias_cols = p->bias_kv_cols;

@@ -42,6 +42,7 @@ struct FwdKParams {
     int num_seqs, hq, g, hpw, n_tiles, n_hg;
     float scale_log2;
     int causal, window;
+    int bias_v4;      // bias rows 16-byte aligned (pointer and strides)
 };
 
 // GENERAL = explicit per-element logit scaling, with the optional bias; the
@@ -126,9 +127,31 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
 
     const int qrow = qa + l32;
     const Band band = key_band(qrow, coff, kv_len, p.causal, p.window);
+    // Bias row of this lane's query (rows past the sequence end read its last
+    // row: finite, never stored). Columns at or past bias_cols read as 0.
+    const bool has_bias = BIAS && p.bias != nullptr;
     const float* brow = nullptr;
-    if (BIAS && p.bias != nullptr && qrow < q_len)
-        brow = p.bias + (int64_t)(qr.start + qrow) * p.bias_qs + (int64_t)head * p.bias_hs;
+    if (has_bias)
+        brow = p.bias + (int64_t)(qr.start + min(qrow, q_len - 1)) * p.bias_qs + (int64_t)head * p.bias_hs;
+    // The bias of a whole tile (this lane's 32 keys: 4-key groups at
+    // 32 kb + 8 g + 4 hi) is loaded up front, all loads in flight together,
+    // and consumed after the S products; 16-byte loads when aligned.
+    auto load_bias = [&](int kt, f32x4_t (&bv)[8]) {
+        if (kt + kKT <= p.bias_cols && p.bias_v4) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                bv[i] = *reinterpret_cast<const f32x4_t*>(brow + kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int key = kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi + j;
+                    const float b = brow[min(key, (int)p.bias_cols - 1)];
+                    bv[i][j] = key < p.bias_cols ? b : 0.f;
+                }
+        }
+    };
     const float c2 = p.scale_log2;
     constexpr bool raw_max = !GENERAL;   // max(s * c) = c * max(s) needs c > 0 (host-checked)
     // Rescale O only when the running max grows by more than 2^8: unnormalised
@@ -141,9 +164,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         // tile `it` landed (the next one may still be in flight), then publish
         if (it + 1 < n_kv_tiles) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
         __syncthreads();
-        // the buffer of tile it + 2 was last read in iteration it - 1
-        if (it + 2 < n_kv_tiles) stage(it + 2);
+        // the buffer of tile it + 2 was last read in iteration it - 1 (with a
+        // bias, the tile loads go out after the bias is consumed: the bias
+        // loads' wait would otherwise also wait for them)
+        if (!has_bias && it + 2 < n_kv_tiles) stage(it + 2);
         const int kt = kv_lo + it * kKT;
+        f32x4_t bv[8];
+        if (has_bias) load_bias(kt, bv);
 
         // A tile outside this wave's band is computed fully masked (P = 0)
         // rather than skipped: a branch around the MFMAs makes the compiler
@@ -199,10 +226,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
                 for (int r = 0; r < 16; ++r) {
                     const float sv = sacc[kb][r];
                     float x = sv == kNegInf ? kNegInf : sv * c2;   // masked stays -inf for any sign of c2
-                    if (BIAS && brow != nullptr) {
-                        const int key = kt + 32 * kb + 8 * (r >> 2) + 4 * hi + (r & 3);
-                        if (x != kNegInf && key < p.bias_cols) x = fmaf(brow[key], kLog2e, x);
-                    }
+                    if (has_bias) x = fmaf(bv[4 * kb + (r >> 2)][r & 3], kLog2e, x);
                     sacc[kb][r] = x;
                     mx = fmaxf(mx, x);
                 }
@@ -219,6 +243,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
             for (int db = 0; db < DB; ++db) oacc[db] *= corr;
         }
         m_run = m_new;
+        if (has_bias && it + 2 < n_kv_tiles) stage(it + 2);
         // P (rounded to T) as B operands; chunk c covers tile keys
         // 16c + 8(j/4) + 4hi + j%4. The row sum adds the rounded values.
         u32x4_t pf[4];
@@ -284,6 +309,7 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     p.n_hg = g.hq / p.hpw;
     p.scale_log2 = g.scale * kLog2e;
     p.causal = g.causal; p.window = g.window > 0 ? g.window : 0;
+    p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0;
     const int64_t blocks = (int64_t)p.n_tiles * p.n_hg;
     if (blocks <= 0) return hipSuccess;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
