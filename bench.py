@@ -9,7 +9,8 @@ autograd step of the op, through the same `_C` calls autograd makes. FLOPs
 count attended pairs only (the reference's convention, mtlattn/bench.py:25-32):
 fwd 4*D*Hq*pairs, bwd 2.5x that, fwd+bwd 14*D*Hq*pairs. Inputs are synthetic
 N(0,1) and resident in HBM before timing. The secondary line item is split-KV
-decode HBM GB/s (config C5).
+decode HBM GB/s (config C5); the other prefill configs (C1, C2, C4) follow
+as fwd+bwd TFLOP/s and fraction of peak under "other_configs".
 
 Per-kernel times: each kernel is launched alone through the C ABI
 (mtlattn_amd/capi.py) on torch's current stream, K times back to back between
@@ -31,6 +32,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA (spec)
+PEAK_FP32_TFLOPS = 157.3       # MI355X fp32 (spec)
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E (spec)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -47,6 +49,7 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C1/C2/C4 lines")
     ap.add_argument("--only", choices=["c3", "c5", "copy"], default=None,
                     help="run one workload (or the 1 GiB copy used to calibrate HBM byte counters) "
                          "and print only its timing: the short program profilers wrap")
@@ -145,6 +148,83 @@ def bench_c3(args):
     flops = 14.0 * unit
     return {"ms_per_step": wall_ms, "tflops": flops / (wall_ms * 1e-3) / 1e12, "pairs": pairs, "flops": flops,
             "kern_ms": kern_ms, "algo_flop": algo, "launches_timed": n, "finite": fin}
+
+
+def _attended_pairs(lens, causal, window):
+    pairs = 0
+    for L in lens:
+        if not causal:
+            pairs += L * L
+        elif window <= 0:
+            pairs += L * (L + 1) // 2
+        else:
+            w = min(L, window)
+            pairs += w * (w + 1) // 2 + (L - w) * window
+    return pairs
+
+
+def bench_configs(args):
+    """The other prefill configs of BASELINE.json (C1, C2, C4): fwd+bwd per
+    step through `_C`, as for C3. Synthetic N(0,1) inputs generated on the
+    device; C2's lengths and C4's bias follow the config sheet."""
+    import torch
+    import mtlattn
+    C = mtlattn._C
+    gl = torch.Generator().manual_seed(args.seed)
+    c2_lens = torch.randint(256, 4097, (32,), generator=gl).tolist()
+    cfgs = [
+        ("C1", "fp32 plumbing: lens {17,64,129,250}, Hq=Hkv=4, D=64, non-causal", [17, 64, 129, 250], 4, 4, 64,
+         torch.float32, False, 0, False),
+        ("C2", "bf16 ragged: 32 seqs, L ~ U[256,4096] (seeded), Hq=Hkv=16, D=64, non-causal", c2_lens, 16, 16, 64,
+         torch.bfloat16, False, 0, False),
+        ("C4", "bf16 4x16384, Hq=32, Hkv=8, D=128, causal, window 4096, fp32 bias [65536,1,16384] = -(i-j)/16",
+         [16384] * 4, 32, 8, 128, torch.bfloat16, True, 4096, True),
+    ]
+    out = {}
+    for name, desc, lens, hq, hkv, d, dt, causal, window, with_bias in cfgs:
+        g = torch.Generator(device="cuda").manual_seed(args.seed + 7)
+        T = sum(lens)
+        q = torch.randn(T, hq, d, device="cuda", generator=g).to(dt)
+        k = torch.randn(T, hkv, d, device="cuda", generator=g).to(dt)
+        v = torch.randn(T, hkv, d, device="cuda", generator=g).to(dt)
+        do = torch.randn(T, hq, d, device="cuda", generator=g).to(dt)
+        cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device="cuda")
+        bias = None
+        if with_bias:
+            L = lens[0]
+            i = torch.arange(L, device="cuda")[:, None]
+            j = torch.arange(L, device="cuda")[None, :]
+            blk = torch.where(j <= i, -(i - j).float() / 16.0, torch.zeros((), device="cuda"))
+            bias = blk.unsqueeze(1).repeat(len(lens), 1, 1)
+            del i, j, blk
+        lse = torch.empty(T, hq, dtype=torch.float32, device="cuda")
+        scale = 1.0 / math.sqrt(d)
+        max_q = max(lens)
+        st = {}
+
+        def step():
+            st["o"] = C.varlen_attention(q, k, v, cu, cu, max_q, scale, causal, window, lse, bias)
+            st["g"] = C.varlen_attention_bwd(q, k, v, st["o"], do, lse, cu, cu, scale, causal, window, bias)
+
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        n = max(3, args.steps // 4)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / n
+        pairs = _attended_pairs(lens, causal, window)
+        flops = 14.0 * d * hq * pairs
+        tf = flops / (ms * 1e-3) / 1e12
+        peak = PEAK_FP32_TFLOPS if dt == torch.float32 else PEAK_BF16_TFLOPS
+        out[name] = {"workload": desc, "ms_per_step": round(ms, 4), "tflops": round(tf, 2),
+                     "frac_of_peak": round(tf / peak, 4), "peak_tflops": peak, "attended_pairs_per_head": pairs,
+                     "steps": n, "dtype": "fp32" if dt == torch.float32 else "bf16"}
+        del q, k, v, do, bias, lse, st
+        torch.cuda.empty_cache()
+    return out
 
 
 def c5_inputs(seed):
@@ -265,6 +345,7 @@ def main():
         return
     c3 = bench_c3(args)
     dec = None if args.no_decode else bench_c5(args)
+    others = None if args.no_configs else bench_configs(args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.seed)
     km, algo = c3["kern_ms"], c3["algo_flop"]
     dom = max(km, key=km.get)
@@ -297,6 +378,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(dec["GBps"], 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(dec["GBps"] / PEAK_HBM_GBS, 4)},
             "outputs_finite": dec["finite"]},
+        "other_configs": others,
         "outputs_finite": c3["finite"],
         "cpu_baseline": cpu,
     }
