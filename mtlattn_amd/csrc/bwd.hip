@@ -66,9 +66,10 @@ __device__ inline void store4(void* base, int64_t off, float a, float b, float c
 // HBM into a 3-deep LDS ring (K and V row-major, swizzled); K^T operands of
 // the dQ product are transposed LDS reads of the same K tile.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool BIAS, bool OUT_F32>
+// D is the tile width (64 or 128) and DV <= D the head dim, as in the forward.
+template <typename T, int D, int DV, bool BIAS, bool OUT_F32>
 __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
-    constexpr int DC = D / 16, DB = D / 32;
+    constexpr int DC = (DV + 15) / 16, DB = (DV + 31) / 32;
     constexpr int TILE = kKT * D * 2;
     constexpr int STAGE = 2 * TILE;           // K, V
     constexpr int NBUF = 3;
@@ -107,12 +108,13 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     // B operands: Q^T and dO^T fragments (lane = query, d = 16 kc + 8 hi + j).
     u32x4_t qf[DC], df[DC];
     {
-        const uint16_t* qp = p.q + grow * p.q_rs + (int64_t)head * D + 8 * hi;
-        const uint16_t* dp = p.dout + grow * p.do_rs + (int64_t)head * D + 8 * hi;
+        const uint16_t* qp = p.q + grow * p.q_rs + (int64_t)head * DV + 8 * hi;
+        const uint16_t* dp = p.dout + grow * p.do_rs + (int64_t)head * DV + 8 * hi;
 #pragma unroll
         for (int kc = 0; kc < DC; ++kc) {
-            qf[kc] = ld16(qp + 16 * kc);
-            df[kc] = ld16(dp + 16 * kc);
+            const bool in = DV % 16 == 0 || 16 * kc + 8 * hi < DV;    // columns past DV are zero
+            qf[kc] = in ? ld16(qp + 16 * kc) : u32x4_t{};
+            df[kc] = in ? ld16(dp + 16 * kc) : u32x4_t{};
         }
     }
     float lse2 = kPosInf, dlt = 0.f;
@@ -137,13 +139,13 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         kv_lo = (kv_lo / kKT) * kKT;
     }
     const int n_kv_tiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kKT - 1) / kKT : 0;
-    const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * D;
-    const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * D;
+    const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * DV;
+    const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * DV;
     auto stage = [&](int it) {
         char* buf = smem + (it % NBUF) * STAGE;
         const int kt = kv_lo + it * kKT;
-        stage_tile<D, kKT, kWaves>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
-        stage_tile<D, kKT, kWaves>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
+        stage_tile<D, kKT, kWaves, DV>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
+        stage_tile<D, kKT, kWaves, DV>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
     };
 
     const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
@@ -241,12 +243,13 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     }
 
     if (wave_active && row_ok) {
-        const int64_t off = grow * ((int64_t)p.hq * D) + (int64_t)head * D;
+        const int64_t off = grow * ((int64_t)p.hq * DV) + (int64_t)head * DV;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
                 const int d = 32 * db + 8 * rg + 4 * hi;
+                if (DV % 32 != 0 && d >= DV) continue;
                 store4<T, OUT_F32>(p.dq, off + d, dqacc[db][4 * rg] * p.scale, dqacc[db][4 * rg + 1] * p.scale,
                                    dqacc[db][4 * rg + 2] * p.scale, dqacc[db][4 * rg + 3] * p.scale);
             }
@@ -269,9 +272,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
 // dO^T operands are transposed LDS reads. The loop covers the g heads of the
 // group, so the GQA reduction of dK/dV happens in registers.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool BIAS, bool OUT_F32>
+template <typename T, int D, int DV, bool BIAS, bool OUT_F32>
 __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
-    constexpr int DC = D / 16, DB = D / 32;
+    constexpr int DC = (DV + 15) / 16, DB = (DV + 31) / 32;
     constexpr int NP = kWaves / 2;                      // wave pairs
     constexpr int KB = NP * kKW;                        // keys per workgroup
     constexpr int TILE = kQT * D * 2;
@@ -311,9 +314,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     {
         const int64_t grow = kr.start + min(key, kv_len - 1);     // masked past the end
         const uint16_t* kp = role_a ? p.k + grow * p.k_rs : p.v + grow * p.v_rs;
-        kp += (int64_t)hk * D + 8 * hi;
+        kp += (int64_t)hk * DV + 8 * hi;
 #pragma unroll
-        for (int kc = 0; kc < DC; ++kc) kvf[kc] = ld16(kp + 16 * kc);
+        for (int kc = 0; kc < DC; ++kc)     // columns past DV are zero
+            kvf[kc] = (DV % 16 == 0 || 16 * kc + 8 * hi < DV) ? ld16(kp + 16 * kc) : u32x4_t{};
     }
 
     // Query range that can see any key of this workgroup.
@@ -338,16 +342,16 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         char* buf = smem + (st % NBUF) * STAGE;
         const int h = stage_head(st);
         const int qt = stage_q0(st);
-        const int64_t hoff = (int64_t)qr.start * p.q_rs + (int64_t)h * D;
+        const int64_t hoff = (int64_t)qr.start * p.q_rs + (int64_t)h * DV;
         // Without a bias the A waves issue the tile loads: wave B, one stage
         // behind, is the longer of the two and should not stall on issue.
         // With a bias the A waves keep their own bias loads in flight, and
         // the wait for those would also cover tile loads issued after them,
         // so the B waves load the tiles.
         if (ldw >= 0) {
-            stage_tile<D, kQT, NP>(buf, p.q + hoff, p.q_rs, qt, q_len, ldw, lane);
-            stage_tile<D, kQT, NP>(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * D, p.do_rs, qt,
-                                   q_len, ldw, lane);
+            stage_tile<D, kQT, NP, DV>(buf, p.q + hoff, p.q_rs, qt, q_len, ldw, lane);
+            stage_tile<D, kQT, NP, DV>(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * DV, p.do_rs,
+                                       qt, q_len, ldw, lane);
         }
         if (ldw == 0 || ldw == 1) {
             const int q = min(qt + lane, q_len - 1);        // rows past the end are masked
@@ -528,7 +532,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     }
 
     if (pair_active && key_ok) {
-        const int64_t off = (int64_t)(kr.start + key) * ((int64_t)p.hkv * D) + (int64_t)hk * D;
+        const int64_t off = (int64_t)(kr.start + key) * ((int64_t)p.hkv * DV) + (int64_t)hk * DV;
         void* dst = role_a ? p.dv : p.dk;
         const float sc = role_a ? 1.f : p.scale;
 #pragma unroll
@@ -536,6 +540,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
                 const int d = 32 * db + 8 * rg + 4 * hi;
+                if (DV % 32 != 0 && d >= DV) continue;
                 store4<T, OUT_F32>(dst, off + d, acc[db][4 * rg] * sc, acc[db][4 * rg + 1] * sc,
                                    acc[db][4 * rg + 2] * sc, acc[db][4 * rg + 3] * sc);
             }
@@ -625,7 +630,7 @@ BwdKParams make_params(const BwdArgs& a) {
     return p;
 }
 
-template <typename T, int D, bool OUT_F32>
+template <typename T, int D, int DV, bool OUT_F32>
 hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     constexpr int NW = kWaves;
     BwdKParams p = make_params(a);
@@ -636,13 +641,13 @@ hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     const int64_t blocks = (int64_t)p.n_tiles * p.n_hg;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (a.geo.bias != nullptr)
-        hipLaunchKernelGGL((bwd_dq_kernel<T, D, true, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, p);
+        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, true, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, p);
     else
-        hipLaunchKernelGGL((bwd_dq_kernel<T, D, false, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, p);
+        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, false, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, p);
     return hipGetLastError();
 }
 
-template <typename T, int D, bool OUT_F32>
+template <typename T, int D, int DV, bool OUT_F32>
 hipError_t launch_dkv_typed(const BwdArgs& a, hipStream_t st) {
     BwdKParams p = make_params(a);
     constexpr int NW = kWaves;
@@ -650,9 +655,11 @@ hipError_t launch_dkv_typed(const BwdArgs& a, hipStream_t st) {
     const int64_t blocks = (int64_t)p.n_tiles * a.geo.hkv;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (a.geo.bias != nullptr)
-        hipLaunchKernelGGL((bwd_dkv_kernel<T, D, true, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, p);
+        hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, true, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st,
+                           p);
     else
-        hipLaunchKernelGGL((bwd_dkv_kernel<T, D, false, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, p);
+        hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, false, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st,
+                           p);
     return hipGetLastError();
 }
 
@@ -696,29 +703,37 @@ hipError_t launch_zero_outside(void* ptr, int64_t row_bytes, int64_t total_rows,
     return hipGetLastError();
 }
 
-hipError_t launch_bwd_dq_mfma(int dtype, const BwdArgs& a, hipStream_t st) {
-    const int d = a.geo.d;
+// the tile width and head dim of each supported head dim (see the forward)
+template <typename T, template <typename, int, int, bool> class L>
+hipError_t dispatch_dims(const BwdArgs& a, hipStream_t st) {
     const bool f = a.out_f32 != 0;
-    if (dtype == MTLATTN_DTYPE_BF16) {
-        if (d == 128) return f ? launch_dq_typed<BF16, 128, true>(a, st) : launch_dq_typed<BF16, 128, false>(a, st);
-        if (d == 64) return f ? launch_dq_typed<BF16, 64, true>(a, st) : launch_dq_typed<BF16, 64, false>(a, st);
-    } else if (dtype == MTLATTN_DTYPE_F16) {
-        if (d == 128) return f ? launch_dq_typed<F16, 128, true>(a, st) : launch_dq_typed<F16, 128, false>(a, st);
-        if (d == 64) return f ? launch_dq_typed<F16, 64, true>(a, st) : launch_dq_typed<F16, 64, false>(a, st);
+    switch (a.geo.d) {
+        case 64: return f ? L<T, 64, 64, true>::run(a, st) : L<T, 64, 64, false>::run(a, st);
+        case 80: return f ? L<T, 128, 80, true>::run(a, st) : L<T, 128, 80, false>::run(a, st);
+        case 88: return f ? L<T, 128, 88, true>::run(a, st) : L<T, 128, 88, false>::run(a, st);
+        case 96: return f ? L<T, 128, 96, true>::run(a, st) : L<T, 128, 96, false>::run(a, st);
+        case 128: return f ? L<T, 128, 128, true>::run(a, st) : L<T, 128, 128, false>::run(a, st);
+        default: return hipErrorInvalidValue;
     }
+}
+template <typename T, int D, int DV, bool F>
+struct DqLaunch {
+    static hipError_t run(const BwdArgs& a, hipStream_t st) { return launch_dq_typed<T, D, DV, F>(a, st); }
+};
+template <typename T, int D, int DV, bool F>
+struct DkvLaunch {
+    static hipError_t run(const BwdArgs& a, hipStream_t st) { return launch_dkv_typed<T, D, DV, F>(a, st); }
+};
+
+hipError_t launch_bwd_dq_mfma(int dtype, const BwdArgs& a, hipStream_t st) {
+    if (dtype == MTLATTN_DTYPE_BF16) return dispatch_dims<BF16, DqLaunch>(a, st);
+    if (dtype == MTLATTN_DTYPE_F16) return dispatch_dims<F16, DqLaunch>(a, st);
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_bwd_dkv_mfma(int dtype, const BwdArgs& a, hipStream_t st) {
-    const int d = a.geo.d;
-    const bool f = a.out_f32 != 0;
-    if (dtype == MTLATTN_DTYPE_BF16) {
-        if (d == 128) return f ? launch_dkv_typed<BF16, 128, true>(a, st) : launch_dkv_typed<BF16, 128, false>(a, st);
-        if (d == 64) return f ? launch_dkv_typed<BF16, 64, true>(a, st) : launch_dkv_typed<BF16, 64, false>(a, st);
-    } else if (dtype == MTLATTN_DTYPE_F16) {
-        if (d == 128) return f ? launch_dkv_typed<F16, 128, true>(a, st) : launch_dkv_typed<F16, 128, false>(a, st);
-        if (d == 64) return f ? launch_dkv_typed<F16, 64, true>(a, st) : launch_dkv_typed<F16, 64, false>(a, st);
-    }
+    if (dtype == MTLATTN_DTYPE_BF16) return dispatch_dims<BF16, DkvLaunch>(a, st);
+    if (dtype == MTLATTN_DTYPE_F16) return dispatch_dims<F16, DkvLaunch>(a, st);
     return hipErrorInvalidValue;
 }
 

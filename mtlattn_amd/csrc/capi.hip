@@ -125,7 +125,7 @@ int decode_heads_per_group(int g, int max_q) {
 
 // Split-KV applicability without the routing heuristics (kernel limits).
 bool splitkv_supported(const mtlattn_problem* p) {
-    return is16(p->dtype) && mfma_head_dim(p->head_dim) && p->bias == nullptr && p->window <= 0 &&
+    return is16(p->dtype) && decode_head_dim(p->head_dim) && p->bias == nullptr && p->window <= 0 &&
            p->max_seqlen_q >= 1 && p->max_seqlen_q <= 16;
 }
 
@@ -364,7 +364,7 @@ int mtlattn_attn_splitkv(const mtlattn_problem* p, const void* q, int64_t q_row_
     int rc = check_problem(p);
     if (rc != MTLATTN_OK) return rc;
     if (!is16(p->dtype)) return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: half/bf16");
-    if (!mfma_head_dim(p->head_dim)) return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: D in {64,128}");
+    if (!decode_head_dim(p->head_dim)) return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: D in {64,128}");
     if (p->bias != nullptr || p->window > 0)
         return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: no attn_mask or window on the split-KV path");
     if (p->max_seqlen_q < 1 || p->max_seqlen_q > 16)

@@ -214,16 +214,20 @@ __device__ inline void lds_dma4(const void* gptr, const char* lds) {
 // lane loads the global chunk that the swizzle maps to that LDS position.
 // Rows >= row_end read row row_end - 1 (finite data the kernels mask out).
 // NW waves share the ROWS * D * 2 / 1024 instructions; w must be uniform.
-template <int D, int ROWS, int NW>
+// Rows of the source hold DV <= D values (head dims below the tile width):
+// chunks at or past DV / 8 repeat the row's last valid chunk (finite data
+// that the kernels' zero operand columns or discarded outputs never use).
+template <int D, int ROWS, int NW, int DV = D>
 __device__ inline void stage_tile(char* tile, const uint16_t* base, int64_t rs, int row0, int row_end, int w,
                                   int lane) {
+    static_assert(DV % 8 == 0 && DV <= D, "head dim");
     constexpr int PER = ROWS * D * 2 / 1024;
     static_assert(ROWS * D * 2 % 1024 == 0, "tile must be a multiple of 1 KB");
 #pragma unroll
     for (int i = w; i < PER; i += NW) {
         const int byte = i * 1024 + lane * 16;
         const int row = byte / (2 * D);
-        const int chunk = ((byte % (2 * D)) >> 4) ^ row_swz<D>(row);
+        const int chunk = min(((byte % (2 * D)) >> 4) ^ row_swz<D>(row), DV / 8 - 1);
         const int grow = min(row0 + row, row_end - 1);
         lds_dma16(base + (int64_t)grow * rs + chunk * 8, tile + i * 1024);
     }

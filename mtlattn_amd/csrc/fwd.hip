@@ -48,11 +48,15 @@ struct FwdKParams {
 // GENERAL = explicit per-element logit scaling, with the optional bias; the
 // fast variant (no bias, scale > 0) reduces raw scores and folds the scale
 // into one FMA per element.
-template <typename T, int D, bool GENERAL>
+// D is the tile width (64 or 128), DV <= D the head dim (a multiple of 8):
+// contractions over d use the DV / 16 (rounded up) chunks that hold data,
+// with Q's columns past DV zero; P.V computes ceil(DV / 32) output blocks and
+// stores the DV valid columns.
+template <typename T, int D, int DV, bool GENERAL>
 __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     constexpr bool BIAS = GENERAL;
-    constexpr int DC = D / 16;               // MFMA k-chunks over D
-    constexpr int DB = D / 32;               // 32-row output blocks over D
+    constexpr int DC = (DV + 15) / 16;       // MFMA k-chunks over the head dim
+    constexpr int DB = (DV + 31) / 32;       // 32-row output blocks
     constexpr int TILE = kKT * D * 2;        // bytes of one K or V tile
     constexpr int STAGE = 2 * TILE;          // K tile + V tile, both row-major
     constexpr int NBUF = 3;                  // ring of staged key tiles
@@ -88,9 +92,10 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     u32x4_t qf[DC];
     {
         const int row = min(qa + l32, q_len - 1);
-        const uint16_t* qp = p.q + (int64_t)(qr.start + row) * p.q_rs + (int64_t)head * D + 8 * hi;
+        const uint16_t* qp = p.q + (int64_t)(qr.start + row) * p.q_rs + (int64_t)head * DV + 8 * hi;
 #pragma unroll
-        for (int kc = 0; kc < DC; ++kc) qf[kc] = ld16(qp + 16 * kc);
+        for (int kc = 0; kc < DC; ++kc)
+            qf[kc] = (DV % 16 == 0 || 16 * kc + 8 * hi < DV) ? ld16(qp + 16 * kc) : u32x4_t{};
         // settle the fragments here: the key loop's own wait counts cover
         // only the staging loads
         wait_vmcnt<0>();
@@ -106,14 +111,14 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     }
     const int n_kv_tiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kKT - 1) / kKT : 0;
 
-    const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * D;
-    const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * D;
+    const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * DV;
+    const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * DV;
     // All 8 waves stage each tile straight from HBM into LDS (K then V).
     auto stage = [&](int it) {
         char* buf = smem + (it % NBUF) * STAGE;
         const int kt = kv_lo + it * kKT;
-        stage_tile<D, kKT, kWaves>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
-        stage_tile<D, kKT, kWaves>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
+        stage_tile<D, kKT, kWaves, DV>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
+        stage_tile<D, kKT, kWaves, DV>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
     };
 
     // per-lane LDS offsets: K operand rows 32 kb + l32 (chunk 2 kc + hi) and
@@ -275,12 +280,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     const float lt = pair_sum(l_run);
     if (wave_active && qrow < q_len) {
         const float inv = lt > 0.f ? 1.f / lt : 0.f;
-        uint16_t* op = p.o + (int64_t)(qr.start + qrow) * ((int64_t)p.hq * D) + (int64_t)head * D;
+        uint16_t* op = p.o + (int64_t)(qr.start + qrow) * ((int64_t)p.hq * DV) + (int64_t)head * DV;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
                 const int d = 32 * db + 8 * rg + 4 * hi;
+                if (DV % 32 != 0 && d >= DV) continue;
                 st8(op + d, u32x2_t{T::pack2(oacc[db][4 * rg + 0] * inv, oacc[db][4 * rg + 1] * inv),
                                     T::pack2(oacc[db][4 * rg + 2] * inv, oacc[db][4 * rg + 3] * inv)});
             }
@@ -292,7 +298,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
 
 int gcd_int(int a, int b) { while (b) { const int t = a % b; a = b; b = t; } return a; }
 
-template <typename T, int D>
+template <typename T, int D, int DV>
 hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     const Geometry& g = a.geo;
     FwdKParams p;
@@ -314,23 +320,29 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     if (blocks <= 0) return hipSuccess;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (g.bias != nullptr || !(p.scale_log2 > 0.f))
-        hipLaunchKernelGGL((fwd_mfma_kernel<T, D, true>), dim3((unsigned)blocks), dim3(kThreads), 0, st, p);
+        hipLaunchKernelGGL((fwd_mfma_kernel<T, D, DV, true>), dim3((unsigned)blocks), dim3(kThreads), 0, st, p);
     else
-        hipLaunchKernelGGL((fwd_mfma_kernel<T, D, false>), dim3((unsigned)blocks), dim3(kThreads), 0, st, p);
+        hipLaunchKernelGGL((fwd_mfma_kernel<T, D, DV, false>), dim3((unsigned)blocks), dim3(kThreads), 0, st, p);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_fwd_mfma(int dtype, const FwdArgs& a, hipStream_t st) {
-    const int d = a.geo.d;
-    if (dtype == MTLATTN_DTYPE_BF16) {
-        if (d == 128) return launch_typed<BF16, 128>(a, st);
-        if (d == 64) return launch_typed<BF16, 64>(a, st);
-    } else if (dtype == MTLATTN_DTYPE_F16) {
-        if (d == 128) return launch_typed<F16, 128>(a, st);
-        if (d == 64) return launch_typed<F16, 64>(a, st);
+template <typename T>
+hipError_t launch_dims(const FwdArgs& a, hipStream_t st) {
+    switch (a.geo.d) {
+        case 64: return launch_typed<T, 64, 64>(a, st);
+        case 80: return launch_typed<T, 128, 80>(a, st);
+        case 88: return launch_typed<T, 128, 88>(a, st);
+        case 96: return launch_typed<T, 128, 96>(a, st);
+        case 128: return launch_typed<T, 128, 128>(a, st);
+        default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_fwd_mfma(int dtype, const FwdArgs& a, hipStream_t st) {
+    if (dtype == MTLATTN_DTYPE_BF16) return launch_dims<BF16>(a, st);
+    if (dtype == MTLATTN_DTYPE_F16) return launch_dims<F16>(a, st);
     return hipErrorInvalidValue;
 }
 

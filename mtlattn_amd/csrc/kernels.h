@@ -78,6 +78,10 @@ inline int64_t decode_workspace_rows(int64_t total_kv, int num_seqs, int hkv, in
 }
 
 // Which head dims have MFMA kernels.
-inline bool mfma_head_dim(int d) { return d == 64 || d == 128; }
+// head dims of the matrix-core flash kernels (fp16/bf16): 64 and 128 native,
+// 80, 88, 96 on the 128-wide tile with the spare columns unused
+inline bool mfma_head_dim(int d) { return d == 64 || d == 80 || d == 88 || d == 96 || d == 128; }
+// head dims of the split-KV decode kernels
+inline bool decode_head_dim(int d) { return d == 64 || d == 128; }
 
 }  // namespace mtlattn

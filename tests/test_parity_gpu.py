@@ -168,7 +168,7 @@ def test_single_16384(mt):
     assert err < 5e-3
 
 
-# MFMA head dims 64/128 + generic 80/88/96 (tests/test_correctness.py:332-343)
+# head dims 64/80/88/96/128 (matrix-core kernels; tests/test_correctness.py:332-343)
 def test_mfma_d64(mt):
     _fwd(mt, "D=64 full", [2048], [2048], 12, 12, 64, torch.float16)
     _fwd(mt, "D=64 causal", [4096], [4096], 12, 12, 64, torch.float16, causal=True)
@@ -184,6 +184,21 @@ def test_generic_head_dims(mt):
     _fwd(mt, "D=88", [2048], [2048], 8, 8, 88, torch.float16)
     _fwd(mt, "D=88 bf16 causal", [1500], [1500], 8, 8, 88, torch.bfloat16, causal=True)
     _fwd(mt, "D=80 ragged causal", [200, 700], [200, 700], 8, 8, 80, torch.float16, causal=True)
+
+
+def test_mfma_padded_head_dims(mt):
+    """Head dims 80/88/96 run the matrix-core kernels on the 128-wide tile
+    (operand columns past D zero, output columns past D dropped)."""
+    b, h = torch.bfloat16, torch.float16
+    for D in (80, 88, 96):
+        _fwd(mt, f"D={D} bf16 GQA causal ragged", [300, 77, 513], [300, 77, 513], 16, 4, D, b, causal=True)
+        _fwd(mt, f"D={D} fp16 cross window", [64, 200], [333, 260], 8, 2, D, h, causal=True, window=100)
+        _bwd(mt, f"bwd D={D} bf16 GQA ragged", [200, 91, 333], [200, 91, 333], 12, 4, D, b, 4e-2, causal=True)
+        _bwd(mt, f"bwd D={D} fp16 window cross", [150], [410], 8, 8, D, h, 6e-3, causal=True, window=90)
+        _bwd(mt, f"bwd D={D} fp16 per-head bias", [640], [640], 8, 4, D, h, 6e-3,
+             bias=_make_bias(640, 8, 640, False))
+        _bwd(mt, f"bwd D={D} bf16 broadcast bias causal", [512], [512], 8, 8, D, b, 4e-2, causal=True,
+             bias=_make_bias(512, 8, 512, True))
 
 
 def test_large_head_dims(mt):
@@ -461,18 +476,19 @@ def test_determinism(mt):
         assert torch.equal(a, b)
 
 
-def test_mfma_matches_generic(mt):
+@pytest.mark.parametrize("D", [128, 88])
+def test_mfma_matches_generic(mt, D):
     """The MFMA kernels and the portable kernels agree (both vs the oracle too)."""
     import subprocess
     import sys
-    _banner("MFMA vs generic path (subprocess with MTLATTN_NO_MFMA=1)")
+    _banner(f"MFMA vs generic path D={D} (subprocess with MTLATTN_NO_MFMA=1)")
     code = (
         "import torch, mtlattn, math, sys\n"
         "sys.path.insert(0, '.')\n"
         "from tests.helpers import cu_of, randn\n"
         "g = torch.Generator().manual_seed(4)\n"
         "lens=[100,257,31]\n"
-        "q=randn((388,8,128),torch.float16,g).cuda(); k=randn((388,4,128),torch.float16,g).cuda(); v=randn((388,4,128),torch.float16,g).cuda()\n"
+        f"q=randn((388,8,{D}),torch.float16,g).cuda(); k=randn((388,4,{D}),torch.float16,g).cuda(); v=randn((388,4,{D}),torch.float16,g).cuda()\n"
         "cu=cu_of(lens,'cuda')\n"
         "o=mtlattn.varlen_attention(q,k,v,cu,cu,257,causal=True,window=50)\n"
         "torch.save(o.cpu(), sys.argv[1])\n")
