@@ -173,10 +173,13 @@ __device__ inline float pair_sum(float x) {
 // Direct-load writes (global_load_lds_dwordx4) are 1 KB contiguous per
 // instruction and conflict free under any swizzle.
 // ---------------------------------------------------------------------------
+// D = 256 (512-byte rows, each covering the banks twice): the D = 128
+// swizzle on the low 4 chunk bits; both access patterns only constrain a
+// chunk's bank group, chunk & 15.
 template <int D>
 __device__ inline int row_swz(int row) {
-    static_assert(D == 64 || D == 128, "swizzled tiles are defined for D = 64 and 128");
-    return D == 128 ? (((row & 3) << 2) | ((row >> 2) & 3)) : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
+    static_assert(D == 64 || D == 128 || D == 256, "swizzled tiles are defined for D = 64, 128 and 256");
+    return D != 64 ? (((row & 3) << 2) | ((row >> 2) & 3)) : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
 }
 
 template <int D>
@@ -264,8 +267,8 @@ __device__ inline const char* opaque(const char* p) {
     asm volatile("" : "+v"(v));
     return (const char*)(const __attribute__((address_space(3))) char*)(uintptr_t)v;
 }
-// p ^ x on an LDS address (x < 256; tiles start on 256-byte boundaries, so
-// this XORs the within-row byte offset).
+// p ^ x on an LDS address (x below the row size, 512 bytes at most; tiles
+// start on row-size boundaries, so this XORs the within-row byte offset).
 __device__ inline const char* lds_xor(const char* p, uint32_t x) {
     const uint32_t v = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
     return (const char*)(const __attribute__((address_space(3))) char*)(uintptr_t)(v ^ x);

@@ -43,24 +43,30 @@ struct FwdKParams {
     float scale_log2;
     int causal, window;
     int bias_v4;      // bias rows 16-byte aligned (pointer and strides)
+    int col0;         // first output (and V) column of this launch
 };
 
 // GENERAL = explicit per-element logit scaling, with the optional bias; the
 // fast variant (no bias, scale > 0) reduces raw scores and folds the scale
 // into one FMA per element.
-// D is the tile width (64 or 128), DV <= D the head dim (a multiple of 8):
-// contractions over d use the DV / 16 (rounded up) chunks that hold data,
-// with Q's columns past DV zero; P.V computes ceil(DV / 32) output blocks and
-// stores the DV valid columns.
-template <typename T, int D, int DV, bool GENERAL>
+// DV is the head dim (a multiple of 8). K tiles are DK wide (64, 128 or 256
+// >= DV): the S contraction uses ceil(DV / 16) k-chunks, Q's columns past DV
+// are zero. V tiles hold the DO columns [col0, col0 + DO) that this launch
+// outputs, DVL wide (64 or 128 >= DO); P.V computes ceil(DO / 32) output
+// blocks and stores the DO valid columns. Head dims above 128 run as two
+// launches that each produce half of the output columns (the S products are
+// recomputed; their accumulators would not fit otherwise).
+template <typename T, int DK, int DV, int DVL, int DO, bool GENERAL>
 __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     constexpr bool BIAS = GENERAL;
     constexpr int DC = (DV + 15) / 16;       // MFMA k-chunks over the head dim
-    constexpr int DB = (DV + 31) / 32;       // 32-row output blocks
-    constexpr int TILE = kKT * D * 2;        // bytes of one K or V tile
-    constexpr int STAGE = 2 * TILE;          // K tile + V tile, both row-major
+    constexpr int DB = (DO + 31) / 32;       // 32-row output blocks
+    constexpr int KTILE = kKT * DK * 2;      // bytes of one K tile
+    constexpr int VTILE = kKT * DVL * 2;     // bytes of one V tile
+    constexpr int STAGE = KTILE + VTILE;     // K tile + V tile, both row-major
     constexpr int NBUF = 3;                  // ring of staged key tiles
     constexpr int LOADS = STAGE / 1024 / kWaves;   // direct loads per wave per tile
+    static_assert(LOADS <= 15 && STAGE % (1024 * kWaves) == 0, "staging");
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -112,18 +118,18 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     const int n_kv_tiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kKT - 1) / kKT : 0;
 
     const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * DV;
-    const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * DV;
+    const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * DV + p.col0;
     // All 8 waves stage each tile straight from HBM into LDS (K then V).
     auto stage = [&](int it) {
         char* buf = smem + (it % NBUF) * STAGE;
         const int kt = kv_lo + it * kKT;
-        stage_tile<D, kKT, kWaves, DV>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
-        stage_tile<D, kKT, kWaves, DV>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
+        stage_tile<DK, kKT, kWaves, DV>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
+        stage_tile<DVL, kKT, kWaves, DO>(buf + KTILE, vbase, p.v_rs, kt, kv_len, w, lane);
     };
 
     // per-lane LDS offsets: K operand rows 32 kb + l32 (chunk 2 kc + hi) and
     // the transposed V^T operand reads
-    const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
+    const uint32_t rbase = row_base<DK>(l32, hi), tbase = tr_base<DVL>(lane);
 
     float m_run = kNegInf, l_run = 0.f;
     f32x16_t oacc[DB];
@@ -186,13 +192,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
                           ((p.window > 0) & (kt + kKT - 1 < qa + coff - p.window + 1));
         const char* Ks = smem + (it % NBUF) * STAGE;
         const char* kb_ = opaque(Ks + rbase);
-        const char* vtb = opaque(Ks + TILE + tbase);
+        const char* vtb = opaque(Ks + KTILE + tbase);
         f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
 #pragma unroll
         for (int kc = 0; kc < DC; ++kc) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                const u32x4_t a = row_operand<D>(kb_, kc, 32 * kb);
+                const u32x4_t a = row_operand<DK>(kb_, kc, 32 * kb);
                 sacc[kb] = mfma32<T>(a, qf[kc], sacc[kb]);
             }
         }
@@ -272,7 +278,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         for (int c = 0; c < 4; ++c) {
 #pragma unroll
             for (int db = 0; db < DB; ++db)
-                oacc[db] = mfma32<T>(tr_operand<D>(vtb, c, db), pf[c], oacc[db]);
+                oacc[db] = mfma32<T>(tr_operand<DVL>(vtb, c, db), pf[c], oacc[db]);
         }
     }
 
@@ -280,13 +286,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     const float lt = pair_sum(l_run);
     if (wave_active && qrow < q_len) {
         const float inv = lt > 0.f ? 1.f / lt : 0.f;
-        uint16_t* op = p.o + (int64_t)(qr.start + qrow) * ((int64_t)p.hq * DV) + (int64_t)head * DV;
+        uint16_t* op = p.o + (int64_t)(qr.start + qrow) * ((int64_t)p.hq * DV) + (int64_t)head * DV + p.col0;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
                 const int d = 32 * db + 8 * rg + 4 * hi;
-                if (DV % 32 != 0 && d >= DV) continue;
+                if (DO % 32 != 0 && d >= DO) continue;
                 st8(op + d, u32x2_t{T::pack2(oacc[db][4 * rg + 0] * inv, oacc[db][4 * rg + 1] * inv),
                                     T::pack2(oacc[db][4 * rg + 2] * inv, oacc[db][4 * rg + 3] * inv)});
             }
@@ -298,7 +304,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
 
 int gcd_int(int a, int b) { while (b) { const int t = a % b; a = b; b = t; } return a; }
 
-template <typename T, int D, int DV>
+template <typename T, int DK, int DV, int DVL, int DO>
 hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     const Geometry& g = a.geo;
     FwdKParams p;
@@ -319,10 +325,17 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     const int64_t blocks = (int64_t)p.n_tiles * p.n_hg;
     if (blocks <= 0) return hipSuccess;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    if (g.bias != nullptr || !(p.scale_log2 > 0.f))
-        hipLaunchKernelGGL((fwd_mfma_kernel<T, D, DV, true>), dim3((unsigned)blocks), dim3(kThreads), 0, st, p);
-    else
-        hipLaunchKernelGGL((fwd_mfma_kernel<T, D, DV, false>), dim3((unsigned)blocks), dim3(kThreads), 0, st, p);
+    // DO < DV: one launch per DO-column slice; the first writes the LSE
+    for (int c0 = 0; c0 < DV; c0 += DO) {
+        p.col0 = c0;
+        p.lse = c0 == 0 ? a.lse : nullptr;
+        if (g.bias != nullptr || !(p.scale_log2 > 0.f))
+            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, true>), dim3((unsigned)blocks), dim3(kThreads), 0,
+                               st, p);
+        else
+            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, false>), dim3((unsigned)blocks), dim3(kThreads), 0,
+                               st, p);
+    }
     return hipGetLastError();
 }
 
@@ -331,11 +344,13 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
 template <typename T>
 hipError_t launch_dims(const FwdArgs& a, hipStream_t st) {
     switch (a.geo.d) {
-        case 64: return launch_typed<T, 64, 64>(a, st);
-        case 80: return launch_typed<T, 128, 80>(a, st);
-        case 88: return launch_typed<T, 128, 88>(a, st);
-        case 96: return launch_typed<T, 128, 96>(a, st);
-        case 128: return launch_typed<T, 128, 128>(a, st);
+        case 64: return launch_typed<T, 64, 64, 64, 64>(a, st);
+        case 80: return launch_typed<T, 128, 80, 128, 80>(a, st);
+        case 88: return launch_typed<T, 128, 88, 128, 88>(a, st);
+        case 96: return launch_typed<T, 128, 96, 128, 96>(a, st);
+        case 128: return launch_typed<T, 128, 128, 128, 128>(a, st);
+        case 160: return launch_typed<T, 256, 160, 128, 80>(a, st);
+        case 256: return launch_typed<T, 256, 256, 128, 128>(a, st);
         default: return hipErrorInvalidValue;
     }
 }
