@@ -32,8 +32,6 @@ namespace {
 
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kKT = 64;   // dQ: keys per tile
-constexpr int kQT = 64;   // dK/dV: queries per tile
 constexpr int kKW = 32;   // dK/dV: keys per wave
 
 struct BwdKParams {
@@ -66,11 +64,16 @@ __device__ inline void store4(void* base, int64_t off, float a, float b, float c
 // HBM into a 3-deep LDS ring (K and V row-major, swizzled); K^T operands of
 // the dQ product are transposed LDS reads of the same K tile.
 // ---------------------------------------------------------------------------
-// D is the tile width (64 or 128) and DV <= D the head dim, as in the forward.
-template <typename T, int D, int DV, bool BIAS, bool OUT_F32>
+// D is the tile width (64, 128 or 256) and DV <= D the head dim, as in the
+// forward. This launch outputs the DO columns from C0 (head dims above 128
+// take several launches, the S and dP products recomputed in each: their
+// accumulators would not fit otherwise). Key tiles hold 32 * KB keys.
+template <typename T, int D, int DV, int DO, int C0, int KB, bool BIAS, bool OUT_F32>
 __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
-    constexpr int DC = (DV + 15) / 16, DB = (DV + 31) / 32;
-    constexpr int TILE = kKT * D * 2;
+    constexpr int DC = (DV + 15) / 16, DB = (DO + 31) / 32;
+    constexpr int KT = 32 * KB;               // keys per tile
+    static_assert(C0 % 32 == 0 && C0 + DO <= D, "output slice");
+    constexpr int TILE = KT * D * 2;
     constexpr int STAGE = 2 * TILE;           // K, V
     constexpr int NBUF = 3;
     constexpr int LOADS = STAGE / 1024 / kWaves;
@@ -136,16 +139,16 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     int kv_lo = 0;
     if (p.window > 0) {
         kv_lo = max(0, q0 + coff - p.window + 1);
-        kv_lo = (kv_lo / kKT) * kKT;
+        kv_lo = (kv_lo / KT) * KT;
     }
-    const int n_kv_tiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kKT - 1) / kKT : 0;
+    const int n_kv_tiles = kv_hi > kv_lo ? (kv_hi - kv_lo + KT - 1) / KT : 0;
     const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * DV;
     const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * DV;
     auto stage = [&](int it) {
         char* buf = smem + (it % NBUF) * STAGE;
-        const int kt = kv_lo + it * kKT;
-        stage_tile<D, kKT, kWaves, DV>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
-        stage_tile<D, kKT, kWaves, DV>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
+        const int kt = kv_lo + it * KT;
+        stage_tile<D, KT, kWaves, DV>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
+        stage_tile<D, KT, kWaves, DV>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
     };
 
     const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
@@ -163,18 +166,18 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         // (with a bias, the tile loads go out after the bias is consumed: the
         // bias loads' wait would otherwise also wait for them)
         if (!BIAS && it + 2 < n_kv_tiles) stage(it + 2);
-        const int kt = kv_lo + it * kKT;
+        const int kt = kv_lo + it * KT;
         // the bias of the whole tile, all loads in flight together (4-key
         // groups at 32 kb + 8 g + 4 hi)
-        f32x4_t bv[8];
+        f32x4_t bv[4 * KB];
         if (BIAS) {
-            if (kt + kKT <= p.bias_cols && p.bias_v4) {
+            if (kt + KT <= p.bias_cols && p.bias_v4) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
+                for (int i = 0; i < 4 * KB; ++i)
                     bv[i] = *reinterpret_cast<const f32x4_t*>(brow + kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi);
             } else {
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
+                for (int i = 0; i < 4 * KB; ++i)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const int key = kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi + j;
@@ -188,37 +191,39 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         // (bitwise | and &: these uniform tests must not become branches,
         // which would split the loop body into separately scheduled blocks)
         const bool skip = !wave_active | ((p.causal != 0) & (kt > wq_last + coff)) |
-                          ((p.window > 0) & (kt + kKT - 1 < qa + coff - p.window + 1));
+                          ((p.window > 0) & (kt + KT - 1 < qa + coff - p.window + 1));
         const char* Ks = smem + (it % NBUF) * STAGE;
         const char* krb = opaque(Ks + rbase);
         const char* ktb = opaque(Ks + tbase);
-        const bool need_mask = skip | (kt + kKT > kv_len) | ((p.causal != 0) & (kt + kKT - 1 > qa + coff)) |
+        const bool need_mask = skip | (kt + KT > kv_len) | ((p.causal != 0) & (kt + KT - 1 > qa + coff)) |
                                ((p.window > 0) & (kt < wq_last + coff - p.window + 1));
         const int d0 = kt + 4 * hi - band.lo;
         const uint32_t wdt = skip ? 0u : band.width;
         // S^T and dP^T of both 32-key halves on the matrix cores first; half
         // 0's elementwise work overlaps half 1's MFMAs, half 1's overlaps
         // half 0's dQ products. P = exp2(S - lse) needs no running max.
-        f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}}, pacc[2] = {f32x16_t{}, f32x16_t{}};
+        f32x16_t sacc[KB], pacc[KB];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) sacc[kb] = pacc[kb] = f32x16_t{};
 #pragma unroll
         for (int kc = 0; kc < DC; ++kc) {
             const char* a = lds_xor(krb, 32 * kc);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < KB; ++kb) {
                 sacc[kb] = mfma32<T>(ld16(a + kb * 32 * 2 * D), qf[kc], sacc[kb]);
                 pacc[kb] = mfma32<T>(ld16(a + kb * 32 * 2 * D + TILE), df[kc], pacc[kb]);
             }
         }
-        pipe_reads<1, 4 * DC, 4>();
+        pipe_reads<1, 2 * KB * DC, 4>();
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 float x = fmaf(sacc[kb][r], c2, -lse2);
                 if (BIAS) x = fmaf(bv[4 * kb + (r >> 2)][r & 3], kLog2e, x);
                 sacc[kb][r] = __builtin_amdgcn_exp2f(x);
             }
-            if (BIAS && kb == 1 && it + 2 < n_kv_tiles) stage(it + 2);
+            if (BIAS && kb == KB - 1 && it + 2 < n_kv_tiles) stage(it + 2);
             if (need_mask) {     // out-of-band keys -> P = 0
                 asm volatile("");   // keep a real branch (no speculated selects on every tile)
 #pragma unroll
@@ -237,19 +242,20 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
                                            T::pack2(sacc[kb][r0 + 4], sacc[kb][r0 + 5]),
                                            T::pack2(sacc[kb][r0 + 6], sacc[kb][r0 + 7])};
 #pragma unroll
-                for (int db = 0; db < DB; ++db) dqacc[db] = mfma32<T>(tr_operand<D>(ktb, c, db), bs, dqacc[db]);
+                for (int db = 0; db < DB; ++db)
+                    dqacc[db] = mfma32<T>(tr_operand<D>(ktb, c, db + C0 / 32), bs, dqacc[db]);
             }
         }
     }
 
     if (wave_active && row_ok) {
-        const int64_t off = grow * ((int64_t)p.hq * DV) + (int64_t)head * DV;
+        const int64_t off = grow * ((int64_t)p.hq * DV) + (int64_t)head * DV + C0;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
                 const int d = 32 * db + 8 * rg + 4 * hi;
-                if (DV % 32 != 0 && d >= DV) continue;
+                if ((DO % 32 != 0 && d >= DO) || (C0 + DO > DV && C0 + d >= DV)) continue;
                 store4<T, OUT_F32>(p.dq, off + d, dqacc[db][4 * rg] * p.scale, dqacc[db][4 * rg + 1] * p.scale,
                                    dqacc[db][4 * rg + 2] * p.scale, dqacc[db][4 * rg + 3] * p.scale);
             }
@@ -272,16 +278,21 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
 // dO^T operands are transposed LDS reads. The loop covers the g heads of the
 // group, so the GQA reduction of dK/dV happens in registers.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int DV, bool BIAS, bool OUT_F32>
+// D is the tile width (64, 128 or 256) and DV <= D the head dim; this launch
+// outputs the DO columns of dK and dV from C0 (several launches above 128,
+// the S and dP products recomputed in each). A stage holds 32 * NQB queries.
+template <typename T, int D, int DV, int DO, int C0, int NQB, bool BIAS, bool OUT_F32>
 __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
-    constexpr int DC = (DV + 15) / 16, DB = (DV + 31) / 32;
+    constexpr int DC = (DV + 15) / 16, DB = (DO + 31) / 32;
+    static_assert(C0 % 32 == 0 && C0 + DO <= D, "output slice");
+    constexpr int QTL = 32 * NQB;                       // queries per stage
     constexpr int NP = kWaves / 2;                      // wave pairs
     constexpr int KB = NP * kKW;                        // keys per workgroup
-    constexpr int TILE = kQT * D * 2;
-    constexpr int STAGE = 2 * TILE + 2 * kQT * 4;       // Q, dO, lse, delta
+    constexpr int TILE = QTL * D * 2;
+    constexpr int STAGE = 2 * TILE + 2 * 64 * 4;        // Q, dO, lse, delta (64 rows each)
     constexpr int NBUF = 3;
     constexpr int PBLK = 2 * 1024;                      // packed P of one 32x32 block
-    constexpr int PSTAGE = NP * 2 * PBLK;               // one stage, all pairs
+    constexpr int PSTAGE = NP * NQB * PBLK;             // one stage, all pairs
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE + 2 * PSTAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -322,10 +333,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 
     // Query range that can see any key of this workgroup.
     const int k_last_wg = min(kv_len, k0 + KB) - 1;
-    // (tile grid aligned to kQT so workgroups of a sequence share tiles)
-    const int q_lo = p.causal ? max(0, k0 - coff) / kQT * kQT : 0;
+    // (tile grid aligned to QTL so workgroups of a sequence share tiles)
+    const int q_lo = p.causal ? max(0, k0 - coff) / QTL * QTL : 0;
     const int q_hi = p.window > 0 ? min(q_len, k_last_wg - coff + p.window) : q_len;
-    const int n_q_tiles = q_hi > q_lo ? (q_hi - q_lo + kQT - 1) / kQT : 0;
+    const int n_q_tiles = q_hi > q_lo ? (q_hi - q_lo + QTL - 1) / QTL : 0;
     const int n_stages = n_q_tiles * p.g;
 
     // Stage st covers query tile (n_q_tiles - 1 - st / g) of head hk g + st % g:
@@ -333,7 +344,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     // sequence reads the same (tile, head) at the same time and the L2 serves
     // the repeats (each workgroup stops at its own causal start q_lo).
     auto stage_head = [&](int st) { return hk * p.g + st % p.g; };
-    auto stage_q0 = [&](int st) { return q_lo + (n_q_tiles - 1 - st / p.g) * kQT; };
+    auto stage_q0 = [&](int st) { return q_lo + (n_q_tiles - 1 - st / p.g) * QTL; };
     // Direct loads of stage `st`: Q and dO tiles by four loader waves
     // (ldw = 0..3), lse by loader 0, delta by loader 1 (4 bytes per lane,
     // lane l -> row l).
@@ -349,14 +360,14 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         // the wait for those would also cover tile loads issued after them,
         // so the B waves load the tiles.
         if (ldw >= 0) {
-            stage_tile<D, kQT, NP, DV>(buf, p.q + hoff, p.q_rs, qt, q_len, ldw, lane);
-            stage_tile<D, kQT, NP, DV>(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * DV, p.do_rs,
+            stage_tile<D, QTL, NP, DV>(buf, p.q + hoff, p.q_rs, qt, q_len, ldw, lane);
+            stage_tile<D, QTL, NP, DV>(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * DV, p.do_rs,
                                        qt, q_len, ldw, lane);
         }
         if (ldw == 0 || ldw == 1) {
             const int q = min(qt + lane, q_len - 1);        // rows past the end are masked
             const float* src = (ldw == 0 ? p.lse : p.delta) + (int64_t)(qr.start + q) * p.hq + h;
-            lds_dma4(src, buf + 2 * TILE + ldw * kQT * 4);
+            lds_dma4(src, buf + 2 * TILE + ldw * 64 * 4);
         }
     };
 
@@ -366,7 +377,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     f32x16_t acc[DB];                            // dV^T (wave A) or dK^T (wave B)
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = f32x16_t{};
-    f32x16_t pacc[2] = {f32x16_t{}, f32x16_t{}};  // wave B: dP of the previous stage
+    f32x16_t pacc[NQB];                          // wave B: dP of the previous stage
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) pacc[qb] = f32x16_t{};
 
     // Is the 32x32 block (queries qf0.., this pair's keys) of stage st empty
     // or does it need per-element masking? Identical in both waves of a pair.
@@ -396,7 +409,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             const float* ls = reinterpret_cast<const float*>(Qs + 2 * TILE);   // -lse log2(e)
             const char* qrb = opaque(Qs + rbase);
             const char* dtb = opaque(Ds + tbase);
-            char* pb = smem + NBUF * STAGE + (st & 1) * PSTAGE + pair * 2 * PBLK;
+            char* pb = smem + NBUF * STAGE + (st & 1) * PSTAGE + pair * NQB * PBLK;
             const int h = stage_head(st);
             const int qt = stage_q0(st);
             // S of both 32-query blocks on the matrix cores; block 0's
@@ -405,27 +418,29 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             // the stage's bias (this lane's key column, 32 query rows), all
             // loads in flight together under the S products; columns at or
             // past bias_cols read as 0, rows past the end read the last row
-            float bvals[2][16];
+            float bvals[NQB][16];
             if (BIAS) {
                 const float* bcol = p.bias + (int64_t)h * p.bias_hs + min(key, (int)p.bias_cols - 1);
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb)
+                for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int qrow = min(qt + 32 * qb + 8 * (r >> 2) + 4 * hi + (r & 3), q_len - 1);
                         bvals[qb][r] = bcol[(int64_t)(qr.start + qrow) * p.bias_qs];
                     }
             }
-            f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
+            f32x16_t sacc[NQB];
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) sacc[qb] = f32x16_t{};
 #pragma unroll
             for (int kc = 0; kc < DC; ++kc)
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb)
+                for (int qb = 0; qb < NQB; ++qb)
                     sacc[qb] = mfma32<T>(row_operand<D>(qrb, kc, 32 * qb), kvf[kc], sacc[qb]);
             // exponentials of both blocks (overlapping the S MFMAs in flight),
             // then the rarely needed masks, then the dV products
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
+            for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
                 for (int rg = 0; rg < 4; ++rg) {
                     const int qi = 32 * qb + 8 * rg + 4 * hi;    // stage-local query of r = 4 rg
@@ -446,7 +461,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                 }
             }
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
+            for (int qb = 0; qb < NQB; ++qb) {
                 // out-of-band elements (and rows with no allowed key) -> P = 0
                 if (block_needs_mask(st, qb)) {
                     asm volatile("");   // keep a real branch (no speculated selects on every block)
@@ -457,7 +472,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                 }
             }
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
+            for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {
                     const int r0 = 8 * cc;
@@ -468,7 +483,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                     st16(pb + qb * PBLK + cc * 1024 + lane * 16, bp);
 #pragma unroll
                     for (int db = 0; db < DB; ++db)
-                        acc[db] = mfma32<T>(tr_operand<D>(dtb, 2 * qb + cc, db), bp, acc[db]);
+                        acc[db] = mfma32<T>(tr_operand<D>(dtb, 2 * qb + cc, db + C0 / 32), bp, acc[db]);
                 }
             }
         }
@@ -482,11 +497,11 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             if (st > 0) {
                 const int sp = st - 1;
                 const char* Qs = smem + (sp % NBUF) * STAGE;
-                const float* dls = reinterpret_cast<const float*>(Qs + 2 * TILE) + kQT;
+                const float* dls = reinterpret_cast<const float*>(Qs + 2 * TILE) + 64;
                 const char* qtb = opaque(Qs + tbase);
-                const char* pb = smem + NBUF * STAGE + (sp & 1) * PSTAGE + pair * 2 * PBLK;
+                const char* pb = smem + NBUF * STAGE + (sp & 1) * PSTAGE + pair * NQB * PBLK;
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb) {
+                for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
                     for (int cc = 0; cc < 2; ++cc) {
                         const u32x4_t pp = ld16(pb + qb * PBLK + cc * 1024 + lane * 16);
@@ -506,18 +521,18 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                                                    T::pack2(dsv[4], dsv[5]), T::pack2(dsv[6], dsv[7])};
 #pragma unroll
                         for (int db = 0; db < DB; ++db)
-                            acc[db] = mfma32<T>(tr_operand<D>(qtb, 2 * qb + cc, db), bs, acc[db]);
+                            acc[db] = mfma32<T>(tr_operand<D>(qtb, 2 * qb + cc, db + C0 / 32), bs, acc[db]);
                     }
                 }
             }
             if (st < n_stages) {
                 const char* drb = opaque(smem + (st % NBUF) * STAGE + TILE + rbase);
-                pacc[0] = f32x16_t{};
-                pacc[1] = f32x16_t{};
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb) pacc[qb] = f32x16_t{};
 #pragma unroll
                 for (int kc = 0; kc < DC; ++kc)
 #pragma unroll
-                    for (int qb = 0; qb < 2; ++qb)
+                    for (int qb = 0; qb < NQB; ++qb)
                         pacc[qb] = mfma32<T>(row_operand<D>(drb, kc, 32 * qb), kvf[kc], pacc[qb]);
             }
         }
@@ -532,7 +547,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     }
 
     if (pair_active && key_ok) {
-        const int64_t off = (int64_t)(kr.start + key) * ((int64_t)p.hkv * DV) + (int64_t)hk * DV;
+        const int64_t off = (int64_t)(kr.start + key) * ((int64_t)p.hkv * DV) + (int64_t)hk * DV + C0;
         void* dst = role_a ? p.dv : p.dk;
         const float sc = role_a ? 1.f : p.scale;
 #pragma unroll
@@ -540,7 +555,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
                 const int d = 32 * db + 8 * rg + 4 * hi;
-                if (DV % 32 != 0 && d >= DV) continue;
+                if ((DO % 32 != 0 && d >= DO) || (C0 + DO > DV && C0 + d >= DV)) continue;
                 store4<T, OUT_F32>(dst, off + d, acc[db][4 * rg] * sc, acc[db][4 * rg + 1] * sc,
                                    acc[db][4 * rg + 2] * sc, acc[db][4 * rg + 3] * sc);
             }
@@ -630,7 +645,7 @@ BwdKParams make_params(const BwdArgs& a) {
     return p;
 }
 
-template <typename T, int D, int DV, bool OUT_F32>
+template <typename T, int D, int DV, int DO, int C0, int KB, bool OUT_F32>
 hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     constexpr int NW = kWaves;
     BwdKParams p = make_params(a);
@@ -641,13 +656,15 @@ hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     const int64_t blocks = (int64_t)p.n_tiles * p.n_hg;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (a.geo.bias != nullptr)
-        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, true, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, p);
+        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64),
+                           0, st, p);
     else
-        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, false, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, p);
+        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, false, OUT_F32>), dim3((unsigned)blocks),
+                           dim3(NW * 64), 0, st, p);
     return hipGetLastError();
 }
 
-template <typename T, int D, int DV, bool OUT_F32>
+template <typename T, int D, int DV, int DO, int C0, int NQB, bool OUT_F32>
 hipError_t launch_dkv_typed(const BwdArgs& a, hipStream_t st) {
     BwdKParams p = make_params(a);
     constexpr int NW = kWaves;
@@ -655,11 +672,11 @@ hipError_t launch_dkv_typed(const BwdArgs& a, hipStream_t st) {
     const int64_t blocks = (int64_t)p.n_tiles * a.geo.hkv;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (a.geo.bias != nullptr)
-        hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, true, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st,
-                           p);
+        hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, DO, C0, NQB, true, OUT_F32>), dim3((unsigned)blocks),
+                           dim3(NW * 64), 0, st, p);
     else
-        hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, false, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0, st,
-                           p);
+        hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, DO, C0, NQB, false, OUT_F32>), dim3((unsigned)blocks),
+                           dim3(NW * 64), 0, st, p);
     return hipGetLastError();
 }
 
@@ -713,16 +730,48 @@ hipError_t dispatch_dims(const BwdArgs& a, hipStream_t st) {
         case 88: return f ? L<T, 128, 88, true>::run(a, st) : L<T, 128, 88, false>::run(a, st);
         case 96: return f ? L<T, 128, 96, true>::run(a, st) : L<T, 128, 96, false>::run(a, st);
         case 128: return f ? L<T, 128, 128, true>::run(a, st) : L<T, 128, 128, false>::run(a, st);
+        case 160: return f ? L<T, 256, 160, true>::run(a, st) : L<T, 256, 160, false>::run(a, st);
+        case 256: return f ? L<T, 256, 256, true>::run(a, st) : L<T, 256, 256, false>::run(a, st);
         default: return hipErrorInvalidValue;
     }
 }
 template <typename T, int D, int DV, bool F>
 struct DqLaunch {
-    static hipError_t run(const BwdArgs& a, hipStream_t st) { return launch_dq_typed<T, D, DV, F>(a, st); }
+    static hipError_t run(const BwdArgs& a, hipStream_t st) {
+        if constexpr (D <= 128) {
+            return launch_dq_typed<T, D, DV, DV, 0, 2, F>(a, st);
+        } else {
+            // 256-wide tiles: 32-key tiles (three K + V stages fit the LDS)
+            // and the output in column slices (96 wide for D = 160; 64 for
+            // D = 256, whose Q^T and dO^T fragments alone take 128 registers)
+            if constexpr (DV > 192) {
+                hipError_t e = launch_dq_typed<T, D, DV, 64, 0, 1, F>(a, st);
+                if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 64, 64, 1, F>(a, st);
+                if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 64, 128, 1, F>(a, st);
+                if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 64, 192, 1, F>(a, st);
+                return e;
+            } else {
+                hipError_t e = launch_dq_typed<T, D, DV, 96, 0, 1, F>(a, st);
+                if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 96, 96, 1, F>(a, st);
+                return e;
+            }
+        }
+    }
 };
 template <typename T, int D, int DV, bool F>
 struct DkvLaunch {
-    static hipError_t run(const BwdArgs& a, hipStream_t st) { return launch_dkv_typed<T, D, DV, F>(a, st); }
+    static hipError_t run(const BwdArgs& a, hipStream_t st) {
+        if constexpr (D <= 128) {
+            return launch_dkv_typed<T, D, DV, DV, 0, 2, F>(a, st);
+        } else {
+            // 256-wide tiles: 32-query stages (three fit the LDS) and the
+            // output in two column slices
+            constexpr int DO = DV > 192 ? 128 : 96;
+            hipError_t e = launch_dkv_typed<T, D, DV, DO, 0, 1, F>(a, st);
+            if (e == hipSuccess) e = launch_dkv_typed<T, D, DV, DO, DO, 1, F>(a, st);
+            return e;
+        }
+    }
 };
 
 hipError_t launch_bwd_dq_mfma(int dtype, const BwdArgs& a, hipStream_t st) {

@@ -236,7 +236,7 @@ int mtlattn_varlen_fwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
     a.geo = make_geo(p);
     a.q = q; a.q_rs = q_row_stride; a.k = k; a.k_rs = k_row_stride; a.v = v; a.v_rs = v_row_stride;
     a.o = out; a.lse = lse;
-    if (is16(p->dtype) && mfma_fwd_head_dim(p->head_dim) && vec_ok && !force_generic())
+    if (is16(p->dtype) && mfma_head_dim(p->head_dim) && vec_ok && !force_generic())
         return launch_status(launch_fwd_mfma(p->dtype, a, st), "flash forward");
     return launch_status(launch_fwd_generic(p->dtype, a, st), "generic forward");
 }

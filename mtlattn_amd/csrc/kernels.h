@@ -79,10 +79,11 @@ inline int64_t decode_workspace_rows(int64_t total_kv, int num_seqs, int hkv, in
 
 // Which head dims have MFMA kernels.
 // head dims of the matrix-core flash kernels (fp16/bf16): 64 and 128 native,
-// 80, 88, 96 on the 128-wide tile with the spare columns unused; the forward
-// also takes 160 and 256 (256-wide K tiles, output columns in two launches)
-inline bool mfma_head_dim(int d) { return d == 64 || d == 80 || d == 88 || d == 96 || d == 128; }
-inline bool mfma_fwd_head_dim(int d) { return mfma_head_dim(d) || d == 160 || d == 256; }
+// 80, 88, 96 on the 128-wide tile with the spare columns unused, 160 and 256
+// on 256-wide tiles with the output columns produced in slices
+inline bool mfma_head_dim(int d) {
+    return d == 64 || d == 80 || d == 88 || d == 96 || d == 128 || d == 160 || d == 256;
+}
 // head dims of the split-KV decode kernels
 inline bool decode_head_dim(int d) { return d == 64 || d == 128; }
 

@@ -201,6 +201,22 @@ def test_mfma_padded_head_dims(mt):
              bias=_make_bias(512, 8, 512, True))
 
 
+def test_mfma_wide_head_dims(mt):
+    """Head dims 160/256 run the matrix-core kernels on 256-wide tiles, the
+    output columns in slices (forward 2, dK/dV 2, dQ 2 or 4 launches)."""
+    b, h = torch.bfloat16, torch.float16
+    for D in (160, 256):
+        _fwd(mt, f"D={D} bf16 GQA causal ragged", [300, 77, 513], [300, 77, 513], 16, 4, D, b, atol=4e-2,
+             causal=True)
+        _fwd(mt, f"D={D} fp16 cross window", [64, 200], [333, 260], 8, 2, D, h, causal=True, window=100)
+        _bwd(mt, f"bwd D={D} bf16 GQA ragged", [200, 91, 333], [200, 91, 333], 12, 4, D, b, 4e-2, causal=True)
+        _bwd(mt, f"bwd D={D} fp16 window cross", [150], [410], 8, 8, D, h, 6e-3, causal=True, window=90)
+        _bwd(mt, f"bwd D={D} fp16 per-head bias", [640], [640], 8, 4, D, h, 6e-3,
+             bias=_make_bias(640, 8, 640, False))
+        _bwd(mt, f"bwd D={D} bf16 broadcast bias causal", [512], [512], 8, 8, D, b, 4e-2, causal=True,
+             bias=_make_bias(512, 8, 512, True))
+
+
 def test_large_head_dims(mt):
     _fwd(mt, "D=160 full", [2048], [2048], 8, 8, 160, torch.float16)
     _fwd(mt, "D=160 causal", [1500], [1500], 12, 12, 160, torch.float16, causal=True)
@@ -476,7 +492,7 @@ def test_determinism(mt):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("D", [128, 88])
+@pytest.mark.parametrize("D", [128, 88, 256])
 def test_mfma_matches_generic(mt, D):
     """The MFMA kernels and the portable kernels agree (both vs the oracle too)."""
     import subprocess
