@@ -185,6 +185,30 @@ int mtlattn_attn_splitkv(const mtlattn_problem* p,
  * so ragged KV lengths stay balanced. Retunes src/ext.mm:372-388. */
 int32_t mtlattn_decode_num_splits(const mtlattn_problem* p);
 
+/*
+ * Key-padding pack / unpack for the SDPA adapter. No counterpart in the
+ * reference's _C: its adapter (mtlattn/__init__.py:202-249) copies each
+ * batch's valid prefix in Python after pulling the lengths to the host; these
+ * do it on the device with no host synchronisation.
+ *
+ * mtlattn_pack_padded: dense src [B, H, N, D] (element strides sb, sh, sn of
+ * the B, H, N dims; D contiguous) -> packed rows dst [B * N, H, D]. Batch b's
+ * first lens[b] tokens (clamped to [0, N]) go to rows cu[b] + n, where
+ * cu = prefix sums of the lengths, written to cu_out [B + 1] (int32, device);
+ * the padded tokens follow all valid ones. Use dst with cu_out as the varlen
+ * q/k/v and cu_seqlens (rows past cu_out[B] belong to no sequence).
+ * mtlattn_unpack_padded: packed rows src [B * N, H, D] -> dense dst
+ * [B, H, N, D] (strides sb, sh, sn): token (b, n) takes row cu[b] + n when
+ * n < lens[b], zeros otherwise.
+ * dtype is MTLATTN_DTYPE_*; all pointers are device pointers.
+ */
+int mtlattn_pack_padded(int32_t dtype, int32_t B, int32_t N, int32_t H, int32_t D,
+                        const void* src, int64_t sb, int64_t sh, int64_t sn,
+                        const int32_t* lens, int32_t* cu_out, void* dst, void* stream);
+int mtlattn_unpack_padded(int32_t dtype, int32_t B, int32_t N, int32_t H, int32_t D,
+                          const void* src, const int32_t* lens, const int32_t* cu,
+                          void* dst, int64_t sb, int64_t sh, int64_t sn, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

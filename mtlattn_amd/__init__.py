@@ -223,33 +223,28 @@ def _try_padding_varlen(query, key, value, attn_mask, is_causal, scale):
     Hkv, Nkv = key.shape[1], key.shape[2]
     if Nq != Nkv:
         return None
-    keep = attn_mask if attn_mask.dtype == torch.bool else attn_mask > -1e30
+    keep0 = attn_mask if attn_mask.dtype == torch.bool else attn_mask > -1e30
     try:
-        keep = keep.expand(B, Hq, Nq, Nkv)
+        keep = keep0.expand(B, Hq, Nq, Nkv)
     except RuntimeError:
         return None
     kv_keep = keep[:, 0, 0, :]
-    if not torch.equal(keep, kv_keep[:, None, None, :].expand_as(keep)):
-        return None
-    lens = kv_keep.sum(dim=1)
+    lens = kv_keep.sum(dim=1, dtype=torch.int32)
     idx = torch.arange(Nkv, device=query.device)
-    if not torch.equal(kv_keep, idx[None, :] < lens[:, None]):
+    # the one host decision: does the mask depend only on (batch, key), with
+    # the kept keys a prefix? (both tests in one device reduction, compared at
+    # the mask's own broadcast shape, not the expanded [B, H, N, N])
+    ok = torch.logical_and((keep0 == kv_keep[:, None, None, :]).all(),
+                           (kv_keep == (idx[None, :] < lens[:, None])).all())
+    if not bool(ok):
         return None
-    lens_host = [int(x) for x in lens.tolist()]
-    total = sum(lens_host)
-    if total == 0:
-        return query.new_zeros(B, Hq, Nq, D)
-    cu = torch.zeros(B + 1, dtype=torch.int32, device=query.device)
-    cu[1:] = torch.cumsum(lens.to(torch.int32), 0)
-    # [B, H, N, D] -> packed [total, H, D] keeping only each batch's valid prefix
-    valid = (idx[None, :] < lens[:, None]).reshape(-1)
-    qp = query.transpose(1, 2).reshape(B * Nq, Hq, D)[valid]
-    kp = key.transpose(1, 2).reshape(B * Nkv, Hkv, D)[valid]
-    vp = value.transpose(1, 2).reshape(B * Nkv, Hkv, D)[valid]
-    op = varlen_attention(qp, kp, vp, cu, cu, max(lens_host), scale, causal=is_causal)
-    out = query.new_zeros(B * Nq, Hq, D)
-    out[valid] = op
-    return out.view(B, Nq, Hq, D).transpose(1, 2).contiguous()
+    # pack, attend, unpack on the device: no lengths on the host, no
+    # per-batch copies (rows past cu[B] belong to no sequence)
+    qp, cu = _C.pack_padded(query, lens)
+    kp, _ = _C.pack_padded(key, lens)
+    vp, _ = _C.pack_padded(value, lens)
+    op = varlen_attention(qp, kp, vp, cu, cu, Nq, scale, causal=is_causal)
+    return _C.unpack_padded(op, cu, lens, B, Nq)
 
 
 def replace_sdpa(min_seqlen=_SDPA_MIN_SEQLEN):

@@ -380,4 +380,34 @@ int mtlattn_attn_splitkv(const mtlattn_problem* p, const void* q, int64_t q_row_
                        workspace_bytes, (hipStream_t)stream);
 }
 
+
+int mtlattn_pack_padded(int32_t dtype, int32_t B, int32_t N, int32_t H, int32_t D, const void* src, int64_t sb,
+                        int64_t sh, int64_t sn, const int32_t* lens, int32_t* cu_out, void* dst, void* stream) {
+    if (dtype != MTLATTN_DTYPE_F32 && dtype != MTLATTN_DTYPE_F16 && dtype != MTLATTN_DTYPE_BF16)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: unsupported dtype %d", dtype);
+    if (B < 0 || N < 0 || H <= 0 || D <= 0 || sb < 0 || sh < 0 || sn < 0)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: pack_padded: bad shape or strides");
+    if (B == 0) return MTLATTN_OK;
+    if (src == nullptr || lens == nullptr || cu_out == nullptr || dst == nullptr)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: pack_padded: null pointer");
+    const int es = dtype == MTLATTN_DTYPE_F32 ? 4 : 2;
+    return launch_status(launch_pad_pack(es, B, N, H, D, src, sb, sh, sn, lens, cu_out, dst, (hipStream_t)stream),
+                         "pack_padded");
+}
+
+int mtlattn_unpack_padded(int32_t dtype, int32_t B, int32_t N, int32_t H, int32_t D, const void* src,
+                          const int32_t* lens, const int32_t* cu, void* dst, int64_t sb, int64_t sh, int64_t sn,
+                          void* stream) {
+    if (dtype != MTLATTN_DTYPE_F32 && dtype != MTLATTN_DTYPE_F16 && dtype != MTLATTN_DTYPE_BF16)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: unsupported dtype %d", dtype);
+    if (B < 0 || N < 0 || H <= 0 || D <= 0 || sb < 0 || sh < 0 || sn < 0)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: unpack_padded: bad shape or strides");
+    if (B == 0) return MTLATTN_OK;
+    if (src == nullptr || lens == nullptr || cu == nullptr || dst == nullptr)
+        return fail(MTLATTN_ERR_INVALID, "mtlattn: unpack_padded: null pointer");
+    const int es = dtype == MTLATTN_DTYPE_F32 ? 4 : 2;
+    return launch_status(launch_pad_unpack(es, B, N, H, D, src, lens, cu, dst, sb, sh, sn, (hipStream_t)stream),
+                         "unpack_padded");
+}
+
 }  // extern "C"

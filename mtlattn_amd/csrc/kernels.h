@@ -69,6 +69,10 @@ hipError_t launch_bwd_dkv_generic(int dtype, const BwdArgs& a, hipStream_t st);
 hipError_t launch_zero_outside(void* ptr, int64_t row_bytes, int64_t total_rows, const int* cu, int num_seqs,
                                hipStream_t st);
 hipError_t launch_decode(int dtype, const DecodeArgs& a, hipStream_t st);
+hipError_t launch_pad_pack(int esize, int B, int N, int H, int D, const void* src, int64_t sb, int64_t sh,
+                           int64_t sn, const int* lens, int* cu, void* dst, hipStream_t st);
+hipError_t launch_pad_unpack(int esize, int B, int N, int H, int D, const void* src, const int* lens, const int* cu,
+                             void* dst, int64_t sb, int64_t sh, int64_t sn, hipStream_t st);
 
 // Partial rows of the split-KV workspace (fp32 O rows of D values plus one
 // LSE each): kv heads x head groups x work-item slots x 16.

@@ -238,6 +238,47 @@ std::tuple<at::Tensor, at::Tensor> mpp_bwd_dkv(const at::Tensor& q, const at::Te
 
 // The reference's "is the fast path usable here" probe (src/ext.mm:780-782):
 // the MFMA kernels are compiled into this build for gfx950.
+// SDPA key-padding adapter on the device (see mtlattn_pack_padded): x is
+// dense [B, H, N, D] with D contiguous, lens int32 [B] on x's device. Returns
+// the packed rows [B * N, H, D] and cu_seqlens [B + 1].
+std::tuple<at::Tensor, at::Tensor> pack_padded(const at::Tensor& x_in, const at::Tensor& lens) {
+    TORCH_CHECK(x_in.is_cuda() && x_in.dim() == 4, "mtlattn: pack_padded expects a [B, H, N, D] GPU tensor");
+    const at::Tensor x = (x_in.size(3) == 1 || x_in.stride(3) == 1) ? x_in : x_in.contiguous();
+    TORCH_CHECK(lens.is_cuda() && lens.scalar_type() == at::kInt && lens.dim() == 1 && lens.size(0) == x.size(0) &&
+                    lens.get_device() == x.get_device(),
+                "mtlattn: lens must be int32 [B] on the device of x");
+    const c10::DeviceGuard guard(x.device());
+    const auto B = x.size(0), H = x.size(1), N = x.size(2), D = x.size(3);
+    auto lc = lens.contiguous();
+    auto packed = at::empty({B * N, H, D}, x.options());
+    auto cu = at::empty({B + 1}, lens.options());
+    check_rc(mtlattn_pack_padded(dtype_code(x.scalar_type()), (int32_t)B, (int32_t)N, (int32_t)H, (int32_t)D,
+                                 x.data_ptr(), x.stride(0), x.stride(1), x.stride(2), lc.data_ptr<int32_t>(),
+                                 cu.data_ptr<int32_t>(), packed.data_ptr(), current_stream(x)));
+    return {packed, cu};
+}
+
+// Inverse of pack_padded: packed rows [B * N, H, D] -> dense contiguous
+// [B, H, N, D], zeros for padded tokens.
+at::Tensor unpack_padded(const at::Tensor& packed, const at::Tensor& cu, const at::Tensor& lens, int64_t B,
+                         int64_t N) {
+    TORCH_CHECK(packed.is_cuda() && packed.dim() == 3 && packed.size(0) == B * N,
+                "mtlattn: unpack_padded expects packed rows [B * N, H, D]");
+    TORCH_CHECK(cu.scalar_type() == at::kInt && cu.numel() == B + 1 && lens.scalar_type() == at::kInt &&
+                    lens.numel() == B && cu.is_cuda() && lens.is_cuda(),
+                "mtlattn: cu_seqlens [B + 1] and lens [B] must be int32 GPU tensors");
+    const c10::DeviceGuard guard(packed.device());
+    auto pc = packed.contiguous();
+    const auto H = pc.size(1), D = pc.size(2);
+    auto out = at::empty({B, H, N, D}, pc.options());
+    auto lc = lens.contiguous();
+    auto cc = cu.contiguous();
+    check_rc(mtlattn_unpack_padded(dtype_code(pc.scalar_type()), (int32_t)B, (int32_t)N, (int32_t)H, (int32_t)D,
+                                   pc.data_ptr(), lc.data_ptr<int32_t>(), cc.data_ptr<int32_t>(), out.data_ptr(),
+                                   out.stride(0), out.stride(1), out.stride(2), current_stream(pc)));
+    return out;
+}
+
 bool mpp_available() { return true; }
 
 int64_t gpu_core_count() {
@@ -250,6 +291,10 @@ int64_t gpu_core_count() {
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("mpp_available", &mpp_available, "True: the MFMA fast path is compiled in for gfx950");
+    m.def("pack_padded", &pack_padded, "SDPA key-padding adapter: dense [B,H,N,D] -> packed rows + cu_seqlens",
+          py::arg("x"), py::arg("lens"));
+    m.def("unpack_padded", &unpack_padded, "Inverse of pack_padded (zeros for padded tokens)", py::arg("packed"),
+          py::arg("cu_seqlens"), py::arg("lens"), py::arg("B"), py::arg("N"));
     m.def("gpu_core_count", &gpu_core_count, "Compute-unit count of the current device (0 if unknown)");
     m.def("abi_version", [] { return mtlattn_abi_version(); }, "C ABI version of libmtlattn_hip.so");
     m.def("attn_splitkv", &attn_splitkv, "split-KV decode with an explicit split count (test entry)", py::arg("q"),

@@ -397,6 +397,32 @@ def test_padding_mask(mt):
         assert err < 5e-3 and pad_zero
 
 
+def test_pack_unpack_padded(mt):
+    """Device pack/unpack of the SDPA adapter: valid prefixes land at
+    cu[b] + n, cu is the prefix sum, padded tokens fill the tail rows, and the
+    unpack restores the dense layout with zeros for padding (bitwise)."""
+    for dtype, (B, H, N, D), lens in [(torch.bfloat16, (4, 3, 40, 64), [40, 0, 17, 33]),
+                                      (torch.float32, (3, 2, 9, 24), [5, 9, 1]),
+                                      (torch.float16, (2, 4, 16, 20), [0, 0])]:
+        _banner(f"pack/unpack {dtype} B{B} H{H} N{N} D{D} lens={lens}")
+        g = torch.Generator().manual_seed(3)
+        base = randn((B, N, H, D), dtype, g).cuda()
+        x = base.permute(0, 2, 1, 3)                       # strided [B, H, N, D] view
+        L = torch.tensor(lens, dtype=torch.int32, device="cuda")
+        packed, cu = mt._C.pack_padded(x, L)
+        torch.cuda.synchronize()
+        ref_cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+        assert torch.equal(cu.cpu(), ref_cu)
+        xc = x.cpu()
+        want = torch.cat([xc[b, :, :lens[b], :].transpose(0, 1) for b in range(B)], 0)
+        assert torch.equal(packed[:int(ref_cu[-1])].cpu(), want)
+        pads = torch.cat([xc[b, :, lens[b]:, :].transpose(0, 1) for b in range(B)], 0)
+        assert torch.equal(packed[int(ref_cu[-1]):].cpu(), pads)     # a permutation: nothing lost
+        out = mt._C.unpack_padded(packed, cu, L, B, N).cpu()
+        keep = (torch.arange(N)[None, :] < torch.tensor(lens)[:, None])[:, None, :, None]
+        assert torch.equal(out, torch.where(keep, xc, torch.zeros((), dtype=dtype)))
+
+
 def test_sdpa_mask(mt):
     import torch.nn.functional as F
     for (B, H, N, bool_mask, bh) in [(2, 8, 1024, False, False), (2, 8, 1024, False, True),
