@@ -168,6 +168,14 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     // Rescale O only when the running max grows by more than 2^8: unnormalised
     // weights stay <= 256, exact after the final division by the row sum.
     constexpr float kRescale = 8.f;
+    // For DK <= 64 the softmax VALU work is a larger share of a tile than the
+    // MFMAs, so the tile max is skipped: weights are taken against the running
+    // max and the max is recomputed only when a row's tile sum reaches
+    // kMaxTileSum (weights up to 2^12, still exact in fp32 after the final
+    // division) or a live row has no finite max yet.
+    constexpr bool kDeferMax = DK <= 64;
+    constexpr float kMaxTileSum = 4096.f;
+    const bool row_live = wave_active & (band.width > 0);
 
     if (n_kv_tiles > 0) stage(0);
     if (n_kv_tiles > 1) stage(1);
@@ -223,14 +231,28 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
                 }
             }
         }
-        float mx = kNegInf;
-        if (raw_max) {
+        // P (rounded to T) as B operands; chunk c covers tile keys
+        // 16c + 8(j/4) + 4hi + j%4. The row sum adds the rounded values.
+        u32x4_t pf[4];
+        auto weights = [&](float m_use, float sum) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int c = 0; c < 4; ++c) {
+                const int kb = c >> 1, r0 = 8 * (c & 1);
+                float e[8];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
-            mx *= c2;
-        } else {
+                for (int j = 0; j < 8; ++j) {
+                    const float x = sacc[kb][r0 + j];
+                    e[j] = __builtin_amdgcn_exp2f(raw_max ? fmaf(x, c2, -m_use) : x - m_use);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    pf[c][j] = T::pack2(e[2 * j], e[2 * j + 1]);
+                    sum = dot2_ones<T>(pf[c][j], sum);
+                }
+            }
+            return sum;
+        };
+        if (!raw_max) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -239,39 +261,41 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
                     float x = sv == kNegInf ? kNegInf : sv * c2;   // masked stays -inf for any sign of c2
                     if (has_bias) x = fmaf(bv[4 * kb + (r >> 2)][r & 3], kLog2e, x);
                     sacc[kb][r] = x;
-                    mx = fmaxf(mx, x);
                 }
             }
         }
-        mx = pair_max(mx);
-        // m_run changes only when the tile max exceeds it by kRescale
-        const float m_new = mx > m_run + kRescale ? mx : m_run;
-        const float m_use = m_new == kNegInf ? 0.f : m_new;
-        if (__any(m_new != m_run)) {
-            const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
-            l_run *= corr;
+        // the running max after the tile: the tile max when it exceeds m_run by
+        // more than `slack`, else m_run; O and l are rescaled when it changes
+        auto update_max = [&](float slack) {
+            float mx = kNegInf;
 #pragma unroll
-            for (int db = 0; db < DB; ++db) oacc[db] *= corr;
-        }
-        m_run = m_new;
-        if (has_bias && it + 2 < n_kv_tiles) stage(it + 2);
-        // P (rounded to T) as B operands; chunk c covers tile keys
-        // 16c + 8(j/4) + 4hi + j%4. The row sum adds the rounded values.
-        u32x4_t pf[4];
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int kb = c >> 1, r0 = 8 * (c & 1);
-            float e[8];
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+            if (raw_max) mx *= c2;
+            mx = pair_max(mx);
+            const float m_new = mx > m_run + slack ? mx : m_run;
+            if (__any(m_new != m_run)) {
+                const float corr = __builtin_amdgcn_exp2f(m_run - (m_new == kNegInf ? 0.f : m_new));
+                l_run *= corr;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float x = sacc[kb][r0 + j];
-                e[j] = __builtin_amdgcn_exp2f(raw_max ? fmaf(x, c2, -m_use) : x - m_use);
+                for (int db = 0; db < DB; ++db) oacc[db] *= corr;
             }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                pf[c][j] = T::pack2(e[2 * j], e[2 * j + 1]);
-                l_run = dot2_ones<T>(pf[c][j], l_run);
+            m_run = m_new;
+        };
+        if constexpr (kDeferMax) {
+            if (has_bias && it + 2 < n_kv_tiles) stage(it + 2);
+            float ts = weights(m_run == kNegInf ? 0.f : m_run, 0.f);
+            if (__any(!(ts < kMaxTileSum) | ((m_run == kNegInf) & row_live))) {
+                asm volatile("");
+                update_max(0.f);
+                ts = weights(m_run == kNegInf ? 0.f : m_run, 0.f);
             }
+            l_run += ts;
+        } else {
+            update_max(kRescale);
+            if (has_bias && it + 2 < n_kv_tiles) stage(it + 2);
+            l_run = weights(m_run == kNegInf ? 0.f : m_run, l_run);
         }
         // O^T += V^T P^T; V^T operands are transposed reads of the row-major V tile
 #pragma unroll

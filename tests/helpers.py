@@ -31,8 +31,10 @@ TOL_RMS = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 2e-2}
 REF_ATOL = {torch.float32: 1e-4, torch.float16: 5e-3, torch.bfloat16: 3e-2}
 # LSE (natural log) absolute bound. The 16-bit kernels sum P after rounding it
 # to the input type (the values the P.V product consumes); each term carries a
-# relative error <= 2^-9 (bf16) / 2^-12 (fp16), so log(l) is off by <= ~2^-9.
-LSE_TOL = {torch.float32: 2e-5, torch.float16: 2e-3, torch.bfloat16: 2e-3}
+# relative error <= the unit roundoff, 2^-8 (bf16) / 2^-11 (fp16), so log(l) is
+# off by <= 2^-8 = 3.9e-3 (bf16), reached when one term dominates the row and
+# its weight exp2(s - m_run) is not a power of two (the running max lags).
+LSE_TOL = {torch.float32: 2e-5, torch.float16: 2e-3, torch.bfloat16: 4e-3}
 
 
 def cu_of(lens, device="cpu"):

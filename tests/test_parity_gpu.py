@@ -176,6 +176,33 @@ def test_mfma_d64(mt):
     _fwd(mt, "D=64 SWA", [2048], [2048], 12, 12, 64, torch.float16, causal=True, window=128)
 
 
+def test_mfma_d64_rising_scores(mt):
+    """Logits that grow along the key axis (key norms ramp up x12), so later
+    tiles outweigh the running max by far more than 2^12: the D=64 forward's
+    deferred tile max must rescale. Also a bias that lifts the last keys."""
+    for dtype, causal in ((torch.float16, False), (torch.bfloat16, True)):
+        name = f"D=64 rising scores {dtype} causal={causal}"
+        _banner(name)
+        lens = [1500, 2600]
+        q, k, v = _inputs(lens, lens, 8, 8, 64, dtype, seed=5)
+        for s, n in zip(cu_of(lens)[:-1].tolist(), lens):
+            ramp = 1.0 + 11.0 * torch.arange(n, dtype=torch.float32) / n
+            k[s:s + n] = (k[s:s + n].float() * ramp[:, None, None]).to(dtype)
+        cu = cu_of(lens)
+        lse = torch.empty(sum(lens), 8, dtype=torch.float32, device="cuda")
+        out = mt._C.varlen_attention(q.cuda(), k.cuda(), v.cuda(), cu.cuda(), cu.cuda(), max(lens),
+                                     0.125, causal, 0, lse, None).cpu()
+        ref, ref_lse = oracle.varlen_forward(q, k, v, cu, cu, 0.125, causal)
+        err = (out.float() - ref).abs().max().item()
+        lerr = (lse.cpu() - ref_lse).abs().max().item()
+        print(f"  max_err={err:.3e} lse_err={lerr:.3e}", flush=True)
+        assert torch.isfinite(out.float()).all()
+        assert err < REF_ATOL[dtype] and lerr < LSE_TOL[dtype]
+    bias = _make_bias(2048, 8, 2048, False)
+    bias[:, :, 1900:] += 40.0
+    _fwd(mt, "D=64 bias lifts the tail", [2048], [2048], 8, 8, 64, torch.float16, bias=bias)
+
+
 def test_generic_head_dims(mt):
     _fwd(mt, "D=96 causal", [2048], [2048], 12, 12, 96, torch.float16, causal=True)
     _fwd(mt, "D=96 bf16", [1500], [1500], 8, 8, 96, torch.bfloat16)
