@@ -144,11 +144,14 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     const int n_kv_tiles = kv_hi > kv_lo ? (kv_hi - kv_lo + KT - 1) / KT : 0;
     const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * DV;
     const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * DV;
+    TileStager<D, KT, kWaves, DV> kst, vst;
+    kst.init(p.k_rs, w, lane);
+    vst.init(p.v_rs, w, lane);
     auto stage = [&](int it) {
         char* buf = smem + (it % NBUF) * STAGE;
         const int kt = kv_lo + it * KT;
-        stage_tile<D, KT, kWaves, DV>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
-        stage_tile<D, KT, kWaves, DV>(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
+        kst.issue(buf, kbase, p.k_rs, kt, kv_len, w, lane);
+        vst.issue(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
     };
 
     const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
@@ -269,6 +272,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
 // splits the four products between its two waves:
 //   wave A (i):     S = Q K^T,  P = exp2(S c - lse2),  dV^T += dO^T P
 //   wave B (i + 4): dP = dO V^T, dS = P (dP - delta),   dK^T += Q^T dS
+//                   (the dP products start from -delta)
 // A hands P (rounded to the input type, C layout) to B through LDS; B runs
 // one stage behind A, so one barrier per stage orders everything. Each wave
 // holds one operand (K or V) and one accumulator set in registers, which keeps
@@ -349,6 +353,11 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     // (ldw = 0..3), lse by loader 0, delta by loader 1 (4 bytes per lane,
     // lane l -> row l).
     const int ldw = BIAS ? (role_a ? -1 : w - NP) : (role_a ? w : -1);
+    TileStager<D, QTL, NP, DV> qst, dost;
+    if (ldw >= 0) {
+        qst.init(p.q_rs, ldw, lane);
+        dost.init(p.do_rs, ldw, lane);
+    }
     auto stage = [&](int st) {
         char* buf = smem + (st % NBUF) * STAGE;
         const int h = stage_head(st);
@@ -360,9 +369,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         // the wait for those would also cover tile loads issued after them,
         // so the B waves load the tiles.
         if (ldw >= 0) {
-            stage_tile<D, QTL, NP, DV>(buf, p.q + hoff, p.q_rs, qt, q_len, ldw, lane);
-            stage_tile<D, QTL, NP, DV>(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * DV, p.do_rs,
-                                       qt, q_len, ldw, lane);
+            qst.issue(buf, p.q + hoff, p.q_rs, qt, q_len, ldw, lane);
+            dost.issue(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * DV, p.do_rs, qt, q_len, ldw,
+                       lane);
         }
         if (ldw == 0 || ldw == 1) {
             const int q = min(qt + lane, q_len - 1);        // rows past the end are masked
@@ -398,7 +407,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     if (n_stages > 0) {
         stage(0);
         wait_vmcnt<0>();
-        if (ldw == 0) reinterpret_cast<float*>(smem + 2 * TILE)[lane] *= -kLog2e;
+        if (ldw == 0 || ldw == 1) reinterpret_cast<float*>(smem + 2 * TILE)[64 * ldw + lane] *= ldw ? -1.f : -kLog2e;
         __syncthreads();
     }
     for (int st = 0; n_stages > 0 && st <= n_stages; ++st) {
@@ -497,7 +506,6 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             if (st > 0) {
                 const int sp = st - 1;
                 const char* Qs = smem + (sp % NBUF) * STAGE;
-                const float* dls = reinterpret_cast<const float*>(Qs + 2 * TILE) + 64;
                 const char* qtb = opaque(Qs + tbase);
                 const char* pb = smem + NBUF * STAGE + (sp & 1) * PSTAGE + pair * NQB * PBLK;
 #pragma unroll
@@ -507,15 +515,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                         const u32x4_t pp = ld16(pb + qb * PBLK + cc * 1024 + lane * 16);
                         float dsv[8];
 #pragma unroll
-                        for (int rg2 = 0; rg2 < 2; ++rg2) {
-                            const int qi = 32 * qb + 8 * (2 * cc + rg2) + 4 * hi;
-                            const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(dls + qi);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const int j = 4 * rg2 + e;              // r = 8 cc + j
-                                const float pr = (j & 1) ? hi16<T>(pp[j >> 1]) : lo16<T>(pp[j >> 1]);
-                                dsv[j] = pr * (pacc[qb][8 * cc + j] - d4[e]);
-                            }
+                        for (int j = 0; j < 8; ++j) {
+                            const float pr = (j & 1) ? hi16<T>(pp[j >> 1]) : lo16<T>(pp[j >> 1]);
+                            dsv[j] = pr * pacc[qb][8 * cc + j];
                         }
                         const u32x4_t bs = u32x4_t{T::pack2(dsv[0], dsv[1]), T::pack2(dsv[2], dsv[3]),
                                                    T::pack2(dsv[4], dsv[5]), T::pack2(dsv[6], dsv[7])};
@@ -526,9 +528,18 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                 }
             }
             if (st < n_stages) {
+                // dP - delta: the products accumulate onto -delta (the staged
+                // delta column is negated), so dS is one multiply per element
                 const char* drb = opaque(smem + (st % NBUF) * STAGE + TILE + rbase);
+                const float* dls = reinterpret_cast<const float*>(smem + (st % NBUF) * STAGE + 2 * TILE) + 64;
 #pragma unroll
-                for (int qb = 0; qb < NQB; ++qb) pacc[qb] = f32x16_t{};
+                for (int qb = 0; qb < NQB; ++qb)
+#pragma unroll
+                    for (int rg = 0; rg < 4; ++rg) {
+                        const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(dls + 32 * qb + 8 * rg + 4 * hi);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) pacc[qb][4 * rg + e] = d4[e];
+                    }
 #pragma unroll
                 for (int kc = 0; kc < DC; ++kc)
 #pragma unroll
@@ -536,12 +547,13 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                         pacc[qb] = mfma32<T>(row_operand<D>(drb, kc, 32 * qb), kvf[kc], pacc[qb]);
             }
         }
-        // stage st + 1 landed for this wave; loader 0 pre-scales its lse
-        // column (-lse log2 e) before the barrier publishes the stage
+        // stage st + 1 landed for this wave; loaders 0 and 1 turn their lse
+        // and delta columns into -lse log2 e and -delta before the barrier
+        // publishes the stage
         wait_vmcnt<0>();
-        if (ldw == 0 && st + 1 < n_stages) {
+        if ((ldw == 0 || ldw == 1) && st + 1 < n_stages) {
             float* l = reinterpret_cast<float*>(smem + ((st + 1) % NBUF) * STAGE + 2 * TILE);
-            l[lane] *= -kLog2e;
+            l[64 * ldw + lane] *= ldw ? -1.f : -kLog2e;
         }
         __syncthreads();
     }

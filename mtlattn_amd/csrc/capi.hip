@@ -57,6 +57,12 @@ bool aligned16(const void* ptr, int64_t row_stride, int dtype) {
     return ((uintptr_t)ptr & 15u) == 0 && (row_stride * elem_size(dtype)) % 16 == 0;
 }
 
+// The matrix-core kernels address a staged 64-row tile with 32-bit per-lane
+// byte offsets: row strides below 2^25 elements (the reference passes row
+// strides as uint32, src/ext.mm:48-51). Larger strides take the portable
+// kernels.
+bool tile_stride_ok(int64_t row_stride) { return row_stride >= 0 && row_stride < (int64_t(1) << 25); }
+
 // Shape/flag checks shared by every entry (src/ext.mm:306-331).
 int check_problem(const mtlattn_problem* p) {
     if (p == nullptr) return fail(MTLATTN_ERR_INVALID, "mtlattn: null problem descriptor");
@@ -236,7 +242,8 @@ int mtlattn_varlen_fwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
     a.geo = make_geo(p);
     a.q = q; a.q_rs = q_row_stride; a.k = k; a.k_rs = k_row_stride; a.v = v; a.v_rs = v_row_stride;
     a.o = out; a.lse = lse;
-    if (is16(p->dtype) && mfma_head_dim(p->head_dim) && vec_ok && !force_generic())
+    if (is16(p->dtype) && mfma_head_dim(p->head_dim) && vec_ok && tile_stride_ok(k_row_stride) &&
+        tile_stride_ok(v_row_stride) && !force_generic())
         return launch_status(launch_fwd_mfma(p->dtype, a, st), "flash forward");
     return launch_status(launch_fwd_generic(p->dtype, a, st), "generic forward");
 }
@@ -274,7 +281,8 @@ BwdArgs make_bwd(const mtlattn_problem* p, const void* q, int64_t qrs, const voi
 bool bwd_mfma_ok(const mtlattn_problem* p, const void* q, int64_t qrs, const void* k, int64_t krs, const void* v,
                  int64_t vrs, const void* dout, int64_t dors) {
     return is16(p->dtype) && mfma_head_dim(p->head_dim) && !force_generic() && aligned16(q, qrs, p->dtype) &&
-           aligned16(k, krs, p->dtype) && aligned16(v, vrs, p->dtype) && aligned16(dout, dors, p->dtype);
+           aligned16(k, krs, p->dtype) && aligned16(v, vrs, p->dtype) && aligned16(dout, dors, p->dtype) &&
+           tile_stride_ok(qrs) && tile_stride_ok(krs) && tile_stride_ok(vrs) && tile_stride_ok(dors);
 }
 
 }  // namespace

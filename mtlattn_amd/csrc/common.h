@@ -191,50 +191,87 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
-// One global_load_lds_dwordx4: each lane's 16 bytes at gptr land at LDS
-// lds + 16 * lane. Issued as inline asm so the compiler's wait-count
-// bookkeeping does not see it: the compiler conservatively waits for every
+// LDS direct loads (global_load_lds_*): each lane's data lands at LDS
+// lds + (4 or 16) * lane. Issued as inline asm so the compiler's wait-count
+// bookkeeping does not see them: the compiler conservatively waits for every
 // outstanding direct load before any transposed LDS read (ds_read_b64_tr)
 // and before barriers, which would drain the staging pipeline each tile.
 // Callers therefore order these loads themselves (wait_vmcnt, then a barrier)
 // before LDS reads of the staged data. `lds` (passed in M0) must be
 // wave-uniform. The s_nop covers the one wait state required between an M0
 // write and an LDS direct load.
-__device__ inline void lds_dma16(const void* gptr, const char* lds) {
-    const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "{m0}"(a) : "memory");
-}
-// Same for 4 bytes per lane (global_load_lds_dword): lane data lands at
-// lds + 4 * lane.
+//
+// 4 bytes per lane from a per-lane address.
 __device__ inline void lds_dma4(const void* gptr, const char* lds) {
     const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
     asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(gptr), "{m0}"(a) : "memory");
 }
+// 16 bytes per lane from a wave-uniform base plus a 32-bit per-lane byte
+// offset (the instruction's SADDR form: no 64-bit address arithmetic).
+__device__ inline void lds_dma16s(const void* sbase, uint32_t voff, const char* lds) {
+    const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(a) : "memory");
+}
 
-// Stage rows [row0, row0 + ROWS) of a [*, D] 16-bit matrix (row stride rs
+// Stages rows [row0, row0 + ROWS) of a [*, D] 16-bit matrix (row stride rs
 // elements) into a swizzled LDS tile with global_load_lds_dwordx4: each
 // instruction moves 1 KB and lands lane l's 16 bytes at tile + 16 l, so the
 // lane loads the global chunk that the swizzle maps to that LDS position.
-// Rows >= row_end read row row_end - 1 (finite data the kernels mask out).
 // NW waves share the ROWS * D * 2 / 1024 instructions; w must be uniform.
 // Rows of the source hold DV <= D values (head dims below the tile width):
 // chunks at or past DV / 8 repeat the row's last valid chunk (finite data
 // that the kernels' zero operand columns or discarded outputs never use).
+// The per-lane part is fixed once: off[j] is the byte offset, from the
+// tile's first row, of what this lane loads in its j-th instruction, so a
+// full tile costs its DMA instructions and no vector arithmetic (the row
+// base is scalar). A tile that runs past row_end recomputes the offsets with
+// rows >= row_end reading row row_end - 1 (finite data the kernels mask
+// out). The offsets are 32-bit: callers keep ROWS * 2 * rs below 2^32 (row
+// strides below 2^25 elements for 64-row tiles).
 template <int D, int ROWS, int NW, int DV = D>
-__device__ inline void stage_tile(char* tile, const uint16_t* base, int64_t rs, int row0, int row_end, int w,
-                                  int lane) {
+struct TileStager {
     static_assert(DV % 8 == 0 && DV <= D, "head dim");
-    constexpr int PER = ROWS * D * 2 / 1024;
     static_assert(ROWS * D * 2 % 1024 == 0, "tile must be a multiple of 1 KB");
-#pragma unroll
-    for (int i = w; i < PER; i += NW) {
+    static constexpr int PER = ROWS * D * 2 / 1024;     // instructions per tile
+    static constexpr int N = (PER + NW - 1) / NW;       // per loader wave
+    uint32_t off[N];
+
+    __device__ static int row_of(int i, int lane) { return (i * 1024 + lane * 16) / (2 * D); }
+    __device__ static uint32_t lane_off(int i, int lane, int grow, uint32_t rs2) {
         const int byte = i * 1024 + lane * 16;
-        const int row = byte / (2 * D);
-        const int chunk = min(((byte % (2 * D)) >> 4) ^ row_swz<D>(row), DV / 8 - 1);
-        const int grow = min(row0 + row, row_end - 1);
-        lds_dma16(base + (int64_t)grow * rs + chunk * 8, tile + i * 1024);
+        const int chunk = min(((byte % (2 * D)) >> 4) ^ row_swz<D>(row_of(i, lane)), DV / 8 - 1);
+        return (uint32_t)grow * rs2 + (uint32_t)chunk * 16u;
     }
-}
+    // w: this wave's loader index in [0, NW)
+    __device__ void init(int64_t rs, int w, int lane) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int i = w + j * NW;
+            off[j] = (PER % NW == 0 || i < PER) ? lane_off(i, lane, row_of(i, lane), (uint32_t)(2 * rs)) : 0u;
+        }
+    }
+    // rows [row0, row0 + ROWS) of base (row0 < row_end) into tile
+    __device__ void issue(char* tile, const uint16_t* base, int64_t rs, int row0, int row_end, int w,
+                          int lane) const {
+        const char* tb = reinterpret_cast<const char*>(base + (int64_t)row0 * rs);
+        if (row0 + ROWS <= row_end) {
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                const int i = w + j * NW;
+                if (PER % NW != 0 && i >= PER) break;
+                lds_dma16s(tb, off[j], tile + i * 1024);
+            }
+        } else {
+            const int rmax = max(row_end - 1 - row0, 0);
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                const int i = w + j * NW;
+                if (PER % NW != 0 && i >= PER) break;
+                lds_dma16s(tb, lane_off(i, lane, min(row_of(i, lane), rmax), (uint32_t)(2 * rs)), tile + i * 1024);
+            }
+        }
+    }
+};
 
 // Wait until at most N of this wave's vector memory operations are pending
 // (s_waitcnt vmcnt(N), other counters untouched); N <= 15.

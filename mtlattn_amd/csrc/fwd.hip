@@ -120,11 +120,15 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * DV;
     const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * DV + p.col0;
     // All 8 waves stage each tile straight from HBM into LDS (K then V).
+    TileStager<DK, kKT, kWaves, DV> kst;
+    TileStager<DVL, kKT, kWaves, DO> vst;
+    kst.init(p.k_rs, w, lane);
+    vst.init(p.v_rs, w, lane);
     auto stage = [&](int it) {
         char* buf = smem + (it % NBUF) * STAGE;
         const int kt = kv_lo + it * kKT;
-        stage_tile<DK, kKT, kWaves, DV>(buf, kbase, p.k_rs, kt, kv_len, w, lane);
-        stage_tile<DVL, kKT, kWaves, DO>(buf + KTILE, vbase, p.v_rs, kt, kv_len, w, lane);
+        kst.issue(buf, kbase, p.k_rs, kt, kv_len, w, lane);
+        vst.issue(buf + KTILE, vbase, p.v_rs, kt, kv_len, w, lane);
     };
 
     // per-lane LDS offsets: K operand rows 32 kb + l32 (chunk 2 kc + hi) and
