@@ -45,7 +45,8 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # GPU clocks ramp for ~60 ms of sustained load: the default warmup covers it
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
@@ -72,6 +73,35 @@ def avg_launch_ms(fn, n, stream):
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / n
+
+
+def warm(step, min_ms):
+    """Runs `step` (synchronised) until at least min_ms of it has run: GPU
+    clocks ramp under sustained load."""
+    import torch
+    t0 = time.perf_counter()
+    while True:
+        step()
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= min_ms:
+            return
+
+
+def step_kernel_ms(calls, n, stream):
+    """Average duration of each call in `calls` (one kernel launch each, run
+    in order as one step) over n steps, from HIP events recorded on `stream`
+    between consecutive launches."""
+    import torch
+    names = list(calls)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(n)]
+    torch.cuda.synchronize()
+    for i in range(n):
+        ev[i][0].record(stream)
+        for j, name in enumerate(names):
+            calls[name]()
+            ev[i][j + 1].record(stream)
+    torch.cuda.synchronize()
+    return {name: sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(n)) / n for j, name in enumerate(names)}
 
 
 def c3_inputs(seed):
@@ -101,19 +131,7 @@ def bench_c3(args):
         state["o"] = C.varlen_attention(q, k, v, cu, cu, L, scale, True, 0, lse, None)
         state["g"] = C.varlen_attention_bwd(q, k, v, state["o"], do, lse, cu, cu, scale, True, 0, None)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    o = state["o"]
-    fin = bool(torch.isfinite(o.float()).all().item()) and all(
-        bool(torch.isfinite(t.float()).all().item()) for t in state["g"])
-
-    # one kernel per launch through the C ABI, on torch's current stream
+    # the same step as four C-ABI calls (one kernel each) on torch's stream
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
     p = capi.problem_for(q, k, cu, cu, L, scale, causal=True)
@@ -127,7 +145,7 @@ def bench_c3(args):
     calls = {
         "fwd_mfma": lambda: capi.call("mtlattn_varlen_fwd", p, q.data_ptr(), rs, k.data_ptr(), rk, v.data_ptr(), rk,
                                       out2.data_ptr(), lse.data_ptr(), None, 0, sh),
-        "bwd_preprocess": lambda: capi.call("mtlattn_bwd_preprocess", p, o.data_ptr(), rs, do.data_ptr(), rs,
+        "bwd_preprocess": lambda: capi.call("mtlattn_bwd_preprocess", p, out2.data_ptr(), rs, do.data_ptr(), rs,
                                             delta.data_ptr(), sh),
         "bwd_dq": lambda: capi.call("mtlattn_bwd_dq", p, q.data_ptr(), rs, k.data_ptr(), rk, v.data_ptr(), rk,
                                     do.data_ptr(), rs, lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), bf, sh),
@@ -135,13 +153,23 @@ def bench_c3(args):
                                      do.data_ptr(), rs, lse.data_ptr(), delta.data_ptr(), dk.data_ptr(),
                                      dv.data_ptr(), bf, sh),
     }
-    calls["fwd_mfma"]()
-    calls["bwd_preprocess"]()
-    n = max(5, args.steps // 2)
-    kern_ms = {}
-    for name, fn in calls.items():
-        fn()
-        kern_ms[name] = avg_launch_ms(fn, n, stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # Per-kernel durations, straight after the timed steps (clocks and caches
+    # as there): HIP events on the launch stream between the four kernels of
+    # each step, over as many steps as the timed region.
+    n = args.steps
+    kern_ms = step_kernel_ms(calls, n, stream)
+    o = state["o"]
+    fin = bool(torch.isfinite(o.float()).all().item()) and all(
+        bool(torch.isfinite(t.float()).all().item()) for t in state["g"])
     pairs = c3_pairs(L, B)
     unit = D * Hq * pairs
     algo = {"fwd_mfma": 4.0 * unit, "bwd_preprocess": 0.0, "bwd_dq": 2.0 * unit, "bwd_dkv": 8.0 * unit}
@@ -206,9 +234,7 @@ def bench_configs(args):
             st["o"] = C.varlen_attention(q, k, v, cu, cu, max_q, scale, causal, window, lse, bias)
             st["g"] = C.varlen_attention_bwd(q, k, v, st["o"], do, lse, cu, cu, scale, causal, window, bias)
 
-        for _ in range(2):
-            step()
-        torch.cuda.synchronize()
+        warm(step, 100.0)
         n = max(3, args.steps // 4)
         t0 = time.perf_counter()
         for _ in range(n):

@@ -621,12 +621,23 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(const typename T::r
     delta[i] = acc;
 }
 
-// Zero the rows of a [total_rows, row_elems] 16/32-bit tensor that lie outside
-// [cu[0], cu[num_seqs]) -- rows no sequence owns receive no gradient.
-__global__ __launch_bounds__(256) void zero_outside_kernel(uint16_t* __restrict__ ptr, int64_t row_halves,
-                                                           int64_t total_rows, const int* __restrict__ cu,
-                                                           int num_seqs) {
-    int64_t first = cu[0], last = cu[num_seqs];
+// Zero the rows of [total_rows, row_elems] 16/32-bit tensors that lie outside
+// [cu[0], cu[num_seqs]) -- rows no sequence owns receive no gradient. One
+// launch covers up to three tensors (blockIdx.y picks the job).
+struct ZeroJob {
+    uint16_t* ptr;
+    int64_t row_halves, total_rows;
+    const int* cu;
+};
+struct ZeroJobs {
+    ZeroJob job[3];
+    int num_seqs;
+};
+__global__ __launch_bounds__(256) void zero_outside_kernel(ZeroJobs jobs) {
+    const ZeroJob& j = jobs.job[blockIdx.y];
+    uint16_t* __restrict__ ptr = j.ptr;
+    const int64_t row_halves = j.row_halves, total_rows = j.total_rows;
+    int64_t first = j.cu[0], last = j.cu[jobs.num_seqs];
     first = first < 0 ? 0 : (first > total_rows ? total_rows : first);
     last = last < first ? first : (last > total_rows ? total_rows : last);
     const int64_t head_end = first * row_halves, tail_begin = last * row_halves, end = total_rows * row_halves;
@@ -724,11 +735,16 @@ hipError_t launch_bwd_preprocess(int dtype, const Geometry& geo, const void* o, 
     return hipGetLastError();
 }
 
-hipError_t launch_zero_outside(void* ptr, int64_t row_bytes, int64_t total_rows, const int* cu, int num_seqs,
-                               hipStream_t st) {
-    if (total_rows <= 0 || row_bytes <= 0) return hipSuccess;
-    hipLaunchKernelGGL(zero_outside_kernel, dim3(64), dim3(256), 0, st, (uint16_t*)ptr, row_bytes / 2, total_rows,
-                       cu, num_seqs);
+hipError_t launch_zero_outside(const ZeroFill* fills, int n, int num_seqs, hipStream_t st) {
+    ZeroJobs jobs{};
+    jobs.num_seqs = num_seqs;
+    int used = 0;
+    for (int i = 0; i < n && i < 3; ++i) {
+        if (fills[i].total_rows <= 0 || fills[i].row_bytes <= 0) continue;
+        jobs.job[used++] = ZeroJob{(uint16_t*)fills[i].ptr, fills[i].row_bytes / 2, fills[i].total_rows, fills[i].cu};
+    }
+    if (used == 0) return hipSuccess;
+    hipLaunchKernelGGL(zero_outside_kernel, dim3(64, used), dim3(256), 0, st, jobs);
     return hipGetLastError();
 }
 

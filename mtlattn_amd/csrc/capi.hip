@@ -355,10 +355,10 @@ int mtlattn_varlen_bwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
     hipStream_t st = (hipStream_t)stream;
     const int64_t es = elem_size(p->dtype);
     const int64_t qrow = (int64_t)p->num_heads_q * p->head_dim * es, krow = (int64_t)p->num_heads_kv * p->head_dim * es;
-    hipError_t e = launch_zero_outside(dq, qrow, p->total_q, p->cu_seqlens_q, p->num_seqs, st);
-    if (e == hipSuccess) e = launch_zero_outside(dk, krow, p->total_kv, p->cu_seqlens_kv, p->num_seqs, st);
-    if (e == hipSuccess) e = launch_zero_outside(dv, krow, p->total_kv, p->cu_seqlens_kv, p->num_seqs, st);
-    return launch_status(e, "gradient tail fill");
+    const ZeroFill fills[3] = {{dq, qrow, p->total_q, p->cu_seqlens_q},
+                               {dk, krow, p->total_kv, p->cu_seqlens_kv},
+                               {dv, krow, p->total_kv, p->cu_seqlens_kv}};
+    return launch_status(launch_zero_outside(fills, 3, p->num_seqs, st), "gradient tail fill");
 }
 
 size_t mtlattn_attn_splitkv_workspace_size(const mtlattn_problem* p, int32_t num_splits) {

@@ -66,8 +66,14 @@ hipError_t launch_bwd_dq_mfma(int dtype, const BwdArgs& a, hipStream_t st);
 hipError_t launch_bwd_dkv_mfma(int dtype, const BwdArgs& a, hipStream_t st);
 hipError_t launch_bwd_dq_generic(int dtype, const BwdArgs& a, hipStream_t st);
 hipError_t launch_bwd_dkv_generic(int dtype, const BwdArgs& a, hipStream_t st);
-hipError_t launch_zero_outside(void* ptr, int64_t row_bytes, int64_t total_rows, const int* cu, int num_seqs,
-                               hipStream_t st);
+// Rows of a [total_rows, row_bytes] tensor outside [cu[0], cu[num_seqs]).
+struct ZeroFill {
+    void* ptr;
+    int64_t row_bytes, total_rows;
+    const int* cu;
+};
+// Zeroes those rows of up to three tensors in one launch.
+hipError_t launch_zero_outside(const ZeroFill* fills, int n, int num_seqs, hipStream_t st);
 hipError_t launch_decode(int dtype, const DecodeArgs& a, hipStream_t st);
 hipError_t launch_pad_pack(int esize, int B, int N, int H, int D, const void* src, int64_t sb, int64_t sh,
                            int64_t sn, const int* lens, int* cu, void* dst, hipStream_t st);

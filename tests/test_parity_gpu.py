@@ -527,6 +527,39 @@ def test_ragged_equals_per_sequence(mt):
         off += L
 
 
+def test_rows_outside_sequences(mt):
+    """cu_seqlens that start after row 0 and end before the last row: the
+    rows no sequence owns get zero dQ / dK / dV (all three cleared in one
+    launch), the owned rows match the oracle on the owned slice."""
+    _banner("rows outside [cu[0], cu[B]) get zero gradient")
+    lens = [100, 250]
+    q0, k0, tail = 3, 5, 7
+    g = torch.Generator().manual_seed(9)
+    Hq, Hkv, D, dt = 8, 2, 128, torch.bfloat16
+    q = randn((q0 + sum(lens) + tail, Hq, D), dt, g)
+    k = randn((k0 + sum(lens) + tail, Hkv, D), dt, g)
+    v = randn((k0 + sum(lens) + tail, Hkv, D), dt, g)
+    dout = randn((q.shape[0], Hq, D), dt, g)
+    cq = cu_of(lens) + q0
+    ck = cu_of(lens) + k0
+    qm, km, vm = (t.cuda().requires_grad_() for t in (q, k, v))
+    out = mt.varlen_attention(qm, km, vm, cq.cuda(), ck.cuda(), max(lens), causal=True)
+    out.backward(dout.cuda())
+    torch.cuda.synchronize()
+    for name, gr, lo in (("dQ", qm.grad, q0), ("dK", km.grad, k0), ("dV", vm.grad, k0)):
+        gr = gr.cpu()
+        hi = lo + sum(lens)
+        assert torch.count_nonzero(gr[:lo]) == 0 and torch.count_nonzero(gr[hi:]) == 0, f"{name} outside rows"
+    sl_q, sl_k = slice(q0, q0 + sum(lens)), slice(k0, k0 + sum(lens))
+    _, _, rq, rk, rv = oracle.varlen_forward_backward(q[sl_q], k[sl_k], v[sl_k], dout[sl_q], cu_of(lens), cu_of(lens),
+                                                      None, True)
+    errs = [(qm.grad.cpu()[sl_q].float() - rq).abs().max().item(),
+            (km.grad.cpu()[sl_k].float() - rk).abs().max().item(),
+            (vm.grad.cpu()[sl_k].float() - rv).abs().max().item()]
+    print(f"  dQ/dK/dV max_err={errs}", flush=True)
+    assert max(errs) < 4e-2
+
+
 def test_determinism(mt):
     """Forward and backward are bitwise run-to-run deterministic (no atomics)."""
     _banner("determinism fwd+bwd")
