@@ -91,7 +91,9 @@ int mtlattn_gpu_core_count(int device);
  * natural-log LSE per (row, head) when `lse` is non-NULL.
  * Replaces _C.varlen_attention (src/ext.mm:293-489) including its routing:
  * few-query / long-KV calls go to split-KV decode + combine
- * (src/ext.mm:367-390), everything else to the flash forward.
+ * (src/ext.mm:367-390; here also with a window or a bias, which the
+ * reference sends to its flash forward), everything else to the flash
+ * forward.
  *   out : contiguous [total_q, Hq, D], same dtype as q
  *   lse : NULL or fp32 [total_q, Hq] (rows with no allowed key get -inf)
  */
@@ -164,9 +166,11 @@ int mtlattn_bwd_dkv(const mtlattn_problem* p,
  * partial O and its LSE; a combine kernel merges them and also writes the
  * final LSE when `lse` is non-NULL. num_splits == 1 is a plain forward.
  * Replaces _C.attn_splitkv (src/ext.mm:716-773; kernels
- * src/attn_mpp.metal:384-535). Requires fp16/bf16, D in {64, 128}, no bias,
- * no window, max_seqlen_q * (Hq / Hkv) rows per kv head handled in groups of
- * 16. Workspace: fp32 partial rows of D values plus one LSE each, 16 rows per
+ * src/attn_mpp.metal:384-535). Requires fp16/bf16, D in {64, 128},
+ * max_seqlen_q <= 16 (query rows of a kv head handled in groups of 16).
+ * Bias and window are honoured (the reference's split path has neither);
+ * with a window the splits divide only the keys the sequence's rows can see.
+ * Workspace: fp32 partial rows of D values plus one LSE each, 16 rows per
  * (kv head, head group, sequence, split).
  */
 size_t mtlattn_attn_splitkv_workspace_size(const mtlattn_problem* p, int32_t num_splits);
@@ -182,7 +186,9 @@ int mtlattn_attn_splitkv(const mtlattn_problem* p,
  * decode routing would use for `p` (0 = the call is not routed to split-KV).
  * The automatic path cuts each sequence's KV into fixed-length chunks (about
  * 18 work items per CU) rather than a fixed number of splits per sequence,
- * so ragged KV lengths stay balanced. Retunes src/ext.mm:372-388. */
+ * so ragged KV lengths stay balanced; with a window each sequence gets a
+ * fixed number of equal splits of its window band instead (slots =
+ * num_seqs * splits). Retunes src/ext.mm:372-388. */
 int32_t mtlattn_decode_num_splits(const mtlattn_problem* p);
 
 /*

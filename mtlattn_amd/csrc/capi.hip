@@ -131,8 +131,7 @@ int decode_heads_per_group(int g, int max_q) {
 
 // Split-KV applicability without the routing heuristics (kernel limits).
 bool splitkv_supported(const mtlattn_problem* p) {
-    return is16(p->dtype) && decode_head_dim(p->head_dim) && p->bias == nullptr && p->window <= 0 &&
-           p->max_seqlen_q >= 1 && p->max_seqlen_q <= 16;
+    return is16(p->dtype) && decode_head_dim(p->head_dim) && p->max_seqlen_q >= 1 && p->max_seqlen_q <= 16;
 }
 
 // Partial rows of the split-KV workspace for ns equal splits per sequence
@@ -168,22 +167,38 @@ int run_splitkv(const mtlattn_problem* p, const void* q, int64_t qrs, const void
     return launch_status(launch_decode(p->dtype, a, st), "split-KV decode");
 }
 
-// KV chunk length (keys, a multiple of 32) of the automatic decode path, or
-// 0 when the call is not routed there. Reference gate (src/ext.mm:372-376):
-// few queries, long KV, no bias/window. Chunks are sized so that about 18
-// work items per CU exist (measured on MI355X: fewer leave a ragged last
-// round, more add per-item start-up and partial-row traffic); every wave
-// then streams the same number of bytes whatever the spread of KV lengths.
+// Work split of the automatic decode path (reference gate src/ext.mm:372-376:
+// few queries and long KV; here also with a window or a bias, which the
+// reference keeps off its split path). Without a window every sequence's KV
+// is cut into fixed chunks of `chunk` keys (a multiple of 256), sized so that
+// about 18 work items per CU exist (measured on MI355X: fewer leave a ragged
+// last round, more add per-item start-up and partial-row traffic), so every
+// wave streams the same number of bytes whatever the spread of KV lengths.
+// With a window only the last W + q_len - 1 keys of a sequence can be seen:
+// each sequence gets `ns` equal splits of that band instead (chunk == 0), so
+// the work items and the workspace scale with the band, not the KV length.
 constexpr int64_t kItemsPerCu = 18;
 
-int decode_chunk(const mtlattn_problem* p) {
-    if (check_problem(p) != MTLATTN_OK) return 0;
-    if (p->total_q <= 0 || env_set("MTLATTN_NO_SPLITKV") || force_generic() || !splitkv_supported(p)) return 0;
+struct DecodePlan {
+    int chunk = 0;    // > 0: fixed KV chunks of this many keys
+    int ns = 0;       // > 0: equal splits per sequence over the window band
+    bool routed() const { return chunk > 0 || ns > 0; }
+};
+
+DecodePlan decode_plan(const mtlattn_problem* p) {
+    DecodePlan plan;
+    if (check_problem(p) != MTLATTN_OK) return plan;
+    if (p->total_q <= 0 || env_set("MTLATTN_NO_SPLITKV") || force_generic() || !splitkv_supported(p)) return plan;
     const int64_t avg_kv = p->total_kv / (p->num_seqs > 0 ? p->num_seqs : 1);
-    if (avg_kv < 2048) return 0;
+    // keys a sequence's rows can see (band length with a window)
+    const int64_t band = p->window > 0 ? (int64_t)p->window + p->max_seqlen_q - 1 : avg_kv;
+    const int64_t eff = avg_kv < band ? avg_kv : band;
+    if (eff < 2048) return plan;
     const int g = p->num_heads_q / p->num_heads_kv;
     const int64_t groups = (int64_t)p->num_heads_kv * (g / decode_heads_per_group(g, p->max_seqlen_q));
-    int64_t c = (p->total_kv * groups + (int64_t)device_cus() * kItemsPerCu - 1) / ((int64_t)device_cus() * kItemsPerCu);
+    const int64_t work = p->window > 0 ? eff * p->num_seqs : p->total_kv;
+    const int64_t items = (int64_t)device_cus() * kItemsPerCu;
+    int64_t c = (work * groups + items - 1) / items;
     if (const char* e = std::getenv("MTLATTN_DECODE_CHUNK")) {   // tuning override (keys)
         const long v = std::strtol(e, nullptr, 10);
         if (v > 0) c = v;
@@ -191,7 +206,15 @@ int decode_chunk(const mtlattn_problem* p) {
     c = (c + 128) / 256 * 256;      // nearest multiple of 256 keys
     if (c < 256) c = 256;
     if (c > 8192) c = 8192;
-    return (int)c;
+    if (p->window <= 0) {
+        plan.chunk = (int)c;
+    } else {
+        // the band starts at a tile boundary at or below coff - W + 1: up to
+        // 31 more keys than W + q_len - 1
+        const int64_t span = band + 31;
+        plan.ns = (int)((span + c - 1) / c);
+    }
+    return plan;
 }
 
 }  // namespace
@@ -212,15 +235,16 @@ int mtlattn_gpu_core_count(int device) {
 }
 
 int32_t mtlattn_decode_num_splits(const mtlattn_problem* p) {
-    const int c = decode_chunk(p);
-    if (c <= 0) return 0;
-    const int64_t slots = p->total_kv / c + p->num_seqs + 1;
+    const DecodePlan plan = decode_plan(p);
+    if (!plan.routed()) return 0;
+    const int64_t slots = plan.chunk > 0 ? p->total_kv / plan.chunk + p->num_seqs + 1
+                                         : (int64_t)p->num_seqs * plan.ns;
     return slots > 0x7fffffff ? 0x7fffffff : (int32_t)slots;
 }
 
 size_t mtlattn_varlen_fwd_workspace_size(const mtlattn_problem* p) {
-    const int c = decode_chunk(p);
-    return c > 0 ? splitkv_bytes(p, 0, c) : 0;
+    const DecodePlan plan = decode_plan(p);
+    return plan.routed() ? splitkv_bytes(p, plan.ns, plan.chunk) : 0;
 }
 
 int mtlattn_varlen_fwd(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
@@ -232,12 +256,12 @@ int mtlattn_varlen_fwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
     if (q == nullptr || out == nullptr || (p->total_kv > 0 && (k == nullptr || v == nullptr)))
         return fail(MTLATTN_ERR_INVALID, "mtlattn: null q/k/v/out pointer");
     hipStream_t st = (hipStream_t)stream;
-    const int chunk = decode_chunk(p);
+    const DecodePlan plan = decode_plan(p);
     const bool vec_ok = aligned16(q, q_row_stride, p->dtype) && aligned16(k, k_row_stride, p->dtype) &&
                         aligned16(v, v_row_stride, p->dtype) && ((uintptr_t)out & 15u) == 0;
-    if (chunk > 0 && vec_ok)
-        return run_splitkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, 0, chunk, workspace,
-                           workspace_bytes, st);
+    if (plan.routed() && vec_ok)
+        return run_splitkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, plan.ns, plan.chunk,
+                           workspace, workspace_bytes, st);
     FwdArgs a;
     a.geo = make_geo(p);
     a.q = q; a.q_rs = q_row_stride; a.k = k; a.k_rs = k_row_stride; a.v = v; a.v_rs = v_row_stride;

@@ -21,6 +21,12 @@
 //     of its group); the combine kernel merges a sequence's items with LSE
 //     weights and, unlike the reference's (src/attn_mpp.metal:498-521), also
 //     writes the final LSE.
+//   * Sliding window and additive bias, which the reference keeps off this
+//     path (src/ext.mm:372-374): with a window the equal splits cover only
+//     the keys some row of the sequence can see (from coff - W + 1, rounded
+//     down to a tile), and elements below a row's band are masked; the fp32
+//     bias of the lane's row and keys is loaded with the K/V tile it belongs
+//     to and added as bias * log2 e (columns at or past bias_cols read as 0).
 #include "common.h"
 #include "kernels.h"
 #include "../../include/mtlattn_capi.h"
@@ -41,11 +47,14 @@ struct DecKParams {
     const uint16_t* q; const uint16_t* k; const uint16_t* v;
     float* o_part; float* lse_part;
     const int* cu_q; const int* cu_kv;
+    const float* bias;
     int64_t q_rs, k_rs, v_rs;
+    int64_t bias_qs, bias_hs, bias_cols;
     int64_t total_q, total_kv;
     int num_seqs, hq, hkv, g, hpb, n_hg, ns, chunk, n_slots;
     float scale_log2;
-    int causal;
+    int causal, window;
+    int bias_v4;      // bias rows 16-byte aligned (pointer and strides)
 };
 
 // KV range [ks, ke) of work item `slot` of sequence s (false: no keys).
@@ -62,9 +71,15 @@ __device__ inline bool item_range(const DecKParams& p, int slot, int& s, int& ks
         const int split = slot - s * p.ns;
         const SeqRange kr = seq_range(p.cu_kv, s, p.total_kv);
         kv_len = kr.end - kr.start;
-        int c = (kv_len + p.ns - 1) / p.ns;
+        // with a window, split only the keys the sequence's rows can see
+        int lo = 0;
+        if (p.window > 0) {
+            const SeqRange qr = seq_range(p.cu_q, s, p.total_q);
+            lo = max(0, kv_len - (qr.end - qr.start) - p.window + 1) / kDecKT * kDecKT;
+        }
+        int c = (kv_len - lo + p.ns - 1) / p.ns;
         c = (c + kDecKT - 1) / kDecKT * kDecKT;
-        ks = split * c;
+        ks = lo + split * c;
         ke = min(kv_len, ks + c);
     }
     return ke > ks;
@@ -76,7 +91,7 @@ __device__ inline uint32_t dec_tr_offset(int row, int group) {
     return (uint32_t)(row * 64 + ((group ^ f) << 3));
 }
 
-template <typename T, int D>
+template <typename T, int D, bool BIAS>
 __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams p) {
     constexpr int KC = D / 32;          // 32-wide k-chunks over D (QK^T)
     constexpr int DB = D / 16;          // 16-row output blocks over D
@@ -122,9 +137,36 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
     const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * D;
     const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * D;
 
-    // Register tiles: K A-operands [2 key blocks][KC], V rows [VU units][4 keys].
+    // this lane's bias row (head of the row, or the broadcast head)
+    const float* brow = nullptr;
+    if (BIAS) brow = p.bias + grow * p.bias_qs + (int64_t)head * p.bias_hs;
+
+    // Register tiles: K A-operands [2 key blocks][KC], V rows [VU units][4 keys],
+    // bias of the lane's row for its 8 keys.
     u32x4_t ka[2][KC], vr[VU][4];
-    auto load = [&](int kt, u32x4_t (&ka_)[2][KC], u32x4_t (&vr_)[VU][4]) {
+    float bb[2][4];
+    auto load = [&](int kt, u32x4_t (&ka_)[2][KC], u32x4_t (&vr_)[VU][4], float (&bb_)[2][4]) {
+        if (BIAS) {
+            // the lane's 4 keys of a 16-key block are contiguous: one 16-byte
+            // load each when the whole tile lies within the bias columns
+            if (p.bias_v4 && kt + kDecKT <= p.bias_cols) {
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    const f32x4_t b4 = *reinterpret_cast<const f32x4_t*>(brow + kt + 16 * mb + 4 * lg);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) bb_[mb][r] = b4[r];
+                }
+            } else {
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int key = kt + 16 * mb + 4 * lg + r;
+                        const float b = brow[min(key, (int)p.bias_cols - 1)];
+                        bb_[mb][r] = key < p.bias_cols ? b : 0.f;
+                    }
+            }
+        }
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
             // keys past the split end read its last key: finite, masked to P = 0
@@ -153,7 +195,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
     // Two register sets alternate: tile it is computed from set it % 2 while
     // the loads of tiles it + 1 and it + 2 are in flight.
     u32x4_t ka2[2][KC], vr2[VU][4];
-    auto step = [&](int it, u32x4_t (&ka)[2][KC], u32x4_t (&vr)[VU][4]) __attribute__((always_inline)) {
+    float bb2[2][4];
+    auto step = [&](int it, u32x4_t (&ka)[2][KC], u32x4_t (&vr)[VU][4], float (&bb)[2][4])
+                    __attribute__((always_inline)) {
         const int kt = ks + it * kDecKT;
         // stage V^T of this tile in the wave's LDS buffer
         __builtin_amdgcn_wave_barrier();
@@ -173,10 +217,20 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) sc[mb] = mfma16<T>(ka[mb][kc], qf[kc], sc[mb]);
         }
+        // this tile's bias, before the register set is refilled
+        float bt[2][4];
+        if (BIAS) {
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) bt[mb][r] = bb[mb][r];
+        }
         // refill this register set with tile it + 2 (two tiles of latency cover)
-        if (it + 2 < n_tiles) load(kt + 2 * kDecKT, ka, vr);
+        if (it + 2 < n_tiles) load(kt + 2 * kDecKT, ka, vr, bb);
 
-        const bool need_mask = (kt + kDecKT > ke) || (p.causal && kt + kDecKT - 1 > coff);
+        // (rows' window bands start at qi + coff - W + 1 <= coff + q_len - W)
+        const bool need_mask = (kt + kDecKT > ke) || (p.causal && kt + kDecKT - 1 > coff) ||
+                               (p.window > 0 && kt < coff + q_len - p.window);
         float mx = kNegInf;
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
@@ -187,8 +241,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
                 if (need_mask) {
                     ok = ok && key < ke;
                     if (p.causal) ok = ok && key <= qi + coff;
+                    if (p.window > 0) ok = ok && key > qi + coff - p.window;
                 }
-                const float x = ok ? sc[mb][r] * p.scale_log2 : kNegInf;
+                float x = sc[mb][r] * p.scale_log2;
+                if (BIAS) x = fmaf(bt[mb][r], kLog2e, x);
+                x = ok ? x : kNegInf;
                 sc[mb][r] = x;
                 mx = fmaxf(mx, x);
             }
@@ -224,11 +281,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
             oacc[db] = mfma16<T>(u32x4_t{x0[0], x0[1], x1[0], x1[1]}, pf, oacc[db]);
         }
     };
-    if (n_tiles > 0) load(ks, ka, vr);
-    if (n_tiles > 1) load(ks + kDecKT, ka2, vr2);
+    if (n_tiles > 0) load(ks, ka, vr, bb);
+    if (n_tiles > 1) load(ks + kDecKT, ka2, vr2, bb2);
     for (int it = 0; it < n_tiles; it += 2) {
-        step(it, ka, vr);
-        if (it + 1 < n_tiles) step(it + 1, ka2, vr2);
+        step(it, ka, vr, bb);
+        if (it + 1 < n_tiles) step(it + 1, ka2, vr2, bb2);
     }
 
     // l_run is split over the 4 lane groups holding a row's keys.
@@ -318,6 +375,7 @@ hipError_t launch_typed(const DecodeArgs& a, hipStream_t st) {
     p.q = (const uint16_t*)a.q; p.k = (const uint16_t*)a.k; p.v = (const uint16_t*)a.v;
     p.o_part = a.o_part; p.lse_part = a.lse_part;
     p.cu_q = g.cu_q; p.cu_kv = g.cu_kv;
+    p.bias = g.bias; p.bias_qs = g.bias_qs; p.bias_hs = g.bias_hs; p.bias_cols = g.bias_cols;
     p.q_rs = a.q_rs; p.k_rs = a.k_rs; p.v_rs = a.v_rs;
     p.total_q = g.total_q; p.total_kv = g.total_kv;
     p.num_seqs = g.num_seqs; p.hq = g.hq; p.hkv = g.hkv; p.g = g.g;
@@ -335,11 +393,19 @@ hipError_t launch_typed(const DecodeArgs& a, hipStream_t st) {
     p.n_slots = (int)slots;
     p.scale_log2 = g.scale * kLog2e;
     p.causal = g.causal;
+    p.window = g.window;
+    p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0;
     const int64_t waves = (int64_t)g.hkv * p.n_hg * p.n_slots;
     const int64_t blocks = (waves + kDecWaves - 1) / kDecWaves;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    if (blocks > 0)
-        hipLaunchKernelGGL((decode_split_kernel<T, D>), dim3((unsigned)blocks), dim3(kDecWaves * 64), 0, st, p);
+    if (blocks > 0) {
+        if (p.bias != nullptr)
+            hipLaunchKernelGGL((decode_split_kernel<T, D, true>), dim3((unsigned)blocks), dim3(kDecWaves * 64), 0, st,
+                               p);
+        else
+            hipLaunchKernelGGL((decode_split_kernel<T, D, false>), dim3((unsigned)blocks), dim3(kDecWaves * 64), 0,
+                               st, p);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t rh = g.total_q * g.hq;

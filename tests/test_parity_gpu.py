@@ -282,6 +282,42 @@ def test_decode_small_chunks(mt, monkeypatch):
     _fwd(mt, "decode 256-key chunks, non-causal D=64", [1, 1], [2304, 2560], 8, 8, 64, torch.bfloat16, seed=13)
 
 
+def _decode_routed(q_lens, kv_lens, Hq, Hkv, D, window=0, bias=None, causal=True):
+    from mtlattn_amd import capi
+    q = torch.empty((sum(q_lens), Hq, D), dtype=torch.bfloat16, device="cuda")
+    k = torch.empty((sum(kv_lens), Hkv, D), dtype=torch.bfloat16, device="cuda")
+    p = capi.problem_for(q, k, cu_of(q_lens, "cuda"), cu_of(kv_lens, "cuda"), max(q_lens), 0.1, causal=causal,
+                         window=window, bias=None if bias is None else bias.cuda())
+    return capi.lib().mtlattn_decode_num_splits(p)
+
+
+def test_decode_window_bias(mt, monkeypatch):
+    """Sliding window and additive bias on the split-KV decode path (the
+    reference sends both to its flash forward, src/ext.mm:372-374): the
+    window's equal splits cover only the band, rows' bands are masked per
+    element, the bias is added per (row, key). Every case is checked to be
+    routed to split-KV, then compared with the oracle (O and LSE)."""
+    h, b = torch.float16, torch.bfloat16
+    cases = [
+        ("window 2500, ragged + empty, q_len 1-2", [1, 1, 2, 1], [9000, 5000, 3000, 0], 8, 2, 128, h, True, 2500, None),
+        ("window wider than the KV", [1, 1], [4000, 2600], 8, 8, 128, b, True, 6000, None),
+        ("window non-causal D=64", [1, 3], [7000, 5000], 8, 8, 64, b, False, 3000, None),
+        ("bias per head", [1, 1], [8192, 4000], 8, 8, 128, h, True, 0, "head"),
+        ("bias broadcast GQA 16/2, q_len 3", [3, 1], [6000, 5000], 16, 2, 128, b, True, 0, "bcast"),
+        ("window + bias GQA", [2, 1], [9000, 4500], 8, 2, 128, h, True, 2100, "head"),
+    ]
+    for chunk in (None, "256"):
+        if chunk:
+            monkeypatch.setenv("MTLATTN_DECODE_CHUNK", chunk)
+        for name, ql, kl, hq, hkv, d, dt, causal, w, bk in cases:
+            bias = None
+            if bk is not None:
+                bias = _make_bias(sum(ql), 1 if bk == "bcast" else hq, max(kl), bk == "bcast", seed=len(name))
+            assert _decode_routed(ql, kl, hq, hkv, d, w, bias, causal) > 0, f"{name}: not routed to split-KV"
+            _fwd(mt, f"decode {name} (chunk {chunk or 'auto'})", ql, kl, hq, hkv, d, dt, causal=causal, window=w,
+                 bias=bias, seed=len(name))
+
+
 # causal (tests/test_correctness.py:367-371)
 def test_causal_cases(mt):
     _fwd(mt, "causal self D=128", [1024], [1024], 12, 12, 128, torch.float16, causal=True)
