@@ -397,8 +397,6 @@ int mtlattn_attn_splitkv(const mtlattn_problem* p, const void* q, int64_t q_row_
     if (rc != MTLATTN_OK) return rc;
     if (!is16(p->dtype)) return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: half/bf16");
     if (!decode_head_dim(p->head_dim)) return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: D in {64,128}");
-    if (p->bias != nullptr || p->window > 0)
-        return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: no attn_mask or window on the split-KV path");
     if (p->max_seqlen_q < 1 || p->max_seqlen_q > 16)
         return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: max_seqlen_q must be in [1, 16]");
     if (num_splits < 1 || num_splits > 4096) return fail(MTLATTN_ERR_INVALID, "splitkv: num_splits in [1, 4096]");

@@ -170,16 +170,20 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> varlen_attention_bwd(
     return {dQ, dK, dV};
 }
 
-// _C.attn_splitkv (src/ext.mm:716-773).
+// _C.attn_splitkv (src/ext.mm:716-773). `window` and `attn_bias` (after the
+// reference's arguments) have no counterpart there: its split path takes
+// neither.
 at::Tensor attn_splitkv(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& cu_q_in,
                         const at::Tensor& cu_kv_in, int64_t max_seqlen_q, double scale, bool causal,
-                        int64_t num_splits) {
+                        int64_t num_splits, int64_t window, c10::optional<at::Tensor> attn_bias) {
     check_qkv(q, k, v);
     check_cu(cu_q_in, cu_kv_in, q);
     const c10::OptionalDeviceGuard guard(q.device());
     auto cu_q = cu_q_in.contiguous(), cu_kv = cu_kv_in.contiguous();
     auto out = at::empty({q.size(0), q.size(1), q.size(2)}, q.options());
-    mtlattn_problem p = make_problem(q, k, cu_q, cu_kv, max_seqlen_q, scale, causal, 0);
+    mtlattn_problem p = make_problem(q, k, cu_q, cu_kv, max_seqlen_q, scale, causal, window);
+    at::Tensor bias_keep;
+    fill_bias(p, attn_bias, q, bias_keep);
     const size_t ws_bytes = mtlattn_attn_splitkv_workspace_size(&p, (int32_t)num_splits);
     at::Tensor ws = workspace((int64_t)ws_bytes, q);
     check_rc(mtlattn_attn_splitkv(&p, q.data_ptr(), row_stride(q), k.data_ptr(), row_stride(k), v.data_ptr(),
@@ -299,7 +303,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("abi_version", [] { return mtlattn_abi_version(); }, "C ABI version of libmtlattn_hip.so");
     m.def("attn_splitkv", &attn_splitkv, "split-KV decode with an explicit split count (test entry)", py::arg("q"),
           py::arg("k"), py::arg("v"), py::arg("cu_q"), py::arg("cu_kv"), py::arg("max_seqlen_q"), py::arg("scale"),
-          py::arg("causal"), py::arg("num_splits"));
+          py::arg("causal"), py::arg("num_splits"), py::arg("window") = 0, py::arg("attn_bias") = c10::nullopt);
     m.def("mpp_bwd_dkv", &mpp_bwd_dkv, "dK/dV backward kernel, fp32 outputs (test entry)", py::arg("q"), py::arg("k"),
           py::arg("v"), py::arg("dO"), py::arg("lse"), py::arg("delta"), py::arg("cu_q"), py::arg("cu_kv"),
           py::arg("max_seqlen_kv"), py::arg("scale"), py::arg("causal") = false, py::arg("window") = 0,

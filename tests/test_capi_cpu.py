@@ -144,7 +144,8 @@ def _c5_like(**kw):
 
 def test_decode_routing(lib, monkeypatch):
     """Reference gate (src/ext.mm:372-376): few queries, long KV, fp16/bf16,
-    D in {64,128}, no bias, no window."""
+    D in {64,128}; unlike the reference, a bias or a window (whose band is
+    long enough) is routed too."""
     monkeypatch.delenv("MTLATTN_NO_SPLITKV", raising=False)
     monkeypatch.delenv("MTLATTN_NO_MPP", raising=False)
     monkeypatch.delenv("MTLATTN_NO_MFMA", raising=False)
@@ -159,8 +160,19 @@ def test_decode_routing(lib, monkeypatch):
     # 8 kv heads x 1 head group (8 heads x q_len 1 fill a 16-row group)
     assert lib.mtlattn_varlen_fwd_workspace_size(ctypes.byref(_c5_like())) == _splitkv_bytes(8 * slots * 16, 128)
     for kw in (dict(dtype=F32), dict(head_dim=96), dict(window=128), dict(max_seqlen_q=17),
-               dict(total_kv=64 * 2000), dict(bias=FAKE, bias_kv_cols=10)):
+               dict(total_kv=64 * 2000)):
         assert lib.mtlattn_decode_num_splits(ctypes.byref(_c5_like(**kw))) == 0, kw
+    # a bias changes nothing in the split plan
+    assert lib.mtlattn_decode_num_splits(ctypes.byref(_c5_like(bias=FAKE, bias_kv_cols=10))) == slots
+    # a window: equal splits of the band (W + q_len - 1 keys, plus up to 31
+    # below it for the tile-aligned start) per sequence, the split length
+    # sized like the chunk for the band's work (64 sequences x 4096 keys)
+    c = -(-(64 * 4096 * 8) // (256 * 18))
+    c = (c + 128) // 256 * 256
+    ns = -(-(4096 + 31) // c)
+    assert lib.mtlattn_decode_num_splits(ctypes.byref(_c5_like(window=4096))) == 64 * ns
+    assert lib.mtlattn_varlen_fwd_workspace_size(ctypes.byref(_c5_like(window=4096))) == \
+        _splitkv_bytes(8 * 64 * ns * 16, 128)
     monkeypatch.setenv("MTLATTN_NO_SPLITKV", "1")
     assert lib.mtlattn_decode_num_splits(ctypes.byref(_c5_like())) == 0
 
@@ -169,9 +181,14 @@ def test_splitkv_entry_validation(lib):
     p = problem(dtype=F32, max_seqlen_q=1)
     rc = lib.mtlattn_attn_splitkv(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, None, 2, None, 0, None)
     assert rc == ERR_UNSUPPORTED and b"half/bf16" in lib.mtlattn_last_error()
-    p = problem(max_seqlen_q=1, window=4)
+    p = problem(max_seqlen_q=17)
     rc = lib.mtlattn_attn_splitkv(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, None, 2, None, 0, None)
     assert rc == ERR_UNSUPPORTED
+    # a window passes validation (the split path honours it): the empty
+    # workspace is what fails
+    p = problem(max_seqlen_q=1, window=4)
+    rc = lib.mtlattn_attn_splitkv(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, None, 2, None, 0, None)
+    assert rc == ERR_WORKSPACE
     p = problem(max_seqlen_q=1)
     rc = lib.mtlattn_attn_splitkv(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, None, 0, None, 0, None)
     assert rc == ERR_INVALID

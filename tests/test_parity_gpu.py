@@ -547,6 +547,24 @@ def test_split_kv_invariants(mt):
         assert (o - outs[0]).abs().max().item() < 2e-2
 
 
+def test_split_kv_window_bias(mt):
+    """Explicit split counts with a window (splits of the band only) and a
+    per-head bias, through _C.attn_splitkv's window/attn_bias arguments."""
+    _banner("split-KV num_splits sweep, window + bias")
+    q_lens, kv_lens = [1, 2, 1], [5000, 2100, 9001]
+    q, k, v = _inputs(q_lens, kv_lens, 8, 2, 128, torch.bfloat16, seed=3)
+    bias = _make_bias(sum(q_lens), 8, max(kv_lens), False, seed=4)
+    cq, ck = cu_of(q_lens, "cuda"), cu_of(kv_lens, "cuda")
+    for w, b in ((1500, None), (0, bias), (3000, bias)):
+        ref, _ = oracle.varlen_forward(q, k, v, cu_of(q_lens), cu_of(kv_lens), 1 / math.sqrt(128), True, w, b)
+        for ns in (1, 3, 16):
+            o = mt._C.attn_splitkv(q.cuda(), k.cuda(), v.cuda(), cq, ck, 2, 1 / math.sqrt(128), True, ns, window=w,
+                                   attn_bias=None if b is None else b.cuda()).cpu()
+            err = (o.float() - ref).abs().max().item()
+            print(f"  window={w} bias={b is not None} ns={ns} max_err={err:.3e}", flush=True)
+            assert err < 3e-2
+
+
 def test_ragged_equals_per_sequence(mt):
     """A ragged batch equals per-sequence calls, bitwise (varlen bookkeeping)."""
     _banner("ragged == per-sequence (bitwise)")
