@@ -182,6 +182,36 @@ int mtlattn_attn_splitkv(const mtlattn_problem* p,
                          void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/*
+ * Decode over a paged KV cache. No counterpart in the reference (it has no
+ * paged KV); the layout is FlashAttention's varlen call with a block table.
+ * Same computation as the forward (causal, window, bias, LSE) for
+ * max_seqlen_q <= 16, fp16/bf16, D in {64, 128}, through split-KV + combine.
+ *   k_cache / v_cache : [num_pages, page_size, Hkv, D], token row strides
+ *                       k_row_stride / v_row_stride (elements); a page is
+ *                       page_size consecutive token rows
+ *   block_table       : int32 [num_seqs, block_table_stride] on the device;
+ *                       logical key j of sequence s is row j % page_size of
+ *                       page block_table[s * block_table_stride + j / page_size]
+ *                       (page indices are clamped to [0, num_pages))
+ *   p->cu_seqlens_kv  : logical KV lengths (prefix sums); p->total_kv is an
+ *                       upper bound on cu_seqlens_kv[num_seqs]
+ *   page_size         : a multiple of 16
+ *   max_seqlen_kv     : bound on the logical KV lengths (sizes the splits)
+ * Workspace: mtlattn_paged_decode_workspace_size(p, max_seqlen_kv) bytes.
+ */
+size_t mtlattn_paged_decode_workspace_size(const mtlattn_problem* p, int64_t max_seqlen_kv);
+int mtlattn_paged_decode(const mtlattn_problem* p,
+                         const void* q, int64_t q_row_stride,
+                         const void* k_cache, int64_t k_row_stride,
+                         const void* v_cache, int64_t v_row_stride,
+                         int32_t page_size, int64_t num_pages,
+                         const int32_t* block_table, int64_t block_table_stride,
+                         int64_t max_seqlen_kv,
+                         void* out, float* lse,
+                         void* workspace, size_t workspace_bytes,
+                         void* stream);
+
 /* Number of split-KV work-item slots per (kv head, head group) the forward's
  * decode routing would use for `p` (0 = the call is not routed to split-KV).
  * The automatic path cuts each sequence's KV into fixed-length chunks (about

@@ -138,6 +138,26 @@ def flash_attn_varlen_kvpacked_func(q, kv, cu_seqlens_q, cu_seqlens_k, max_seqle
                             causal=causal, window=_window_from_kwargs(window, kwargs))
 
 
+def paged_decode(q, k_cache, v_cache, cu_seqlens_q, cu_seqlens_kv, block_table, max_seqlen_q,
+                 max_seqlen_kv, scale=None, causal=False, window=0, attn_bias=None, lse_out=None):
+    """Decode (max_seqlen_q <= 16 query rows per sequence) over a paged KV
+    cache; the reference has no paged KV, the layout is FlashAttention's
+    varlen call with a block table.
+
+    q: [Mq, Hq, D]; k_cache, v_cache: [num_pages, page_size, Hkv, D] with
+    page_size a multiple of 16; block_table: int [B, max_pages], logical key
+    j of sequence s in page block_table[s, j // page_size]; cu_seqlens_kv:
+    int [B+1] prefix sums of the logical KV lengths; max_seqlen_kv bounds
+    them. causal / window / attn_bias as in varlen_attention; lse_out: an
+    optional fp32 [Mq, Hq] tensor receiving the natural-log LSE. Forward
+    only (fp16/bf16, D in {64, 128}). Returns [Mq, Hq, D]."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    return _C.paged_decode(q, k_cache, v_cache, cu_seqlens_q.int(), cu_seqlens_kv.int(), block_table.int(),
+                           int(max_seqlen_q), int(max_seqlen_kv), float(scale), bool(causal), int(window),
+                           lse_out, _prep_bias(attn_bias))
+
+
 # ---- dense scaled_dot_product_attention adapter ----
 
 _ORIG_SDPA = None

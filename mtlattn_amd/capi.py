@@ -60,6 +60,9 @@ SIGNATURES = {
     "mtlattn_attn_splitkv_workspace_size": (_sz, [_P, _i32]),
     "mtlattn_attn_splitkv": (ctypes.c_int, [_P, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp, _sz, _vp]),
     "mtlattn_decode_num_splits": (_i32, [_P]),
+    "mtlattn_paged_decode_workspace_size": (_sz, [_P, _i64]),
+    "mtlattn_paged_decode": (ctypes.c_int, [_P, _vp, _i64, _vp, _i64, _vp, _i64, _i32, _i64, _vp, _i64, _i64, _vp,
+                                            _vp, _vp, _sz, _vp]),
     "mtlattn_pack_padded": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "mtlattn_unpack_padded": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                              _vp]),

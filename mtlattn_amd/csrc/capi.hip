@@ -148,8 +148,15 @@ size_t splitkv_bytes(const mtlattn_problem* p, int ns, int chunk) {
     return ((o + 255) & ~(size_t)255) + rows * sizeof(float);
 }
 
+struct PagedKV {
+    const int32_t* block_table;
+    int64_t bt_stride, num_pages;
+    int page_size;
+};
+
 int run_splitkv(const mtlattn_problem* p, const void* q, int64_t qrs, const void* k, int64_t krs, const void* v,
-                int64_t vrs, void* out, float* lse, int ns, int chunk, void* ws, size_t ws_bytes, hipStream_t st) {
+                int64_t vrs, void* out, float* lse, int ns, int chunk, void* ws, size_t ws_bytes, hipStream_t st,
+                const PagedKV* paged = nullptr) {
     const size_t need = splitkv_bytes(p, ns, chunk);
     if (ws_bytes < need || (ws == nullptr && need > 0))
         return fail(MTLATTN_ERR_WORKSPACE, "mtlattn: split-KV workspace too small (%zu < %zu bytes)", ws_bytes,
@@ -164,6 +171,12 @@ int run_splitkv(const mtlattn_problem* p, const void* q, int64_t qrs, const void
     a.num_splits = ns;
     a.chunk = chunk;
     a.max_q = p->max_seqlen_q;
+    if (paged != nullptr) {
+        a.block_table = paged->block_table;
+        a.bt_stride = paged->bt_stride;
+        a.page_size = paged->page_size;
+        a.num_pages = (int)paged->num_pages;
+    }
     return launch_status(launch_decode(p->dtype, a, st), "split-KV decode");
 }
 
@@ -185,18 +198,11 @@ struct DecodePlan {
     bool routed() const { return chunk > 0 || ns > 0; }
 };
 
-DecodePlan decode_plan(const mtlattn_problem* p) {
-    DecodePlan plan;
-    if (check_problem(p) != MTLATTN_OK) return plan;
-    if (p->total_q <= 0 || env_set("MTLATTN_NO_SPLITKV") || force_generic() || !splitkv_supported(p)) return plan;
-    const int64_t avg_kv = p->total_kv / (p->num_seqs > 0 ? p->num_seqs : 1);
-    // keys a sequence's rows can see (band length with a window)
-    const int64_t band = p->window > 0 ? (int64_t)p->window + p->max_seqlen_q - 1 : avg_kv;
-    const int64_t eff = avg_kv < band ? avg_kv : band;
-    if (eff < 2048) return plan;
+// Chunk length (keys, a multiple of 256 in [256, 8192]) for `work` keys of
+// work per (kv head, head group).
+int64_t plan_chunk(const mtlattn_problem* p, int64_t work) {
     const int g = p->num_heads_q / p->num_heads_kv;
     const int64_t groups = (int64_t)p->num_heads_kv * (g / decode_heads_per_group(g, p->max_seqlen_q));
-    const int64_t work = p->window > 0 ? eff * p->num_seqs : p->total_kv;
     const int64_t items = (int64_t)device_cus() * kItemsPerCu;
     int64_t c = (work * groups + items - 1) / items;
     if (const char* e = std::getenv("MTLATTN_DECODE_CHUNK")) {   // tuning override (keys)
@@ -206,14 +212,44 @@ DecodePlan decode_plan(const mtlattn_problem* p) {
     c = (c + 128) / 256 * 256;      // nearest multiple of 256 keys
     if (c < 256) c = 256;
     if (c > 8192) c = 8192;
+    return c;
+}
+
+// Keys a sequence of `kv` keys lets its rows see: the window band (W +
+// q_len - 1, plus up to 31 below it for the tile-aligned start) or all.
+int64_t band_keys(const mtlattn_problem* p, int64_t kv) {
+    if (p->window <= 0) return kv;
+    const int64_t band = (int64_t)p->window + p->max_seqlen_q - 1 + 31;
+    return kv < band ? kv : band;
+}
+
+DecodePlan decode_plan(const mtlattn_problem* p) {
+    DecodePlan plan;
+    if (check_problem(p) != MTLATTN_OK) return plan;
+    if (p->total_q <= 0 || env_set("MTLATTN_NO_SPLITKV") || force_generic() || !splitkv_supported(p)) return plan;
+    const int64_t avg_kv = p->total_kv / (p->num_seqs > 0 ? p->num_seqs : 1);
+    // keys a sequence's rows see on average (the window band at most)
+    const int64_t band = (int64_t)p->window + p->max_seqlen_q - 1;
+    const int64_t eff = p->window > 0 && avg_kv > band ? band : avg_kv;
+    if (eff < 2048) return plan;
     if (p->window <= 0) {
-        plan.chunk = (int)c;
+        plan.chunk = (int)plan_chunk(p, p->total_kv);
     } else {
-        // the band starts at a tile boundary at or below coff - W + 1: up to
-        // 31 more keys than W + q_len - 1
-        const int64_t span = band + 31;
-        plan.ns = (int)((span + c - 1) / c);
+        // the splits must cover the longest band: W + q_len - 1 keys plus up
+        // to 31 below its tile-aligned start
+        const int64_t c = plan_chunk(p, eff * p->num_seqs);
+        plan.ns = (int)((band + 31 + c - 1) / c);
     }
+    return plan;
+}
+
+// Paged decode: equal splits per sequence (the logical KV total is device
+// data), sized for num_seqs * max_seqlen_kv keys (of the window band).
+DecodePlan paged_plan(const mtlattn_problem* p, int64_t max_seqlen_kv) {
+    DecodePlan plan;
+    const int64_t span = band_keys(p, max_seqlen_kv > 0 ? max_seqlen_kv : 1);
+    const int64_t c = plan_chunk(p, span * p->num_seqs);
+    plan.ns = (int)((span + c - 1) / c);
     return plan;
 }
 
@@ -408,6 +444,42 @@ int mtlattn_attn_splitkv(const mtlattn_problem* p, const void* q, int64_t q_row_
         return fail(MTLATTN_ERR_UNSUPPORTED, "splitkv: q/k/v rows must be 16-byte aligned");
     return run_splitkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, num_splits, 0, workspace,
                        workspace_bytes, (hipStream_t)stream);
+}
+
+size_t mtlattn_paged_decode_workspace_size(const mtlattn_problem* p, int64_t max_seqlen_kv) {
+    if (check_problem(p) != MTLATTN_OK || !splitkv_supported(p)) return 0;
+    const DecodePlan plan = paged_plan(p, max_seqlen_kv);
+    return splitkv_bytes(p, plan.ns, plan.chunk);
+}
+
+int mtlattn_paged_decode(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k_cache,
+                         int64_t k_row_stride, const void* v_cache, int64_t v_row_stride, int32_t page_size,
+                         int64_t num_pages, const int32_t* block_table, int64_t block_table_stride,
+                         int64_t max_seqlen_kv, void* out, float* lse, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+    int rc = check_problem(p);
+    if (rc != MTLATTN_OK) return rc;
+    if (!is16(p->dtype)) return fail(MTLATTN_ERR_UNSUPPORTED, "paged_decode: half/bf16");
+    if (!decode_head_dim(p->head_dim)) return fail(MTLATTN_ERR_UNSUPPORTED, "paged_decode: D in {64,128}");
+    if (p->max_seqlen_q < 1 || p->max_seqlen_q > 16)
+        return fail(MTLATTN_ERR_UNSUPPORTED, "paged_decode: max_seqlen_q must be in [1, 16]");
+    if (page_size < 16 || page_size % 16 != 0)
+        return fail(MTLATTN_ERR_INVALID, "paged_decode: page_size must be a positive multiple of 16 (got %d)",
+                    page_size);
+    if (num_pages < 1 || num_pages > 0x7fffffffLL || num_pages * (int64_t)page_size > 0x7fffffffLL)
+        return fail(MTLATTN_ERR_INVALID, "paged_decode: num_pages * page_size must be in [1, 2^31)");
+    if (block_table_stride < 1) return fail(MTLATTN_ERR_INVALID, "paged_decode: block_table_stride must be >= 1");
+    if (max_seqlen_kv < 0) return fail(MTLATTN_ERR_INVALID, "paged_decode: negative max_seqlen_kv");
+    if (p->total_q == 0) return ok();
+    if (q == nullptr || out == nullptr || k_cache == nullptr || v_cache == nullptr || block_table == nullptr)
+        return fail(MTLATTN_ERR_INVALID, "paged_decode: null q/k_cache/v_cache/block_table/out pointer");
+    if (!aligned16(q, q_row_stride, p->dtype) || !aligned16(k_cache, k_row_stride, p->dtype) ||
+        !aligned16(v_cache, v_row_stride, p->dtype) || ((uintptr_t)out & 15u) != 0)
+        return fail(MTLATTN_ERR_UNSUPPORTED, "paged_decode: q/k/v rows must be 16-byte aligned");
+    const DecodePlan plan = paged_plan(p, max_seqlen_kv);
+    const PagedKV pk{block_table, block_table_stride, num_pages, page_size};
+    return run_splitkv(p, q, q_row_stride, k_cache, k_row_stride, v_cache, v_row_stride, out, lse, plan.ns,
+                       plan.chunk, workspace, workspace_bytes, (hipStream_t)stream, &pk);
 }
 
 

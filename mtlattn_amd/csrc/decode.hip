@@ -27,6 +27,12 @@
 //     down to a tile), and elements below a row's band are masked; the fp32
 //     bias of the lane's row and keys is loaded with the K/V tile it belongs
 //     to and added as bias * log2 e (columns at or past bias_cols read as 0).
+//   * Paged KV (no counterpart in the reference): K/V may live in pages of a
+//     cache, [num_pages, page_size, Hkv, D], logical key j of sequence s in
+//     page block_table[s][j / page_size]. page_size is a multiple of 16 and
+//     tiles start at multiples of 32, so each 16-key block lies in one page:
+//     two wave-uniform page lookups per tile (clamped to the cache) replace
+//     the contiguous row base.
 #include "common.h"
 #include "kernels.h"
 #include "../../include/mtlattn_capi.h"
@@ -55,6 +61,10 @@ struct DecKParams {
     float scale_log2;
     int causal, window;
     int bias_v4;      // bias rows 16-byte aligned (pointer and strides)
+    // paged KV (PAGED kernels): block table rows of bt_stride page indices
+    const int* block_table;
+    int64_t bt_stride;
+    int page_size, num_pages;
 };
 
 // KV range [ks, ke) of work item `slot` of sequence s (false: no keys).
@@ -91,7 +101,7 @@ __device__ inline uint32_t dec_tr_offset(int row, int group) {
     return (uint32_t)(row * 64 + ((group ^ f) << 3));
 }
 
-template <typename T, int D, bool BIAS>
+template <typename T, int D, bool BIAS, bool PAGED>
 __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams p) {
     constexpr int KC = D / 32;          // 32-wide k-chunks over D (QK^T)
     constexpr int DB = D / 16;          // 16-row output blocks over D
@@ -134,8 +144,15 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
 
     const int n_tiles = has_keys ? (ke - ks + kDecKT - 1) / kDecKT : 0;
 
-    const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * D;
-    const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * D;
+    // K/V rows: the sequence's contiguous rows, or cache rows through pages
+    const uint16_t* kbase = p.k + (PAGED ? 0 : (int64_t)kr.start * p.k_rs) + (int64_t)hk * D;
+    const uint16_t* vbase = p.v + (PAGED ? 0 : (int64_t)kr.start * p.v_rs) + (int64_t)hk * D;
+    const int* bt = PAGED ? p.block_table + (int64_t)s * p.bt_stride : nullptr;
+    // cache row of logical key `key` (wave-uniform), page index clamped
+    auto page_row = [&](int key) -> int64_t {
+        const int pg = min(max(bt[key / p.page_size], 0), p.num_pages - 1);
+        return (int64_t)pg * p.page_size + key % p.page_size;
+    };
 
     // this lane's bias row (head of the row, or the broadcast head)
     const float* brow = nullptr;
@@ -146,6 +163,17 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
     u32x4_t ka[2][KC], vr[VU][4];
     float bb[2][4];
     auto load = [&](int kt, u32x4_t (&ka_)[2][KC], u32x4_t (&vr_)[VU][4], float (&bb_)[2][4]) {
+        // row of a (clamped, < ke) key of this tile: keys [kt, kt + 16) lie
+        // in the page of kt, keys [kt + 16, ke) in the page of kt + 16
+        int64_t r0 = 0, r1 = 0;
+        if (PAGED) {
+            r0 = page_row(kt);
+            r1 = page_row(min(kt + 16, ke - 1));
+        }
+        auto row = [&](int key) -> int64_t {
+            if (!PAGED) return key;
+            return key < kt + 16 ? r0 + (key - kt) : r1 + (key - (kt + 16));
+        };
         if (BIAS) {
             // the lane's 4 keys of a 16-key block are contiguous: one 16-byte
             // load each when the whole tile lies within the bias columns
@@ -171,7 +199,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
         for (int mb = 0; mb < 2; ++mb) {
             // keys past the split end read its last key: finite, masked to P = 0
             const int key = min(kt + 16 * mb + n16, ke - 1);
-            const uint16_t* kp = kbase + (int64_t)key * p.k_rs + 8 * lg;
+            const uint16_t* kp = kbase + row(key) * p.k_rs + 8 * lg;
 #pragma unroll
             for (int kc = 0; kc < KC; ++kc) ka_[mb][kc] = ld16(kp + 32 * kc);
         }
@@ -182,7 +210,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int key = min(kt + 4 * kg + i, ke - 1);
-                vr_[u][i] = ld16(vbase + (int64_t)key * p.v_rs + 8 * dc);
+                vr_[u][i] = ld16(vbase + row(key) * p.v_rs + 8 * dc);
             }
         }
     };
@@ -395,16 +423,24 @@ hipError_t launch_typed(const DecodeArgs& a, hipStream_t st) {
     p.causal = g.causal;
     p.window = g.window;
     p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0;
+    p.block_table = a.block_table;
+    p.bt_stride = a.bt_stride;
+    p.page_size = a.page_size;
+    p.num_pages = a.num_pages;
+    const bool paged = a.block_table != nullptr;
+    if (paged && (a.page_size < 16 || a.page_size % 16 != 0 || a.num_pages < 1)) return hipErrorInvalidValue;
     const int64_t waves = (int64_t)g.hkv * p.n_hg * p.n_slots;
     const int64_t blocks = (waves + kDecWaves - 1) / kDecWaves;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (blocks > 0) {
-        if (p.bias != nullptr)
-            hipLaunchKernelGGL((decode_split_kernel<T, D, true>), dim3((unsigned)blocks), dim3(kDecWaves * 64), 0, st,
-                               p);
-        else
-            hipLaunchKernelGGL((decode_split_kernel<T, D, false>), dim3((unsigned)blocks), dim3(kDecWaves * 64), 0,
-                               st, p);
+        const dim3 grid((unsigned)blocks), block(kDecWaves * 64);
+        if (p.bias != nullptr) {
+            if (paged) hipLaunchKernelGGL((decode_split_kernel<T, D, true, true>), grid, block, 0, st, p);
+            else hipLaunchKernelGGL((decode_split_kernel<T, D, true, false>), grid, block, 0, st, p);
+        } else {
+            if (paged) hipLaunchKernelGGL((decode_split_kernel<T, D, false, true>), grid, block, 0, st, p);
+            else hipLaunchKernelGGL((decode_split_kernel<T, D, false, false>), grid, block, 0, st, p);
+        }
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

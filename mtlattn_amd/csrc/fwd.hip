@@ -206,6 +206,10 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         const char* kb_ = opaque(Ks + rbase);
         const char* vtb = opaque(Ks + KTILE + tbase);
         f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
+        // raised priority while issuing the S products: when the other wave
+        // of the SIMD is in its softmax, the matrix core gets the issue slot
+        // (measured +1%)
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kc = 0; kc < DC; ++kc) {
 #pragma unroll
@@ -218,6 +222,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         // keep the V^T reads of the P.V phase from being hoisted above the
         // softmax (they would pin 64 registers across it)
         __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
         const bool need_mask = skip | (kt + kKT > kv_len) | ((p.causal != 0) & (kt + kKT - 1 > qa + coff)) |
                                ((p.window > 0) & (kt < wq_last + coff - p.window + 1));
         if (need_mask) {

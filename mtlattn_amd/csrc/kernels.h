@@ -55,6 +55,13 @@ struct DecodeArgs {
     int num_splits;               // equal splits per sequence (used when chunk == 0)
     int chunk;                    // > 0: fixed KV chunk length (multiple of 32)
     int max_q;                    // bound on q lengths; heads_per_group * max_q <= 16
+    // paged KV: k / v are caches [num_pages, page_size, hkv, d] (row strides
+    // k_rs / v_rs per token), logical key j of sequence s in page
+    // block_table[s * bt_stride + j / page_size]; block_table == nullptr:
+    // contiguous K/V by cu_seqlens_kv
+    const int* block_table = nullptr;
+    int64_t bt_stride = 0;
+    int page_size = 0, num_pages = 0;
 };
 
 // Launchers return hipSuccess or the launch error. `dtype` is MTLATTN_DTYPE_*.

@@ -192,6 +192,79 @@ at::Tensor attn_splitkv(const at::Tensor& q, const at::Tensor& k, const at::Tens
     return out;
 }
 
+// _C.paged_decode: decode over a paged KV cache (no reference counterpart).
+// k_cache / v_cache [num_pages, page_size, Hkv, D] (token rows may be
+// strided; pages are page_size consecutive token rows), block_table int32
+// [B, max_pages], cu_seqlens_kv the logical KV lengths.
+at::Tensor paged_decode(const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
+                        const at::Tensor& cu_seqlens_q, const at::Tensor& cu_seqlens_kv, const at::Tensor& block_table,
+                        int64_t max_seqlen_q, int64_t max_seqlen_kv, double scale, bool causal, int64_t window,
+                        c10::optional<at::Tensor> lse_out, c10::optional<at::Tensor> attn_bias) {
+    TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda(), "mtlattn: q/k_cache/v_cache must be GPU tensors");
+    TORCH_CHECK(q.dim() == 3, "mtlattn: q must be [M, H, D]");
+    TORCH_CHECK(k_cache.dim() == 4 && v_cache.dim() == 4 && k_cache.sizes() == v_cache.sizes(),
+                "mtlattn: k_cache/v_cache must both be [num_pages, page_size, Hkv, D]");
+    const int64_t D = q.size(2), Hkv = k_cache.size(2), page_size = k_cache.size(1);
+    TORCH_CHECK(k_cache.size(3) == D, "mtlattn: k_cache head dim must match q");
+    TORCH_CHECK(Hkv > 0 && q.size(1) % Hkv == 0, "mtlattn: query heads must be a multiple of kv heads");
+    TORCH_CHECK(q.scalar_type() == k_cache.scalar_type() && q.scalar_type() == v_cache.scalar_type(),
+                "mtlattn: dtype mismatch");
+    dtype_code(q.scalar_type());
+    TORCH_CHECK((q.size(2) == 1 || q.stride(2) == 1) && (q.size(1) == 1 || q.stride(1) == D),
+                "mtlattn: q inner dims must be contiguous");
+    for (const auto& c : {k_cache, v_cache}) {
+        TORCH_CHECK(c.stride(3) == 1 && (Hkv == 1 || c.stride(2) == D),
+                    "mtlattn: cache inner dims [Hkv, D] must be contiguous");
+        TORCH_CHECK(c.size(0) <= 1 || c.stride(0) == page_size * c.stride(1),
+                    "mtlattn: cache pages must be page_size consecutive token rows");
+        TORCH_CHECK(c.get_device() == q.get_device(), "mtlattn: q and the caches must be on the same device");
+    }
+    check_cu(cu_seqlens_q, cu_seqlens_kv, q);
+    TORCH_CHECK(block_table.is_cuda() && block_table.get_device() == q.get_device() &&
+                    block_table.scalar_type() == at::kInt && block_table.dim() == 2 &&
+                    block_table.size(0) == cu_seqlens_q.numel() - 1,
+                "mtlattn: block_table must be an int32 [B, max_pages] GPU tensor");
+    const c10::OptionalDeviceGuard guard(q.device());
+    auto cu_q = cu_seqlens_q.contiguous(), cu_kv = cu_seqlens_kv.contiguous();
+    auto bt = block_table.stride(1) == 1 ? block_table : block_table.contiguous();
+    auto out = at::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+    float* lse = nullptr;
+    if (defined(lse_out)) {
+        const at::Tensor& l = *lse_out;
+        TORCH_CHECK(l.is_cuda() && l.scalar_type() == at::kFloat && l.is_contiguous() && l.dim() == 2 &&
+                        l.size(0) == q.size(0) && l.size(1) == q.size(1),
+                    "mtlattn: lse_out must be a contiguous fp32 [total_q, H] GPU tensor");
+        lse = l.data_ptr<float>();
+    }
+    if (q.size(0) == 0) return out;
+    mtlattn_problem p;
+    std::memset(&p, 0, sizeof(p));
+    p.dtype = dtype_code(q.scalar_type());
+    p.num_seqs = (int32_t)(cu_q.numel() - 1);
+    p.total_q = q.size(0);
+    // an upper bound on the logical KV total (cu_seqlens_kv[B])
+    p.total_kv = std::min<int64_t>((int64_t)p.num_seqs * std::max<int64_t>(max_seqlen_kv, 0), 0x7fffffff);
+    p.num_heads_q = (int32_t)q.size(1);
+    p.num_heads_kv = (int32_t)Hkv;
+    p.head_dim = (int32_t)D;
+    p.max_seqlen_q = (int32_t)std::min<int64_t>(max_seqlen_q, 0x7fffffff);
+    p.scale = (float)scale;
+    p.causal = causal ? 1 : 0;
+    p.window = window > 0 ? (int32_t)std::min<int64_t>(window, 0x7fffffff) : 0;
+    p.cu_seqlens_q = cu_q.data_ptr<int32_t>();
+    p.cu_seqlens_kv = cu_kv.data_ptr<int32_t>();
+    at::Tensor bias_keep;
+    fill_bias(p, attn_bias, q, bias_keep);
+    const size_t ws_bytes = mtlattn_paged_decode_workspace_size(&p, max_seqlen_kv);
+    at::Tensor ws = workspace((int64_t)ws_bytes, q);
+    const int64_t krs = k_cache.size(1) > 1 ? k_cache.stride(1) : Hkv * D;
+    const int64_t vrs = v_cache.size(1) > 1 ? v_cache.stride(1) : Hkv * D;
+    check_rc(mtlattn_paged_decode(&p, q.data_ptr(), row_stride(q), k_cache.data_ptr(), krs, v_cache.data_ptr(), vrs,
+                                  (int32_t)page_size, k_cache.size(0), bt.data_ptr<int32_t>(), bt.stride(0),
+                                  max_seqlen_kv, out.data_ptr(), lse, ws.data_ptr(), ws_bytes, current_stream(q)));
+    return out;
+}
+
 // _C.mpp_bwd_dq (src/ext.mm:656-711): fp32 dQ.
 at::Tensor mpp_bwd_dq(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& dO,
                       const at::Tensor& lse, const at::Tensor& delta, const at::Tensor& cu_q_in,
@@ -304,6 +377,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("attn_splitkv", &attn_splitkv, "split-KV decode with an explicit split count (test entry)", py::arg("q"),
           py::arg("k"), py::arg("v"), py::arg("cu_q"), py::arg("cu_kv"), py::arg("max_seqlen_q"), py::arg("scale"),
           py::arg("causal"), py::arg("num_splits"), py::arg("window") = 0, py::arg("attn_bias") = c10::nullopt);
+    m.def("paged_decode", &paged_decode, "decode (max_seqlen_q <= 16) over a paged KV cache", py::arg("q"),
+          py::arg("k_cache"), py::arg("v_cache"), py::arg("cu_seqlens_q"), py::arg("cu_seqlens_kv"),
+          py::arg("block_table"), py::arg("max_seqlen_q"), py::arg("max_seqlen_kv"), py::arg("scale"),
+          py::arg("causal") = false, py::arg("window") = 0, py::arg("lse_out") = c10::nullopt,
+          py::arg("attn_bias") = c10::nullopt);
     m.def("mpp_bwd_dkv", &mpp_bwd_dkv, "dK/dV backward kernel, fp32 outputs (test entry)", py::arg("q"), py::arg("k"),
           py::arg("v"), py::arg("dO"), py::arg("lse"), py::arg("delta"), py::arg("cu_q"), py::arg("cu_kv"),
           py::arg("max_seqlen_kv"), py::arg("scale"), py::arg("causal") = false, py::arg("window") = 0,

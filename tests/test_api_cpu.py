@@ -15,6 +15,8 @@ def test_import_name_is_the_same_module():
     assert mtlattn._C is M._C
     assert set(mtlattn.__all__) == {"varlen_attention", "flash_attn_varlen_qkvpacked_func",
                                     "flash_attn_varlen_kvpacked_func", "sdpa", "replace_sdpa", "restore_sdpa"}
+    # paged-KV decode has no reference counterpart: reachable, not in __all__
+    assert mtlattn.paged_decode is M.paged_decode and hasattr(M._C, "paged_decode")
 
 
 def test_binding_exports_reference_names():

@@ -44,6 +44,11 @@ def lib():
     L.mtlattn_attn_splitkv_workspace_size.argtypes = [ctypes.POINTER(Problem), ctypes.c_int32]
     L.mtlattn_decode_num_splits.restype = ctypes.c_int32
     L.mtlattn_decode_num_splits.argtypes = [ctypes.POINTER(Problem)]
+    i64, vp = ctypes.c_int64, ctypes.c_void_p
+    L.mtlattn_paged_decode_workspace_size.restype = ctypes.c_size_t
+    L.mtlattn_paged_decode_workspace_size.argtypes = [ctypes.POINTER(Problem), i64]
+    L.mtlattn_paged_decode.argtypes = [ctypes.POINTER(Problem), vp, i64, vp, i64, vp, i64, ctypes.c_int32, i64, vp,
+                                       i64, i64, vp, vp, vp, ctypes.c_size_t, vp]
     return L
 
 
@@ -192,6 +197,31 @@ def test_splitkv_entry_validation(lib):
     p = problem(max_seqlen_q=1)
     rc = lib.mtlattn_attn_splitkv(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, None, 0, None, 0, None)
     assert rc == ERR_INVALID
+
+
+def test_paged_decode_validation(lib):
+    """Paged decode (no reference counterpart): argument checks before any
+    launch, and the workspace is the equal-split plan's size."""
+    args = lambda p, ps=16, pages=8, bt=FAKE, bts=4: (ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, ps, pages, bt, bts,
+                                                      4096, FAKE, None, None, 0, None)   # noqa: E731
+    p = problem(max_seqlen_q=1)
+    assert lib.mtlattn_paged_decode(*args(p, ps=24)) == ERR_INVALID
+    assert b"multiple of 16" in lib.mtlattn_last_error()
+    assert lib.mtlattn_paged_decode(*args(p, ps=0)) == ERR_INVALID
+    assert lib.mtlattn_paged_decode(*args(p, pages=0)) == ERR_INVALID
+    assert lib.mtlattn_paged_decode(*args(p, bts=0)) == ERR_INVALID
+    assert lib.mtlattn_paged_decode(*args(p, bt=None)) == ERR_INVALID
+    assert lib.mtlattn_paged_decode(*args(problem(max_seqlen_q=17))) == ERR_UNSUPPORTED
+    assert lib.mtlattn_paged_decode(*args(problem(max_seqlen_q=1, head_dim=96))) == ERR_UNSUPPORTED
+    assert lib.mtlattn_paged_decode(*args(problem(max_seqlen_q=1, dtype=F32))) == ERR_UNSUPPORTED
+    # valid arguments: the empty workspace is what fails
+    assert lib.mtlattn_paged_decode(*args(p)) == ERR_WORKSPACE
+    # 2 sequences, 4096 keys at most, 2 kv heads x 1 head group (4 heads x
+    # q_len 1 in a 16-row group): split length sized for 2 * 4096 keys
+    c = -(-(2 * 4096 * 2) // (256 * 18))
+    c = max(256, (c + 128) // 256 * 256)
+    ns = -(-4096 // c)
+    assert lib.mtlattn_paged_decode_workspace_size(ctypes.byref(p), 4096) == _splitkv_bytes(2 * 2 * ns * 16, 128)
 
 
 def test_dq_dtype_checked(lib):

@@ -565,6 +565,73 @@ def test_split_kv_window_bias(mt):
             assert err < 3e-2
 
 
+def _paged(k, v, kv_lens, page_size, seed):
+    """Scatter contiguous K/V rows into randomly permuted pages of a cache
+    [num_pages, page_size, Hkv, D] (two spare pages); block_table rows past a
+    sequence's pages hold -1."""
+    g = torch.Generator().manual_seed(seed)
+    n_pages = [-(-L // page_size) for L in kv_lens]
+    total = sum(n_pages) + 2
+    perm = torch.randperm(total, generator=g)
+    kc = torch.randn((total, page_size) + tuple(k.shape[1:]), generator=g).to(k.dtype)
+    vc = torch.randn((total, page_size) + tuple(v.shape[1:]), generator=g).to(v.dtype)
+    bt = torch.full((len(kv_lens), max(max(n_pages), 1)), -1, dtype=torch.int32)
+    off, used = 0, 0
+    for s, L in enumerate(kv_lens):
+        for j in range(n_pages[s]):
+            pg = int(perm[used])
+            used += 1
+            bt[s, j] = pg
+            n = min(page_size, L - j * page_size)
+            kc[pg, :n] = k[off + j * page_size: off + j * page_size + n]
+            vc[pg, :n] = v[off + j * page_size: off + j * page_size + n]
+        off += L
+    return kc, vc, bt
+
+
+def test_paged_decode(mt, monkeypatch):
+    """Decode over a paged KV cache (no reference counterpart): pages of 16,
+    48, 64 and 256 tokens in permuted order, against the oracle on the
+    contiguous K/V (O and LSE), with causal, window and bias; and, with the
+    split length fixed, bitwise equal to the contiguous split-KV path with
+    the same split count."""
+    cases = [
+        ("ps16 ragged GQA", [1, 1, 2], [3000, 700, 5001], 8, 2, 128, torch.bfloat16, 16, True, 0, False),
+        ("ps48 D64 non-causal", [1, 3], [2500, 4100], 8, 8, 64, torch.float16, 48, False, 0, False),
+        ("ps64 window", [1, 1], [6000, 2000], 16, 2, 128, torch.bfloat16, 64, True, 1500, False),
+        ("ps256 bias", [2, 1], [4500, 3333], 8, 2, 128, torch.float16, 256, True, 0, True),
+        ("ps16 empty sequence", [1, 1], [0, 1234], 8, 8, 128, torch.bfloat16, 16, True, 0, False),
+    ]
+    for name, ql, kl, hq, hkv, d, dt, ps, causal, w, with_bias in cases:
+        _banner(f"paged decode {name}")
+        q, k, v = _inputs(ql, kl, hq, hkv, d, dt, seed=len(name))
+        kc, vc, bt = _paged(k, v, kl, ps, seed=len(name))
+        bias = _make_bias(sum(ql), hq, max(kl), False, seed=3) if with_bias else None
+        cq, ck = cu_of(ql), cu_of(kl)
+        lse = torch.empty(sum(ql), hq, dtype=torch.float32, device="cuda")
+        out = mt.paged_decode(q.cuda(), kc.cuda(), vc.cuda(), cq.cuda(), ck.cuda(), bt.cuda(), max(ql), max(kl),
+                              causal=causal, window=w, attn_bias=None if bias is None else bias.cuda(),
+                              lse_out=lse).cpu()
+        ref, ref_lse = oracle.varlen_forward(q, k, v, cq, ck, 1 / math.sqrt(d), causal, w, bias)
+        err = (out.float() - ref).abs().max().item()
+        fin = torch.isfinite(ref_lse)
+        assert torch.equal(torch.isfinite(lse.cpu()), fin), f"{name}: LSE -inf pattern"
+        lerr = (lse.cpu()[fin] - ref_lse[fin]).abs().max().item()
+        print(f"  max_err={err:.3e} lse_err={lerr:.3e}", flush=True)
+        assert err < REF_ATOL[dt] and lerr < LSE_TOL[dt], name
+    # fixed 256-key split length: the paged plan is ceil(max_kv / 256) equal
+    # splits per sequence, the same arithmetic as the contiguous entry
+    monkeypatch.setenv("MTLATTN_DECODE_CHUNK", "256")
+    ql, kl = [1, 1, 1], [3000, 1111, 4444]
+    q, k, v = _inputs(ql, kl, 8, 2, 128, torch.bfloat16, seed=21)
+    kc, vc, bt = _paged(k, v, kl, 32, seed=21)
+    cq, ck = cu_of(ql, "cuda"), cu_of(kl, "cuda")
+    out = mt.paged_decode(q.cuda(), kc.cuda(), vc.cuda(), cq, ck, bt.cuda(), 1, max(kl), causal=True).cpu()
+    ref = mt._C.attn_splitkv(q.cuda(), k.cuda(), v.cuda(), cq, ck, 1, 1 / math.sqrt(128), True,
+                             -(-max(kl) // 256)).cpu()
+    assert torch.equal(out, ref), "paged != contiguous split-KV with the same splits"
+
+
 def test_ragged_equals_per_sequence(mt):
     """A ragged batch equals per-sequence calls, bitwise (varlen bookkeeping)."""
     _banner("ragged == per-sequence (bitwise)")
