@@ -197,7 +197,11 @@ int mtlattn_attn_splitkv(const mtlattn_problem* p,
  *   p->cu_seqlens_kv  : logical KV lengths (prefix sums); p->total_kv is an
  *                       upper bound on cu_seqlens_kv[num_seqs]
  *   page_size         : a multiple of 16
- *   max_seqlen_kv     : bound on the logical KV lengths (sizes the splits)
+ *   max_seqlen_kv     : bound on the logical KV lengths (sizes the window
+ *                       splits)
+ * Work split: fixed KV chunks numbered by the logical prefix sums (slots for
+ * p->total_kv keys) as on the contiguous decode path; with a window, equal
+ * splits of each sequence's band.
  * Workspace: mtlattn_paged_decode_workspace_size(p, max_seqlen_kv) bytes.
  */
 size_t mtlattn_paged_decode_workspace_size(const mtlattn_problem* p, int64_t max_seqlen_kv);

@@ -243,10 +243,16 @@ DecodePlan decode_plan(const mtlattn_problem* p) {
     return plan;
 }
 
-// Paged decode: equal splits per sequence (the logical KV total is device
-// data), sized for num_seqs * max_seqlen_kv keys (of the window band).
+// Paged decode: the logical KV total is device data, p->total_kv bounds it.
+// Without a window, fixed chunks as on the contiguous path (slots for the
+// bound; chunks past a sequence's end exit at once); with one, equal splits
+// of the band sized for num_seqs bands of work.
 DecodePlan paged_plan(const mtlattn_problem* p, int64_t max_seqlen_kv) {
     DecodePlan plan;
+    if (p->window <= 0) {
+        plan.chunk = (int)plan_chunk(p, p->total_kv > 0 ? p->total_kv : 1);
+        return plan;
+    }
     const int64_t span = band_keys(p, max_seqlen_kv > 0 ? max_seqlen_kv : 1);
     const int64_t c = plan_chunk(p, span * p->num_seqs);
     plan.ns = (int)((span + c - 1) / c);

@@ -242,8 +242,10 @@ at::Tensor paged_decode(const at::Tensor& q, const at::Tensor& k_cache, const at
     p.dtype = dtype_code(q.scalar_type());
     p.num_seqs = (int32_t)(cu_q.numel() - 1);
     p.total_q = q.size(0);
-    // an upper bound on the logical KV total (cu_seqlens_kv[B])
-    p.total_kv = std::min<int64_t>((int64_t)p.num_seqs * std::max<int64_t>(max_seqlen_kv, 0), 0x7fffffff);
+    // an upper bound on the logical KV total (cu_seqlens_kv[B]): the cache's
+    // capacity or B * max_seqlen_kv, whichever is smaller
+    p.total_kv = std::min<int64_t>({(int64_t)p.num_seqs * std::max<int64_t>(max_seqlen_kv, 0),
+                                    k_cache.size(0) * page_size, 0x7fffffff});
     p.num_heads_q = (int32_t)q.size(1);
     p.num_heads_kv = (int32_t)Hkv;
     p.head_dim = (int32_t)D;

@@ -216,12 +216,15 @@ def test_paged_decode_validation(lib):
     assert lib.mtlattn_paged_decode(*args(problem(max_seqlen_q=1, dtype=F32))) == ERR_UNSUPPORTED
     # valid arguments: the empty workspace is what fails
     assert lib.mtlattn_paged_decode(*args(p)) == ERR_WORKSPACE
-    # 2 sequences, 4096 keys at most, 2 kv heads x 1 head group (4 heads x
-    # q_len 1 in a 16-row group): split length sized for 2 * 4096 keys
-    c = -(-(2 * 4096 * 2) // (256 * 18))
+    # fixed chunks for p.total_kv = 64 keys (bound on the logical total): a
+    # 256-key chunk, slots 64 // 256 + 2 + 1 per (kv head x 1 head group)
+    assert lib.mtlattn_paged_decode_workspace_size(ctypes.byref(p), 4096) == _splitkv_bytes(2 * 3 * 16, 128)
+    # with a window: equal splits of the band (W + q_len - 1 + 31 keys)
+    pw = problem(max_seqlen_q=1, window=1000)
+    c = -(-(2 * 1031 * 2) // (256 * 18))
     c = max(256, (c + 128) // 256 * 256)
-    ns = -(-4096 // c)
-    assert lib.mtlattn_paged_decode_workspace_size(ctypes.byref(p), 4096) == _splitkv_bytes(2 * 2 * ns * 16, 128)
+    ns = -(-1031 // c)
+    assert lib.mtlattn_paged_decode_workspace_size(ctypes.byref(pw), 4096) == _splitkv_bytes(2 * 2 * ns * 16, 128)
 
 
 def test_dq_dtype_checked(lib):

@@ -619,17 +619,17 @@ def test_paged_decode(mt, monkeypatch):
         lerr = (lse.cpu()[fin] - ref_lse[fin]).abs().max().item()
         print(f"  max_err={err:.3e} lse_err={lerr:.3e}", flush=True)
         assert err < REF_ATOL[dt] and lerr < LSE_TOL[dt], name
-    # fixed 256-key split length: the paged plan is ceil(max_kv / 256) equal
-    # splits per sequence, the same arithmetic as the contiguous entry
+    # fixed 256-key chunks on both paths: the same work items, the same
+    # arithmetic as the contiguous automatic decode path
     monkeypatch.setenv("MTLATTN_DECODE_CHUNK", "256")
     ql, kl = [1, 1, 1], [3000, 1111, 4444]
     q, k, v = _inputs(ql, kl, 8, 2, 128, torch.bfloat16, seed=21)
     kc, vc, bt = _paged(k, v, kl, 32, seed=21)
     cq, ck = cu_of(ql, "cuda"), cu_of(kl, "cuda")
+    assert _decode_routed(ql, kl, 8, 2, 128) > 0
     out = mt.paged_decode(q.cuda(), kc.cuda(), vc.cuda(), cq, ck, bt.cuda(), 1, max(kl), causal=True).cpu()
-    ref = mt._C.attn_splitkv(q.cuda(), k.cuda(), v.cuda(), cq, ck, 1, 1 / math.sqrt(128), True,
-                             -(-max(kl) // 256)).cpu()
-    assert torch.equal(out, ref), "paged != contiguous split-KV with the same splits"
+    ref = mt.varlen_attention(q.cuda(), k.cuda(), v.cuda(), cq, ck, 1, causal=True).cpu()
+    assert torch.equal(out, ref), "paged != contiguous split-KV with the same chunks"
 
 
 def test_ragged_equals_per_sequence(mt):
