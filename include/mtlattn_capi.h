@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MTLATTN_ABI_VERSION 1
+#define MTLATTN_ABI_VERSION 2
 
 /* element types of q/k/v/out/dout/dq/dk/dv */
 enum {
@@ -74,6 +74,14 @@ typedef struct mtlattn_problem {
     int64_t bias_q_stride;    /* elements between query rows of bias */
     int64_t bias_h_stride;    /* elements between heads; 0 = broadcast over heads */
     int64_t bias_kv_cols;     /* size of bias's key dim; keys beyond read as 0 */
+    /* Row addressing of bias (no counterpart in the reference, which indexes
+     * by global query row): 0 = row of global query r at r * bias_q_stride;
+     * 1 = row of query i of sequence s at s * bias_seq_stride +
+     * min(i, bias_seq_rows - 1) * bias_q_stride (a dense [B or 1, H or 1,
+     * Nq, Nkv] mask used in place, stride 0 for a broadcast batch dim). */
+    int32_t bias_seq_local;
+    int64_t bias_seq_stride;
+    int64_t bias_seq_rows;
 } mtlattn_problem;
 
 /* Version of this header the library was built from (== MTLATTN_ABI_VERSION). */

@@ -71,9 +71,11 @@ class _VarlenAttnFn(torch.autograd.Function):
 
 def _prep_bias(attn_bias):
     """Bring an additive mask to the kernel contract (reference:
-    mtlattn/__init__.py:49-63): fp32, 3-D, unit stride on the key dim. A mask
-    that requires grad is rejected -- it would be applied but never receive a
-    gradient."""
+    mtlattn/__init__.py:49-63): fp32, 3-D, unit stride on the key dim. A 4-D
+    mask [B or 1, H or 1, Nq, max_kv], indexed by sequence and
+    sequence-local row (no counterpart in the reference), is passed as it is
+    when its key dim has unit stride. A mask that requires grad is rejected
+    -- it would be applied but never receive a gradient."""
     if attn_bias is None:
         return None
     if attn_bias.requires_grad:
@@ -81,7 +83,7 @@ def _prep_bias(attn_bias):
             "mtlattn: a differentiable attn_bias (requires_grad=True) is not supported; "
             "detach it or treat the mask as constant")
     b = attn_bias if attn_bias.dtype == torch.float32 else attn_bias.float()
-    if b.dim() != 3 or b.stride(-1) != 1:
+    if b.dim() not in (3, 4) or b.stride(-1) != 1:
         b = b.contiguous()
     return b
 
@@ -167,9 +169,12 @@ _SDPA_MIN_SEQLEN = 1024
 
 
 def _sdpa_mask_to_bias(attn_mask, B, Hq, Nq, Nkv):
-    """Dense SDPA mask -> varlen additive bias [B*Nq, h, Nkv] fp32, h in {1, Hq}
-    (reference: mtlattn/__init__.py:132-159). Bool masks keep True (0) and drop
-    False (-inf); float masks are already additive. Shapes: [Nq, Nkv] or
+    """Dense SDPA mask -> additive fp32 bias [b, h, Nq, Nkv], b in {1, B}, h in
+    {1, Hq}, which the kernels index by (sequence, sequence-local row) in
+    place (reference: mtlattn/__init__.py:132-159, which copies it to
+    [B*Nq, h, Nkv]). Bool masks keep True (0) and drop False (-inf); float
+    masks are already additive and are not copied when fp32 with a unit-stride
+    key dim (broadcast dims stay stride 0). Shapes: [Nq, Nkv] or
     [b in {1, B}, h in {1, Hq}, Nq, Nkv]. Anything else raises
     NotImplementedError."""
     m = attn_mask
@@ -185,13 +190,13 @@ def _sdpa_mask_to_bias(attn_mask, B, Hq, Nq, Nkv):
     else:
         m = m.float()
     b, h = m.shape[0], m.shape[1]
-    if b != B:
-        if b != 1:
-            raise NotImplementedError("mtlattn: attn_mask batch dim must be 1 or B")
-        m = m.expand(B, h, Nq, Nkv)
+    if b not in (1, B):
+        raise NotImplementedError("mtlattn: attn_mask batch dim must be 1 or B")
     if h not in (1, Hq):
         raise NotImplementedError("mtlattn: attn_mask head dim must be 1 or num_heads")
-    return m.transpose(1, 2).contiguous().reshape(B * Nq, h, Nkv)
+    if m.stride(-1) != 1 and Nkv > 1:
+        m = m.contiguous()
+    return m
 
 
 def sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, scale=None):

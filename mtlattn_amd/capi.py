@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(_HERE, "libmtlattn_hip.so")
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH = 0, -1, -2, -3, -4
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class Problem(ctypes.Structure):
@@ -31,6 +31,8 @@ class Problem(ctypes.Structure):
         ("cu_seqlens_q", ctypes.c_void_p), ("cu_seqlens_kv", ctypes.c_void_p),
         ("bias", ctypes.c_void_p), ("bias_q_stride", ctypes.c_int64),
         ("bias_h_stride", ctypes.c_int64), ("bias_kv_cols", ctypes.c_int64),
+        ("bias_seq_local", ctypes.c_int32), ("bias_seq_stride", ctypes.c_int64),
+        ("bias_seq_rows", ctypes.c_int64),
     ]
 
 

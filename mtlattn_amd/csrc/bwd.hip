@@ -41,7 +41,7 @@ struct BwdKParams {
     const int* cu_q; const int* cu_kv;
     const float* bias;
     int64_t q_rs, k_rs, v_rs, do_rs;
-    int64_t bias_qs, bias_hs, bias_cols;
+    int64_t bias_qs, bias_hs, bias_cols, bias_ss, bias_rows;
     int64_t total_q, total_kv;
     int num_seqs, hq, hkv, g, hpw, n_tiles, n_hg;
     float scale, scale_log2;
@@ -129,7 +129,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     // bias row of this lane's query (rows past the end read the last row);
     // columns at or past bias_cols read as 0
     const float* brow = nullptr;
-    if (BIAS) brow = p.bias + grow * p.bias_qs + (int64_t)head * p.bias_hs;
+    if (BIAS)
+        brow = p.bias + bias_row_offset(grow, s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows) +
+               (int64_t)head * p.bias_hs;
     // settle these loads here: the key loop's own wait counts cover only the
     // staging loads
     wait_vmcnt<0>();
@@ -435,7 +437,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int qrow = min(qt + 32 * qb + 8 * (r >> 2) + 4 * hi + (r & 3), q_len - 1);
-                        bvals[qb][r] = bcol[(int64_t)(qr.start + qrow) * p.bias_qs];
+                        bvals[qb][r] =
+                            bcol[bias_row_offset(qr.start + qrow, s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows)];
                     }
             }
             f32x16_t sacc[NQB];
@@ -658,13 +661,15 @@ BwdKParams make_params(const BwdArgs& a) {
     p.cu_q = g.cu_q; p.cu_kv = g.cu_kv; p.bias = g.bias;
     p.q_rs = a.q_rs; p.k_rs = a.k_rs; p.v_rs = a.v_rs; p.do_rs = a.do_rs;
     p.bias_qs = g.bias_qs; p.bias_hs = g.bias_hs; p.bias_cols = g.bias_cols;
+    p.bias_ss = g.bias_ss; p.bias_rows = g.bias_rows;
     p.total_q = g.total_q; p.total_kv = g.total_kv;
     p.num_seqs = g.num_seqs; p.hq = g.hq; p.hkv = g.hkv; p.g = g.g;
     p.hpw = 1;
     p.n_tiles = 0; p.n_hg = 0;
     p.scale = g.scale; p.scale_log2 = g.scale * kLog2e;
     p.causal = g.causal; p.window = g.window > 0 ? g.window : 0;
-    p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0;
+    p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0 &&
+                (g.bias_ss < 0 || g.bias_ss % 4 == 0);
     return p;
 }
 

@@ -80,7 +80,8 @@ int check_problem(const mtlattn_problem* p) {
     if (p->cu_seqlens_q == nullptr || p->cu_seqlens_kv == nullptr)
         return fail(MTLATTN_ERR_INVALID, "mtlattn: cu_seqlens must be device int32 pointers");
     if (p->bias != nullptr) {
-        if (p->bias_q_stride < 0 || p->bias_h_stride < 0 || p->bias_kv_cols < 0)
+        if (p->bias_q_stride < 0 || p->bias_h_stride < 0 || p->bias_kv_cols < 0 ||
+            (p->bias_seq_local != 0 && (p->bias_seq_stride < 0 || p->bias_seq_rows < 1)))
             return fail(MTLATTN_ERR_INVALID, "mtlattn: attn_mask strides must be non-negative");
     }
     return MTLATTN_OK;
@@ -105,6 +106,8 @@ Geometry make_geo(const mtlattn_problem* p) {
     g.bias_qs = p->bias_q_stride;
     g.bias_hs = p->bias_h_stride;
     g.bias_cols = p->bias_kv_cols;
+    g.bias_ss = p->bias_seq_local != 0 ? p->bias_seq_stride : -1;
+    g.bias_rows = p->bias_seq_local != 0 ? p->bias_seq_rows : 0;
     return g;
 }
 

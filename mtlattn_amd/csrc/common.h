@@ -191,6 +191,18 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
+// Element offset of the bias row of global query row `grow`, in sequence s
+// whose rows start at `qstart`: grow * qs (rows indexed globally, the
+// reference's layout), or s * ss + min(grow - qstart, rows - 1) * qs when
+// ss >= 0 (rows per sequence: a dense [B, H, Nq, Nkv] mask used in place;
+// rows past a sequence block read its last row).
+__device__ inline int64_t bias_row_offset(int64_t grow, int s, int64_t qstart, int64_t qs, int64_t ss,
+                                          int64_t rows) {
+    if (ss < 0) return grow * qs;
+    const int64_t i = grow - qstart;
+    return (int64_t)s * ss + (i < rows ? i : rows - 1) * qs;
+}
+
 // LDS direct loads (global_load_lds_*): each lane's data lands at LDS
 // lds + (4 or 16) * lane. Issued as inline asm so the compiler's wait-count
 // bookkeeping does not see them: the compiler conservatively waits for every

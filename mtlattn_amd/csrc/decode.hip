@@ -55,7 +55,7 @@ struct DecKParams {
     const int* cu_q; const int* cu_kv;
     const float* bias;
     int64_t q_rs, k_rs, v_rs;
-    int64_t bias_qs, bias_hs, bias_cols;
+    int64_t bias_qs, bias_hs, bias_cols, bias_ss, bias_rows;
     int64_t total_q, total_kv;
     int num_seqs, hq, hkv, g, hpb, n_hg, ns, chunk, n_slots;
     float scale_log2;
@@ -156,7 +156,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
 
     // this lane's bias row (head of the row, or the broadcast head)
     const float* brow = nullptr;
-    if (BIAS) brow = p.bias + grow * p.bias_qs + (int64_t)head * p.bias_hs;
+    if (BIAS)
+        brow = p.bias + bias_row_offset(grow, s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows) +
+               (int64_t)head * p.bias_hs;
 
     // Register tiles: K A-operands [2 key blocks][KC], V rows [VU units][4 keys],
     // bias of the lane's row for its 8 keys.
@@ -404,6 +406,7 @@ hipError_t launch_typed(const DecodeArgs& a, hipStream_t st) {
     p.o_part = a.o_part; p.lse_part = a.lse_part;
     p.cu_q = g.cu_q; p.cu_kv = g.cu_kv;
     p.bias = g.bias; p.bias_qs = g.bias_qs; p.bias_hs = g.bias_hs; p.bias_cols = g.bias_cols;
+    p.bias_ss = g.bias_ss; p.bias_rows = g.bias_rows;
     p.q_rs = a.q_rs; p.k_rs = a.k_rs; p.v_rs = a.v_rs;
     p.total_q = g.total_q; p.total_kv = g.total_kv;
     p.num_seqs = g.num_seqs; p.hq = g.hq; p.hkv = g.hkv; p.g = g.g;
@@ -422,7 +425,8 @@ hipError_t launch_typed(const DecodeArgs& a, hipStream_t st) {
     p.scale_log2 = g.scale * kLog2e;
     p.causal = g.causal;
     p.window = g.window;
-    p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0;
+    p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0 &&
+                (g.bias_ss < 0 || g.bias_ss % 4 == 0);
     p.block_table = a.block_table;
     p.bt_stride = a.bt_stride;
     p.page_size = a.page_size;

@@ -37,7 +37,7 @@ struct FwdKParams {
     const int* cu_q; const int* cu_kv;
     const float* bias;
     int64_t q_rs, k_rs, v_rs;
-    int64_t bias_qs, bias_hs, bias_cols;
+    int64_t bias_qs, bias_hs, bias_cols, bias_ss, bias_rows;
     int64_t total_q, total_kv;
     int num_seqs, hq, g, hpw, n_tiles, n_hg;
     float scale_log2;
@@ -147,7 +147,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     const bool has_bias = BIAS && p.bias != nullptr;
     const float* brow = nullptr;
     if (has_bias)
-        brow = p.bias + (int64_t)(qr.start + min(qrow, q_len - 1)) * p.bias_qs + (int64_t)head * p.bias_hs;
+        brow = p.bias +
+               bias_row_offset(qr.start + min(qrow, q_len - 1), s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows) +
+               (int64_t)head * p.bias_hs;
     // The bias of a whole tile (this lane's 32 keys: 4-key groups at
     // 32 kb + 8 g + 4 hi) is loaded up front, all loads in flight together,
     // and consumed after the S products; 16-byte loads when aligned.
@@ -346,6 +348,7 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     p.cu_q = g.cu_q; p.cu_kv = g.cu_kv; p.bias = g.bias;
     p.q_rs = a.q_rs; p.k_rs = a.k_rs; p.v_rs = a.v_rs;
     p.bias_qs = g.bias_qs; p.bias_hs = g.bias_hs; p.bias_cols = g.bias_cols;
+    p.bias_ss = g.bias_ss; p.bias_rows = g.bias_rows;
     p.total_q = g.total_q; p.total_kv = g.total_kv;
     p.num_seqs = g.num_seqs; p.hq = g.hq; p.g = g.g;
     p.hpw = gcd_int(g.g, kWaves);
@@ -354,7 +357,8 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     p.n_hg = g.hq / p.hpw;
     p.scale_log2 = g.scale * kLog2e;
     p.causal = g.causal; p.window = g.window > 0 ? g.window : 0;
-    p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0;
+    p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0 &&
+                (g.bias_ss < 0 || g.bias_ss % 4 == 0);
     const int64_t blocks = (int64_t)p.n_tiles * p.n_hg;
     if (blocks <= 0) return hipSuccess;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;

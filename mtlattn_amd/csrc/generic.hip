@@ -30,7 +30,7 @@ struct GenParams {
     const int* cu_q; const int* cu_kv;
     const float* bias;
     int64_t q_rs, k_rs, v_rs, do_rs;
-    int64_t bias_qs, bias_hs, bias_cols;
+    int64_t bias_qs, bias_hs, bias_cols, bias_ss, bias_rows;
     int64_t total_q, total_kv;
     int num_seqs, hq, hkv, g, d;
     float scale;
@@ -89,7 +89,9 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_fwd_kernel(GenParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     const int hi = p.causal ? min(kv_len, i + coff + 1) : kv_len;
     const int lo = p.window > 0 ? max(0, i + coff - p.window + 1) : 0;
-    const float* brow = p.bias ? p.bias + row * p.bias_qs + (int64_t)head * p.bias_hs : nullptr;
+    const float* brow =
+        p.bias ? p.bias + bias_row_offset(row, s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows) + (int64_t)head * p.bias_hs
+               : nullptr;
     float m = kNegInf, l = 0.f;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (int kt = lo; kt < hi; kt += 64) {
@@ -156,7 +158,9 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_dq_kernel(GenParams p) {
     const float dlt = p.delta[row * p.hq + head];
     const int hi = p.causal ? min(kv_len, i + coff + 1) : kv_len;
     const int lo = p.window > 0 ? max(0, i + coff - p.window + 1) : 0;
-    const float* brow = p.bias ? p.bias + row * p.bias_qs + (int64_t)head * p.bias_hs : nullptr;
+    const float* brow =
+        p.bias ? p.bias + bias_row_offset(row, s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows) + (int64_t)head * p.bias_hs
+               : nullptr;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     if (lse != kNegInf) {
         for (int kt = lo; kt < hi; kt += 64) {
@@ -231,7 +235,8 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_dkv_kernel(GenParams p) {
                 if (lse != kNegInf) {
                     float x = dot_row<T>(ks_[w], p.q, row * p.q_rs + (int64_t)head * p.d, p.d) * p.scale;
                     if (p.bias != nullptr && j < p.bias_cols)
-                        x += p.bias[row * p.bias_qs + (int64_t)head * p.bias_hs + j];
+                        x += p.bias[bias_row_offset(row, s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows) +
+                                    (int64_t)head * p.bias_hs + j];
                     pi = __expf(x - lse);
                     const float dp = dot_row<T>(vs_[w], p.dout, row * p.do_rs + (int64_t)head * p.d, p.d);
                     dsi = pi * (dp - p.delta[row * p.hq + head]);
@@ -274,6 +279,7 @@ GenParams make_gen(const Geometry& g) {
     GenParams p{};
     p.cu_q = g.cu_q; p.cu_kv = g.cu_kv; p.bias = g.bias;
     p.bias_qs = g.bias_qs; p.bias_hs = g.bias_hs; p.bias_cols = g.bias_cols;
+    p.bias_ss = g.bias_ss; p.bias_rows = g.bias_rows;
     p.total_q = g.total_q; p.total_kv = g.total_kv;
     p.num_seqs = g.num_seqs; p.hq = g.hq; p.hkv = g.hkv; p.g = g.g; p.d = g.d;
     p.scale = g.scale; p.causal = g.causal; p.window = g.window > 0 ? g.window : 0;

@@ -18,6 +18,8 @@ struct Geometry {
     int causal, window;
     const float* bias;            // nullptr = no bias
     int64_t bias_qs, bias_hs, bias_cols;
+    int64_t bias_ss = -1;         // >= 0: bias rows per sequence (bias_row_offset)
+    int64_t bias_rows = 0;        // rows per sequence block when bias_ss >= 0
 };
 
 struct FwdArgs {

@@ -65,14 +65,37 @@ void check_cu(const at::Tensor& cu_q, const at::Tensor& cu_kv, const at::Tensor&
 int64_t row_stride(const at::Tensor& t) { return t.size(0) > 1 ? t.stride(0) : t.size(1) * t.size(2); }
 
 // Bias checks of src/ext.mm:348-365, plus the key-dim extent for bounds.
+// Also accepted (no counterpart in the reference): a 4-D mask [B or 1,
+// H or 1, Nq, max_kv] indexed by (sequence, sequence-local row), used in
+// place (the SDPA adapter's dense masks).
 void fill_bias(mtlattn_problem& p, const c10::optional<at::Tensor>& attn_bias, const at::Tensor& q,
                at::Tensor& keep) {
     p.bias = nullptr;
     p.bias_q_stride = p.bias_h_stride = p.bias_kv_cols = 0;
+    p.bias_seq_local = 0;
+    p.bias_seq_stride = p.bias_seq_rows = 0;
     if (!defined(attn_bias)) return;
     keep = *attn_bias;
     TORCH_CHECK(keep.is_cuda() && keep.get_device() == q.get_device(), "mtlattn: attn_mask must be a GPU tensor");
     TORCH_CHECK(keep.scalar_type() == at::kFloat, "mtlattn: attn_mask must be float32");
+    if (keep.dim() == 4) {
+        TORCH_CHECK(keep.size(0) == p.num_seqs || keep.size(0) == 1,
+                    "mtlattn: a 4-D attn_mask's dim0 must be the number of sequences or 1");
+        TORCH_CHECK(keep.size(1) == q.size(1) || keep.size(1) == 1, "mtlattn: attn_mask dim1 must be num_heads (",
+                    q.size(1), ") or 1 (broadcast)");
+        TORCH_CHECK(keep.size(2) >= 1, "mtlattn: a 4-D attn_mask needs at least one query row");
+        TORCH_CHECK(keep.size(3) <= 1 || keep.stride(3) == 1, "mtlattn: attn_mask last dim must be contiguous");
+        TORCH_CHECK(keep.stride(0) >= 0 && keep.stride(1) >= 0 && keep.stride(2) >= 0,
+                    "mtlattn: attn_mask strides must be non-negative");
+        p.bias = keep.data_ptr<float>();
+        p.bias_seq_local = 1;
+        p.bias_seq_stride = keep.size(0) == 1 ? 0 : keep.stride(0);
+        p.bias_seq_rows = keep.size(2);
+        p.bias_q_stride = keep.stride(2);
+        p.bias_h_stride = keep.size(1) == 1 ? 0 : keep.stride(1);
+        p.bias_kv_cols = keep.size(3);
+        return;
+    }
     TORCH_CHECK(keep.dim() == 3, "mtlattn: attn_mask must be [total_q, H or 1, max_kv]");
     TORCH_CHECK(keep.size(0) == q.size(0), "mtlattn: attn_mask dim0 (", keep.size(0), ") must equal total_q (",
                 q.size(0), ")");

@@ -46,18 +46,27 @@ def test_prep_bias():
 
 
 def test_sdpa_mask_to_bias_bool_and_float():
+    """Dense masks become [b, h, Nq, Nkv] fp32 additive biases that the kernels
+    index by (sequence, local row): bool -> 0 / -inf, fp32 float masks used in
+    place (no copy), broadcast dims kept at size 1."""
     B, H, Nq, Nkv = 2, 3, 4, 5
     m = torch.rand(B, H, Nq, Nkv) > 0.5
     b = M._sdpa_mask_to_bias(m, B, H, Nq, Nkv)
-    assert b.shape == (B * Nq, H, Nkv) and b.dtype == torch.float32
-    exp = torch.where(m, 0.0, float("-inf")).permute(0, 2, 1, 3).reshape(B * Nq, H, Nkv)
-    assert torch.equal(b, exp)
+    assert b.shape == (B, H, Nq, Nkv) and b.dtype == torch.float32
+    assert torch.equal(b, torch.where(m, 0.0, float("-inf")))
     f = torch.randn(1, 1, Nq, Nkv)
     bf = M._sdpa_mask_to_bias(f, B, H, Nq, Nkv)
-    assert bf.shape == (B * Nq, 1, Nkv)            # head broadcast kept at 1
-    assert torch.equal(bf[Nq:2 * Nq, 0], f[0, 0])
+    assert bf.shape == (1, 1, Nq, Nkv) and bf.data_ptr() == f.data_ptr()   # in place
     two_d = M._sdpa_mask_to_bias(f[0, 0], B, H, Nq, Nkv)
-    assert torch.equal(two_d, bf)
+    assert two_d.shape == (1, 1, Nq, Nkv) and two_d.data_ptr() == f.data_ptr()
+    full = torch.randn(B, H, Nq, Nkv)
+    assert M._sdpa_mask_to_bias(full, B, H, Nq, Nkv).data_ptr() == full.data_ptr()
+    # a strided key dim is made contiguous; half precision is cast to fp32
+    t = torch.randn(B, H, Nkv, Nq).transpose(2, 3)
+    assert M._sdpa_mask_to_bias(t, B, H, Nq, Nkv).stride(-1) == 1
+    assert M._sdpa_mask_to_bias(full.half(), B, H, Nq, Nkv).dtype == torch.float32
+    # _prep_bias keeps a 4-D mask with a unit-stride key dim as it is
+    assert M._prep_bias(full).data_ptr() == full.data_ptr()
 
 
 @pytest.mark.parametrize("shape,msg", [

@@ -28,6 +28,8 @@ class Problem(ctypes.Structure):
         ("cu_seqlens_q", ctypes.c_void_p), ("cu_seqlens_kv", ctypes.c_void_p),
         ("bias", ctypes.c_void_p), ("bias_q_stride", ctypes.c_int64),
         ("bias_h_stride", ctypes.c_int64), ("bias_kv_cols", ctypes.c_int64),
+        ("bias_seq_local", ctypes.c_int32), ("bias_seq_stride", ctypes.c_int64),
+        ("bias_seq_rows", ctypes.c_int64),
     ]
 
 

@@ -508,6 +508,45 @@ def test_sdpa_mask(mt):
         assert err < 5e-3
 
 
+def test_bias_per_sequence_rows(mt):
+    """A 4-D bias [B or 1, H or 1, Nq, max_kv] is indexed by (sequence,
+    sequence-local row) in place; rows past Nq read row Nq - 1. It must give
+    bitwise the results of the 3-D bias gathered from it, forward and
+    backward, on the matrix-core, portable and decode kernels."""
+    cases = [
+        ("bf16 D128 ragged causal", [300, 77, 513], [300, 77, 513], 8, 2, 128, torch.bfloat16, True, (3, 8), 513),
+        ("fp16 D64 broadcast batch+head", [200, 650], [200, 650], 4, 4, 64, torch.float16, False, (1, 1), 650),
+        ("bf16 rows past Nq clamp", [100, 260], [100, 260], 8, 8, 128, torch.bfloat16, True, (2, 1), 200),
+        ("fp32 portable kernels", [40, 90], [40, 90], 4, 2, 64, torch.float32, True, (2, 4), 90),
+        ("decode q_len 2", [2, 1], [3000, 2500], 8, 2, 128, torch.bfloat16, True, (2, 8), 2),
+    ]
+    for name, ql, kl, hq, hkv, d, dt, causal, (bb, bh), nq in cases:
+        _banner(f"per-sequence bias rows: {name}")
+        q, k, v = _inputs(ql, kl, hq, hkv, d, dt, seed=len(name))
+        g = torch.Generator().manual_seed(len(name) + 1)
+        b4 = torch.randn((bb, bh, nq, max(kl)), generator=g)
+        b4[..., ::5] -= 20.0
+        rows = []
+        for s, L in enumerate(ql):
+            idx = torch.clamp(torch.arange(L), max=nq - 1)
+            rows.append(b4[s if bb > 1 else 0][:, idx, :].transpose(0, 1))
+        b3 = torch.cat(rows).contiguous()                       # [total_q, bh, max_kv]
+        cq, ck = cu_of(ql, "cuda"), cu_of(kl, "cuda")
+        dout = randn((sum(ql), hq, d), dt, g).cuda()
+        res = []
+        for bias in (b4, b3):
+            qm, km, vm = (t.cuda().requires_grad_() for t in (q, k, v))
+            out = mt.varlen_attention(qm, km, vm, cq, ck, max(ql), causal=causal, attn_bias=bias.cuda())
+            out.backward(dout)
+            res.append([t.detach().cpu() for t in (out, qm.grad, km.grad, vm.grad)])
+        for nm, a, b in zip(("out", "dQ", "dK", "dV"), res[0], res[1]):
+            assert torch.equal(a, b), f"{name}: {nm} differs between 4-D and gathered 3-D bias"
+        ref, _ = oracle.varlen_forward(q, k, v, cu_of(ql), cu_of(kl), 1 / math.sqrt(d), causal, 0, b3)
+        err = (res[0][0].float() - ref).abs().max().item()
+        print(f"  bitwise equal; max_err vs oracle={err:.3e}", flush=True)
+        assert err < REF_ATOL[dt]
+
+
 def test_outlier_channels(mt):
     """Outlier channels x300 (tests/test_correctness.py:449-465): finite output,
     loose tolerance."""
