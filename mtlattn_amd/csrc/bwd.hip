@@ -68,13 +68,18 @@ __device__ inline void store4(void* base, int64_t off, float a, float b, float c
 // forward. This launch outputs the DO columns from C0 (head dims above 128
 // take several launches, the S and dP products recomputed in each: their
 // accumulators would not fit otherwise). Key tiles hold 32 * KB keys.
-template <typename T, int D, int DV, int DO, int C0, int KB, bool BIAS, bool OUT_F32>
+// BROWS > 0: a head-broadcast bias staged in the LDS ring with the K/V tiles
+// (workgroups of BROWS query rows, 64-key tiles), as in the forward.
+template <typename T, int D, int DV, int DO, int C0, int KB, bool BIAS, bool OUT_F32, int BROWS = 0>
 __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     constexpr int DC = (DV + 15) / 16, DB = (DO + 31) / 32;
     constexpr int KT = 32 * KB;               // keys per tile
     static_assert(C0 % 32 == 0 && C0 + DO <= D, "output slice");
+    constexpr bool LDSB = BROWS > 0;
+    static_assert(!LDSB || (BIAS && KT == 64), "staged bias: 64-key tiles");
     constexpr int TILE = KT * D * 2;
-    constexpr int STAGE = 2 * TILE;           // K, V
+    constexpr int BTILE = BROWS * KT * 4;
+    constexpr int STAGE = 2 * TILE + BTILE;   // K, V, staged bias
     constexpr int NBUF = 3;
     constexpr int LOADS = STAGE / 1024 / kWaves;
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE];
@@ -128,8 +133,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     }
     // bias row of this lane's query (rows past the end read the last row);
     // columns at or past bias_cols read as 0
+    constexpr bool reg_bias = BIAS && !LDSB;     // bias loaded into registers per tile
     const float* brow = nullptr;
-    if (BIAS)
+    if (reg_bias)
         brow = p.bias + bias_row_offset(grow, s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows) +
                (int64_t)head * p.bias_hs;
     // settle these loads here: the key loop's own wait counts cover only the
@@ -149,11 +155,22 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     TileStager<D, KT, kWaves, DV> kst, vst;
     kst.init(p.k_rs, w, lane);
     vst.init(p.v_rs, w, lane);
+    // staged bias: WG row r is query q0 + r (rows past the end repeat the last)
+    BiasStager<LDSB ? BROWS : 32> bst;
+    const float* brow0 = nullptr;
+    if (LDSB) {
+        auto row_off = [&](int r) {
+            return bias_row_offset(qr.start + min(q0 + r, q_len - 1), s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows);
+        };
+        bst.init(row_off, w, lane);
+        brow0 = p.bias + row_off(0);
+    }
     auto stage = [&](int it) {
         char* buf = smem + (it % NBUF) * STAGE;
         const int kt = kv_lo + it * KT;
         kst.issue(buf, kbase, p.k_rs, kt, kv_len, w, lane);
         vst.issue(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
+        if (LDSB) bst.issue(buf + 2 * TILE, brow0, kt, (int)p.bias_cols, w);
     };
 
     const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
@@ -170,12 +187,28 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         __syncthreads();
         // (with a bias, the tile loads go out after the bias is consumed: the
         // bias loads' wait would otherwise also wait for them)
-        if (!BIAS && it + 2 < n_kv_tiles) stage(it + 2);
+        if (!reg_bias && it + 2 < n_kv_tiles) stage(it + 2);
         const int kt = kv_lo + it * KT;
         // the bias of the whole tile, all loads in flight together (4-key
         // groups at 32 kb + 8 g + 4 hi)
         f32x4_t bv[4 * KB];
-        if (BIAS) {
+        if (LDSB) {   // from the staged tile: this lane's query row
+            const char* bt = opaque(smem + (it % NBUF) * STAGE + 2 * TILE + bias_base(32 * (w % wph) + l32, hi));
+#pragma unroll
+            for (int i = 0; i < 4 * KB; ++i)
+                bv[i] = *reinterpret_cast<const f32x4_t*>(lds_xor(bt, 16 * (8 * (i >> 2) + 2 * (i & 3))));
+            if (kt + KT > p.bias_cols) {   // keys at or past the bias columns read as 0
+                asm volatile("");
+#pragma unroll
+                for (int i = 0; i < 4 * KB; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi + j >= p.bias_cols) bv[i][j] = 0.f;
+            }
+            // (keeps these reads out of the operand read pipeline below)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (reg_bias) {
             if (kt + KT <= p.bias_cols && p.bias_v4) {
 #pragma unroll
                 for (int i = 0; i < 4 * KB; ++i)
@@ -228,7 +261,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
                 if (BIAS) x = fmaf(bv[4 * kb + (r >> 2)][r & 3], kLog2e, x);
                 sacc[kb][r] = __builtin_amdgcn_exp2f(x);
             }
-            if (BIAS && kb == KB - 1 && it + 2 < n_kv_tiles) stage(it + 2);
+            if (reg_bias && kb == KB - 1 && it + 2 < n_kv_tiles) stage(it + 2);
             if (need_mask) {     // out-of-band keys -> P = 0
                 asm volatile("");   // keep a real branch (no speculated selects on every tile)
 #pragma unroll
@@ -683,6 +716,20 @@ hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     p.n_hg = a.geo.hq / p.hpw;
     const int64_t blocks = (int64_t)p.n_tiles * p.n_hg;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    // head-broadcast bias staged in LDS: the forward's conditions
+    const Geometry& g = a.geo;
+    if (KB == 2 && D <= 128 && g.bias != nullptr && g.bias_hs == 0 && p.bias_v4 && g.bias_cols >= 4 &&
+        g.bias_cols % 4 == 0 && (QT == 32 || QT == 64) && ((int64_t)QT * g.bias_qs + g.bias_cols) * 4 < ((int64_t)1 << 32)) {
+        if constexpr (KB == 2 && D <= 128) {
+            if (QT == 32)
+                hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32, 32>), dim3((unsigned)blocks),
+                                   dim3(NW * 64), 0, st, p);
+            else
+                hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32, 64>), dim3((unsigned)blocks),
+                                   dim3(NW * 64), 0, st, p);
+            return hipGetLastError();
+        }
+    }
     if (a.geo.bias != nullptr)
         hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64),
                            0, st, p);

@@ -285,6 +285,52 @@ struct TileStager {
     }
 };
 
+// Stages the fp32 bias of a key tile -- ROWS query rows x 64 keys, one
+// head-broadcast block shared by every wave of a workgroup -- into LDS with
+// global_load_lds_dwordx4: rows of 256 bytes, 16-byte chunk c of row r at
+// position c ^ (r & 15), so that 16 consecutive rows read at one chunk (the
+// MFMA C layout: lane = query row) hit 16 distinct bank groups. Instruction
+// i (1 KB) fills rows 4i .. 4i + 3; 8 waves share the ROWS / 4 instructions.
+// A lane's source is its row's bias row plus the tile's first column: the
+// row part is a fixed 32-bit byte offset from the workgroup's first row
+// (rows past a sequence's end repeat its last row), the column part the
+// chunk. Columns at or past `cols` (a multiple of 4) are never read: a
+// tile crossing `cols` loads the row's last chunk in their place, and the
+// readers zero those keys.
+template <int ROWS>
+struct BiasStager {
+    static_assert(ROWS == 32 || ROWS == 64, "bias tile rows");
+    static constexpr int PER = ROWS / 4;   // 1 KB instructions per tile
+    static constexpr int N = PER / 8;      // per wave
+    uint32_t roff[N];                      // byte offset of the lane's row from row 0
+    int chunk[N];                          // chunk the lane loads
+    // row_off(r): element offset of WG row r's bias row (r = 0 .. ROWS - 1)
+    template <typename RowOff>
+    __device__ void init(RowOff row_off, int w, int lane) {
+        const int64_t base = row_off(0);
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int r = 4 * (w + 8 * j) + (lane >> 4);
+            chunk[j] = (lane & 15) ^ (r & 15);
+            roff[j] = (uint32_t)((row_off(r) - base) * 4);
+        }
+    }
+    // row0: bias row of WG row 0 (wave-uniform); keys kt .. kt + 63
+    __device__ void issue(char* tile, const float* row0, int kt, int cols, int w) const {
+        if (kt + 64 <= cols) {
+#pragma unroll
+            for (int j = 0; j < N; ++j) lds_dma16s(row0 + kt, roff[j] + 16u * (uint32_t)chunk[j], tile + (w + 8 * j) * 1024);
+        } else {   // columns clamped to the row's last chunk
+#pragma unroll
+            for (int j = 0; j < N; ++j)
+                lds_dma16s(row0, roff[j] + 4u * (uint32_t)min(kt + 4 * chunk[j], cols - 4), tile + (w + 8 * j) * 1024);
+        }
+    }
+};
+// Byte offset, within a staged bias tile, of chunk (8 a + 2 b + hi) of row
+// rr is bias_base(rr, hi) ^ (16 (8 a + 2 b)).
+__device__ inline uint32_t bias_base(int rr, int hi) { return (uint32_t)(rr * 256 + 16 * (hi ^ (rr & 15))); }
+
 // Wait until at most N of this wave's vector memory operations are pending
 // (s_waitcnt vmcnt(N), other counters untouched); N <= 15.
 template <int N>

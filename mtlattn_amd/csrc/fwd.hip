@@ -40,15 +40,17 @@ struct FwdKParams {
     int64_t bias_qs, bias_hs, bias_cols, bias_ss, bias_rows;
     int64_t total_q, total_kv;
     int num_seqs, hq, g, hpw, n_tiles, n_hg;
-    float scale_log2;
+    float scale, scale_log2;
     int causal, window;
     int bias_v4;      // bias rows 16-byte aligned (pointer and strides)
     int col0;         // first output (and V) column of this launch
 };
 
-// GENERAL = explicit per-element logit scaling, with the optional bias; the
-// fast variant (no bias, scale > 0) reduces raw scores and folds the scale
-// into one FMA per element.
+// Softmax modes (SM). 0: no bias, scale > 0: the running max is taken over
+// raw scores and the scale folded into one FMA per element. 1: bias,
+// scale > 0: logits y = s * scale + bias (one FMA), the max taken over y and
+// log2(e) folded into the exponent's FMA. 2: any scale, optional bias:
+// explicit per-element scaling (scale <= 0 flips the order of raw scores).
 // DV is the head dim (a multiple of 8). K tiles are DK wide (64, 128 or 256
 // >= DV): the S contraction uses ceil(DV / 16) k-chunks, Q's columns past DV
 // are zero. V tiles hold the DO columns [col0, col0 + DO) that this launch
@@ -56,14 +58,21 @@ struct FwdKParams {
 // blocks and stores the DO valid columns. Head dims above 128 run as two
 // launches that each produce half of the output columns (the S products are
 // recomputed; their accumulators would not fit otherwise).
-template <typename T, int DK, int DV, int DVL, int DO, bool GENERAL>
+// BROWS > 0 (SM 1 only): the bias is one block broadcast over heads and a
+// workgroup covers BROWS query rows; each key tile's bias block is staged in
+// the LDS ring with the K/V tiles (read from LDS by all waves of all heads)
+// instead of every wave loading its rows from global memory.
+template <typename T, int DK, int DV, int DVL, int DO, int SM, int BROWS = 0>
 __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
-    constexpr bool BIAS = GENERAL;
+    constexpr bool BIAS = SM != 0;
+    constexpr bool LDSB = BROWS > 0;
+    static_assert(!LDSB || SM == 1, "staged bias is for the biased raw-max softmax");
     constexpr int DC = (DV + 15) / 16;       // MFMA k-chunks over the head dim
     constexpr int DB = (DO + 31) / 32;       // 32-row output blocks
     constexpr int KTILE = kKT * DK * 2;      // bytes of one K tile
     constexpr int VTILE = kKT * DVL * 2;     // bytes of one V tile
-    constexpr int STAGE = KTILE + VTILE;     // K tile + V tile, both row-major
+    constexpr int BTILE = BROWS * kKT * 4;   // bytes of one staged bias tile
+    constexpr int STAGE = KTILE + VTILE + BTILE;   // K, V (row-major), bias
     constexpr int NBUF = 3;                  // ring of staged key tiles
     constexpr int LOADS = STAGE / 1024 / kWaves;   // direct loads per wave per tile
     static_assert(LOADS <= 15 && STAGE % (1024 * kWaves) == 0, "staging");
@@ -124,11 +133,22 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     TileStager<DVL, kKT, kWaves, DO> vst;
     kst.init(p.k_rs, w, lane);
     vst.init(p.v_rs, w, lane);
+    // Staged bias: WG row r is query q0 + r (rows past the end repeat the last)
+    BiasStager<LDSB ? BROWS : 32> bst;
+    const float* brow0 = nullptr;
+    if (LDSB) {
+        auto row_off = [&](int r) {
+            return bias_row_offset(qr.start + min(q0 + r, q_len - 1), s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows);
+        };
+        bst.init(row_off, w, lane);
+        brow0 = p.bias + row_off(0);
+    }
     auto stage = [&](int it) {
         char* buf = smem + (it % NBUF) * STAGE;
         const int kt = kv_lo + it * kKT;
         kst.issue(buf, kbase, p.k_rs, kt, kv_len, w, lane);
         vst.issue(buf + KTILE, vbase, p.v_rs, kt, kv_len, w, lane);
+        if (LDSB) bst.issue(buf + KTILE + VTILE, brow0, kt, (int)p.bias_cols, w);
     };
 
     // per-lane LDS offsets: K operand rows 32 kb + l32 (chunk 2 kc + hi) and
@@ -145,8 +165,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     // Bias row of this lane's query (rows past the sequence end read its last
     // row: finite, never stored). Columns at or past bias_cols read as 0.
     const bool has_bias = BIAS && p.bias != nullptr;
+    const bool reg_bias = has_bias && !LDSB;     // bias loaded into registers per tile
     const float* brow = nullptr;
-    if (has_bias)
+    if (reg_bias)
         brow = p.bias +
                bias_row_offset(qr.start + min(qrow, q_len - 1), s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows) +
                (int64_t)head * p.bias_hs;
@@ -170,7 +191,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         }
     };
     const float c2 = p.scale_log2;
-    constexpr bool raw_max = !GENERAL;   // max(s * c) = c * max(s) needs c > 0 (host-checked)
+    // raw-max modes: the max is taken over x (raw scores, or s * scale + bias)
+    // and cmul * x is the base-2 logit; max(cmul * x) = cmul * max(x) needs
+    // cmul > 0 (scale > 0, host-checked)
+    constexpr bool raw_max = SM != 2;
+    const float cmul = SM == 1 ? kLog2e : c2;
     // Rescale O only when the running max grows by more than 2^8: unnormalised
     // weights stay <= 256, exact after the final division by the row sum.
     constexpr float kRescale = 8.f;
@@ -192,10 +217,27 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         // the buffer of tile it + 2 was last read in iteration it - 1 (with a
         // bias, the tile loads go out after the bias is consumed: the bias
         // loads' wait would otherwise also wait for them)
-        if (!has_bias && it + 2 < n_kv_tiles) stage(it + 2);
+        if (!reg_bias && it + 2 < n_kv_tiles) stage(it + 2);
         const int kt = kv_lo + it * kKT;
         f32x4_t bv[8];
-        if (has_bias) load_bias(kt, bv);
+        if (reg_bias) load_bias(kt, bv);
+        if (LDSB) {
+            // this lane's 4-key groups of its query row from the staged tile
+            const char* bt = opaque(smem + (it % NBUF) * STAGE + KTILE + VTILE + bias_base(32 * (w % wph) + l32, hi));
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                bv[i] = *reinterpret_cast<const f32x4_t*>(lds_xor(bt, 16 * (8 * (i >> 2) + 2 * (i & 3))));
+            if (kt + kKT > p.bias_cols) {   // keys at or past the bias columns read as 0
+                asm volatile("");
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi + j >= p.bias_cols) bv[i][j] = 0.f;
+            }
+            // (keeps these reads out of the K operand read pipeline below)
+            __builtin_amdgcn_sched_barrier(0);
+        }
 
         // A tile outside this wave's band is computed fully masked (P = 0)
         // rather than skipped: a branch around the MFMAs makes the compiler
@@ -253,7 +295,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const float x = sacc[kb][r0 + j];
-                    e[j] = __builtin_amdgcn_exp2f(raw_max ? fmaf(x, c2, -m_use) : x - m_use);
+                    e[j] = __builtin_amdgcn_exp2f(raw_max ? fmaf(x, cmul, -m_use) : x - m_use);
                 }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -263,7 +305,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
             }
             return sum;
         };
-        if (!raw_max) {
+        if (SM == 1) {   // x = s * scale + bias (masked s = -inf stays -inf: scale > 0)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[kb][r] = fmaf(sacc[kb][r], p.scale, bv[4 * kb + (r >> 2)][r & 3]);
+        }
+        if (SM == 2) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -283,7 +331,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
-            if (raw_max) mx *= c2;
+            if (raw_max) mx *= cmul;
             mx = pair_max(mx);
             const float m_new = mx > m_run + slack ? mx : m_run;
             if (__any(m_new != m_run)) {
@@ -295,7 +343,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
             m_run = m_new;
         };
         if constexpr (kDeferMax) {
-            if (has_bias && it + 2 < n_kv_tiles) stage(it + 2);
+            if (reg_bias && it + 2 < n_kv_tiles) stage(it + 2);
             float ts = weights(m_run == kNegInf ? 0.f : m_run, 0.f);
             if (__any(!(ts < kMaxTileSum) | ((m_run == kNegInf) & row_live))) {
                 asm volatile("");
@@ -305,7 +353,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
             l_run += ts;
         } else {
             update_max(kRescale);
-            if (has_bias && it + 2 < n_kv_tiles) stage(it + 2);
+            if (reg_bias && it + 2 < n_kv_tiles) stage(it + 2);
             l_run = weights(m_run == kNegInf ? 0.f : m_run, l_run);
         }
         // O^T += V^T P^T; V^T operands are transposed reads of the row-major V tile
@@ -355,6 +403,7 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     const int QT = 32 * (kWaves / p.hpw);
     p.n_tiles = (int)(g.total_q / QT) + g.num_seqs + 1;
     p.n_hg = g.hq / p.hpw;
+    p.scale = g.scale;
     p.scale_log2 = g.scale * kLog2e;
     p.causal = g.causal; p.window = g.window > 0 ? g.window : 0;
     p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0 &&
@@ -362,15 +411,38 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     const int64_t blocks = (int64_t)p.n_tiles * p.n_hg;
     if (blocks <= 0) return hipSuccess;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    // A head-broadcast bias whose rows are 16-byte aligned is staged in LDS
+    // when a workgroup covers 32 or 64 query rows (the staged tile's byte
+    // offsets, rows plus columns, stay below 2^32)
+    int brows = 0;
+    const int sm = !(p.scale_log2 > 0.f) ? 2 : g.bias != nullptr ? 1 : 0;
+    if (DK <= 128 && sm == 1 && g.bias_hs == 0 && p.bias_v4 && g.bias_cols >= 4 && g.bias_cols % 4 == 0 &&
+        (QT == 32 || QT == 64) && ((int64_t)QT * g.bias_qs + g.bias_cols) * 4 < ((int64_t)1 << 32))
+        brows = QT;
     // DO < DV: one launch per DO-column slice; the first writes the LSE
     for (int c0 = 0; c0 < DV; c0 += DO) {
         p.col0 = c0;
         p.lse = c0 == 0 ? a.lse : nullptr;
-        if (g.bias != nullptr || !(p.scale_log2 > 0.f))
-            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, true>), dim3((unsigned)blocks), dim3(kThreads), 0,
+        if constexpr (DK <= 128) {
+            if (brows == 32) {
+                hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 1, 32>), dim3((unsigned)blocks),
+                                   dim3(kThreads), 0, st, p);
+                continue;
+            }
+            if (brows == 64) {
+                hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 1, 64>), dim3((unsigned)blocks),
+                                   dim3(kThreads), 0, st, p);
+                continue;
+            }
+        }
+        if (sm == 2)
+            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 2>), dim3((unsigned)blocks), dim3(kThreads), 0,
+                               st, p);
+        else if (sm == 1)
+            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 1>), dim3((unsigned)blocks), dim3(kThreads), 0,
                                st, p);
         else
-            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, false>), dim3((unsigned)blocks), dim3(kThreads), 0,
+            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 0>), dim3((unsigned)blocks), dim3(kThreads), 0,
                                st, p);
     }
     return hipGetLastError();

@@ -416,6 +416,76 @@ def test_bias_bwd(mt):
          bias=_make_bias(1280, 8, 1280, False))
 
 
+def _misaligned(t):
+    """A copy of `t` whose storage starts 4 bytes past a 16-byte boundary: the
+    kernels then take the per-row (register) bias path."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    m = buf[1:].view(t.shape)
+    m.copy_(t)
+    assert m.data_ptr() % 16 != 0
+    return m
+
+
+def test_bias_staged_broadcast(mt):
+    """Head-broadcast bias with GQA groups of 4 or 8 heads (32 or 64 query rows
+    per workgroup) is staged in LDS with the K/V tiles. Checked against the
+    oracle and bitwise against the per-row path (the same bias at a misaligned
+    address), including tiles that cross the bias width and a bias narrower
+    than the keys (missing columns read as 0)."""
+    cases = [
+        # name, q_lens, kv_lens, Hq, Hkv, D, dtype, causal, window, bias cols
+        ("g=4 D128 bf16 causal ragged", [300, 77, 513], [300, 77, 513], 32, 8, 128, torch.bfloat16, True, 0, 516),
+        ("g=8 D128 fp16 causal window", [700], [700], 16, 2, 128, torch.float16, True, 200, 704),
+        ("g=4 D64 fp16 non-causal ragged", [200, 650], [200, 650], 8, 2, 64, torch.float16, False, 0, 652),
+        ("g=4 D96 bf16 cross", [64, 130], [900, 300], 8, 2, 96, torch.bfloat16, False, 0, 900),
+        ("g=4 D128 fp16 bias narrower than keys", [400], [400], 8, 2, 128, torch.float16, True, 0, 260),
+    ]
+    for name, ql, kl, hq, hkv, d, dt, causal, window, cols in cases:
+        g = torch.Generator().manual_seed(len(name))
+        bias = torch.randn((sum(ql), 1, cols), generator=g)
+        bias[:, :, ::7] -= 30.0
+        full = torch.zeros((sum(ql), 1, max(max(kl), cols)))
+        full[:, :, :cols] = bias                       # missing columns read as 0
+        # the oracle takes the zero-padded bias; the kernels the narrow one
+        _banner(f"staged bias: {name}")
+        q, k, v = _inputs(ql, kl, hq, hkv, d, dt, seed=3)
+        cq, ck = cu_of(ql), cu_of(kl)
+        scale = 1.0 / math.sqrt(d)
+        outs = []
+        for b in (bias.cuda(), _misaligned(bias.cuda())):
+            lse = torch.empty(sum(ql), hq, dtype=torch.float32, device="cuda")
+            o = mt._C.varlen_attention(q.cuda(), k.cuda(), v.cuda(), cq.cuda(), ck.cuda(), max(ql), scale, causal,
+                                       window, lse, b)
+            outs.append((o.cpu(), lse.cpu()))
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0][0], outs[1][0]), f"{name}: staged and per-row bias outputs differ"
+        assert torch.equal(outs[0][1], outs[1][1]), f"{name}: staged and per-row bias LSE differ"
+        ref, ref_lse = oracle.varlen_forward(q, k, v, cq, ck, scale, causal, window, full[:, :, :max(kl)])
+        err = (outs[0][0].float() - ref).abs().max().item()
+        fin = torch.isfinite(ref_lse)
+        lerr = (outs[0][1][fin] - ref_lse[fin]).abs().max().item()
+        print(f"  bitwise equal to the per-row path; max_err={err:.3e} lse_err={lerr:.3e}", flush=True)
+        assert err < REF_ATOL[dt], f"{name}: max_err {err}"
+        assert lerr < LSE_TOL[dt], f"{name}: lse err {lerr}"
+        # backward: dQ reads the staged tile too (dK/dV the per-row path)
+        dout = randn((sum(ql), hq, d), dt, torch.Generator().manual_seed(11))
+        grads = []
+        for b in (bias.cuda(), _misaligned(bias.cuda())):
+            qm, km, vm = (t.cuda().requires_grad_() for t in (q, k, v))
+            o = mt.varlen_attention(qm, km, vm, cq.cuda(), ck.cuda(), max(ql), causal=causal, window=window,
+                                    attn_bias=b)
+            o.backward(dout.cuda())
+            grads.append([t.grad.cpu() for t in (qm, km, vm)])
+        for nm, x, y in zip(("dQ", "dK", "dV"), grads[0], grads[1]):
+            assert torch.equal(x, y), f"{name}: staged and per-row bias {nm} differ"
+        _, _, rq, rk, rv = oracle.varlen_forward_backward(q, k, v, dout, cq, ck, None, causal, window,
+                                                          full[:, :, :max(kl)])
+        gerr = max((x.float() - r).abs().max().item() for x, r in zip(grads[0], (rq, rk, rv)))
+        gtol = 4e-2 if dt == torch.bfloat16 else 6e-3
+        print(f"  grads bitwise equal to the per-row path; grad_err={gerr:.3e} (tol {gtol})", flush=True)
+        assert gerr < gtol, f"{name}: grad err {gerr}"
+
+
 # SDPA adapter, padding-mask packing, mask -> bias (tests/test_correctness.py:437-448)
 def test_sdpa_adapter(mt):
     for (B, Hq, Hkv, N, causal) in [(2, 8, 8, 1024, False), (1, 8, 2, 2048, False), (2, 12, 12, 512, True)]:
