@@ -47,6 +47,7 @@ struct BwdKParams {
     float scale, scale_log2;
     int causal, window;
     int bias_v4;      // bias rows 16-byte aligned (pointer and strides)
+    int bias_b32;     // 64 bias rows plus a row's columns span < 2^32 bytes (32-bit buffer offsets)
 };
 
 template <typename T, bool OUT_F32>
@@ -56,6 +57,14 @@ __device__ inline void store4(void* base, int64_t off, float a, float b, float c
     } else {
         st8(reinterpret_cast<uint16_t*>(base) + off, u32x2_t{T::pack2(a, b), T::pack2(c, d)});
     }
+}
+
+// Staged lse / delta columns as the dK/dV products use them: lse (which = 0)
+// becomes -lse log2(e), with rows of no allowed key (lse = -inf) giving -inf
+// so that every P of theirs is exp2(-inf) = 0; delta (which = 1) becomes -delta.
+__device__ inline void neg_col(float* x, int which) {
+    const float v = *x;
+    *x = which ? -v : (v == kNegInf ? kNegInf : -v * kLog2e);
 }
 
 // ---------------------------------------------------------------------------
@@ -442,7 +451,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     if (n_stages > 0) {
         stage(0);
         wait_vmcnt<0>();
-        if (ldw == 0 || ldw == 1) reinterpret_cast<float*>(smem + 2 * TILE)[64 * ldw + lane] *= ldw ? -1.f : -kLog2e;
+        if (ldw == 0 || ldw == 1) neg_col(reinterpret_cast<float*>(smem + 2 * TILE) + 64 * ldw + lane, ldw);
         __syncthreads();
     }
     for (int st = 0; n_stages > 0 && st <= n_stages; ++st) {
@@ -463,7 +472,31 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             // loads in flight together under the S products; columns at or
             // past bias_cols read as 0, rows past the end read the last row
             float bvals[NQB][16];
-            if (BIAS) {
+            // Whole stage inside the sequence (and its bias rows) and every key
+            // of the pair inside the bias columns: buffer loads from the
+            // stage's first bias row, the lane's column and 4 hi rows in the
+            // per-lane offset, each element's row in the scalar offset (no
+            // per-element address arithmetic, no column select).
+            const bool fast_bias = BIAS && p.bias_b32 && (qt + QTL <= q_len) &&
+                                   ((p.bias_ss < 0) | (qt + QTL <= p.bias_rows)) && (kw + kKW <= p.bias_cols);
+            if (fast_bias) {
+                const float* b0 = p.bias + bias_row_offset(qr.start + qt, s, qr.start, p.bias_qs, p.bias_ss,
+                                                           p.bias_rows) + (int64_t)h * p.bias_hs;
+                const __amdgpu_buffer_rsrc_t rs =
+                    __builtin_amdgcn_make_buffer_rsrc((void*)b0, (short)0, (int)0xffffffff, 0x00020000);
+                const int voff = (int)((4 * hi * p.bias_qs + key) * 4);
+                // row stride in bytes, opaque here so that the 32 per-row
+                // scalar offsets are formed per stage (one s_mul each) rather
+                // than hoisted out of the loop into 32 live SGPRs
+                int rs4 = (int)(p.bias_qs * 4);
+                asm volatile("" : "+s"(rs4));
+#pragma unroll
+                for (int qb = 0; qb < NQB; ++qb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        bvals[qb][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                            rs, voff, (32 * qb + 8 * (r >> 2) + (r & 3)) * rs4, 0));
+            } else if (BIAS) {
                 const float* bcol = p.bias + (int64_t)h * p.bias_hs + min(key, (int)p.bias_cols - 1);
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb)
@@ -494,10 +527,12 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                     for (int e = 0; e < 4; ++e) {
                         const int r = 4 * rg + e;
                         float arg;
-                        if (BIAS) {
-                            const float x = fmaf(key < p.bias_cols ? bvals[qb][r] : 0.f, kLog2e, sacc[qb][r] * c2);
-                            // rows whose every logit is -inf (bias) have lse = -inf: P = 0
-                            arg = x == kNegInf ? kNegInf : x + l4[e];
+                        // (rows with no allowed key or every logit -inf
+                        // have lse = -inf and l4 = -inf: P = 0)
+                        if (fast_bias) {
+                            arg = fmaf(bvals[qb][r], kLog2e, fmaf(sacc[qb][r], c2, l4[e]));
+                        } else if (BIAS) {   // the same arithmetic, keys past the bias columns read 0
+                            arg = fmaf(key < p.bias_cols ? bvals[qb][r] : 0.f, kLog2e, fmaf(sacc[qb][r], c2, l4[e]));
                         } else {
                             arg = fmaf(sacc[qb][r], c2, l4[e]);
                         }
@@ -589,7 +624,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         wait_vmcnt<0>();
         if ((ldw == 0 || ldw == 1) && st + 1 < n_stages) {
             float* l = reinterpret_cast<float*>(smem + ((st + 1) % NBUF) * STAGE + 2 * TILE);
-            l[64 * ldw + lane] *= ldw ? -1.f : -kLog2e;
+            neg_col(l + 64 * ldw + lane, ldw);
         }
         __syncthreads();
     }
@@ -701,6 +736,7 @@ BwdKParams make_params(const BwdArgs& a) {
     p.n_tiles = 0; p.n_hg = 0;
     p.scale = g.scale; p.scale_log2 = g.scale * kLog2e;
     p.causal = g.causal; p.window = g.window > 0 ? g.window : 0;
+    p.bias_b32 = g.bias != nullptr && (64 * g.bias_qs + g.bias_cols) * 4 < ((int64_t)1 << 32);
     p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0 &&
                 (g.bias_ss < 0 || g.bias_ss % 4 == 0);
     return p;
