@@ -486,6 +486,55 @@ def test_bias_staged_broadcast(mt):
         assert gerr < gtol, f"{name}: grad err {gerr}"
 
 
+def test_scale_modes(mt):
+    """Explicit scales (mtlattn/__init__.py:82-83 only defaults it): a custom
+    positive scale takes the raw-max softmax (with a bias, the biased raw max;
+    with a head-broadcast bias and GQA, the staged bias), zero and negative
+    scales the explicitly scaled one, on the prefill kernels forward and
+    backward and on the split-KV decode path."""
+    cases = [
+        # name, q_lens, kv_lens, Hq, Hkv, D, dtype, causal, scale, bias kind
+        ("scale 0.3 GQA causal", [300, 129], [300, 129], 8, 2, 128, torch.bfloat16, True, 0.3, None),
+        ("scale 0.3 broadcast bias (staged)", [300, 129], [300, 129], 8, 2, 128, torch.float16, True, 0.3, "bcast"),
+        ("scale -0.07 per-head bias", [200, 77], [200, 77], 4, 4, 64, torch.float16, False, -0.07, "head"),
+        ("scale -0.07 GQA causal", [250], [250], 8, 2, 128, torch.bfloat16, True, -0.07, None),
+        ("scale 0 broadcast bias", [150, 90], [150, 90], 8, 2, 128, torch.float16, True, 0.0, "bcast"),
+    ]
+    for name, ql, kl, hq, hkv, d, dt, causal, scale, bk in cases:
+        _banner(f"scale modes: {name}")
+        q, k, v = _inputs(ql, kl, hq, hkv, d, dt, seed=5)
+        cq, ck = cu_of(ql), cu_of(kl)
+        bias = None
+        if bk is not None:
+            bias = _make_bias(sum(ql), hq, max(kl), bk == "bcast", seed=9)
+        dout = randn((sum(ql), hq, d), dt, torch.Generator().manual_seed(12))
+        qm, km, vm = (t.cuda().requires_grad_() for t in (q, k, v))
+        out = mt.varlen_attention(qm, km, vm, cq.cuda(), ck.cuda(), max(ql), scale=scale, causal=causal,
+                                  attn_bias=None if bias is None else bias.cuda())
+        out.backward(dout.cuda())
+        torch.cuda.synchronize()
+        ro, _, rq, rk, rv = oracle.varlen_forward_backward(q, k, v, dout, cq, ck, scale, causal, 0, bias)
+        # the relative criterion (max|err| and RMS(err) against RMS(ref)):
+        # gradients grow with the scale, absolute tolerances do not
+        for nm, a, r in (("out", out, ro), ("dQ", qm.grad, rq), ("dK", km.grad, rk), ("dV", vm.grad, rv)):
+            st = err_stats(a, r, dt)
+            print(f"  {nm}: rel={st['rel']:.3e} rms_rel={st['rms_rel']:.3e} floor={st['floor']:.3e} "
+                  f"max_abs={st['max_abs']:.3e}", flush=True)
+            assert st["ok_elem"], f"{name}: {nm} out of tolerance {st}"
+    # split-KV decode with explicit scales (q_len 1, long KV: the split path)
+    for scale in (0.3, -0.05, 0.0):
+        _banner(f"scale modes: decode scale {scale}")
+        ql, kl = [1, 1, 1], [6000, 9000, 4100]
+        q, k, v = _inputs(ql, kl, 16, 2, 128, torch.bfloat16, seed=6)
+        cq, ck = cu_of(ql), cu_of(kl)
+        out = mt.varlen_attention(q.cuda(), k.cuda(), v.cuda(), cq.cuda(), ck.cuda(), 1, scale=scale,
+                                  causal=True).cpu()
+        ref, _ = oracle.varlen_forward(q, k, v, cq, ck, scale, True, 0, None)
+        err = (out.float() - ref).abs().max().item()
+        print(f"  max_err={err:.3e}", flush=True)
+        assert err < REF_ATOL[torch.bfloat16], f"decode scale {scale}: err {err}"
+
+
 # SDPA adapter, padding-mask packing, mask -> bias (tests/test_correctness.py:437-448)
 def test_sdpa_adapter(mt):
     for (B, Hq, Hkv, N, causal) in [(2, 8, 8, 1024, False), (1, 8, 2, 2048, False), (2, 12, 12, 512, True)]:
