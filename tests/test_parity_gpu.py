@@ -486,6 +486,49 @@ def test_bias_staged_broadcast(mt):
         assert gerr < gtol, f"{name}: grad err {gerr}"
 
 
+def test_empty_sequences(mt):
+    """Zero-length query and key sequences inside a batch (repeated
+    cu_seqlens entries), queries with no keys (O = 0, LSE = -inf, zero
+    gradients) and an empty batch, forward and backward on the matrix-core and
+    portable kernels."""
+    cases = [
+        ("bf16 D128 GQA non-causal", [0, 300, 5, 129, 0], [50, 300, 0, 129, 0], 8, 2, 128, torch.bfloat16, False),
+        ("fp16 D64 causal", [0, 200, 7, 64], [40, 200, 0, 64], 4, 4, 64, torch.float16, True),
+        ("fp32 D64 non-causal (portable)", [0, 30, 5, 12], [50, 30, 0, 12], 4, 2, 64, torch.float32, False),
+    ]
+    for name, ql, kl, hq, hkv, d, dt, causal in cases:
+        _banner(f"empty sequences: {name}")
+        q, k, v = _inputs(ql, kl, hq, hkv, d, dt, seed=8)
+        cq, ck = cu_of(ql), cu_of(kl)
+        dout = randn((sum(ql), hq, d), dt, torch.Generator().manual_seed(13))
+        qm, km, vm = (t.cuda().requires_grad_() for t in (q, k, v))
+        lse = torch.empty(sum(ql), hq, dtype=torch.float32, device="cuda")
+        o1 = mt._C.varlen_attention(q.cuda(), k.cuda(), v.cuda(), cq.cuda(), ck.cuda(), max(ql), 1 / math.sqrt(d),
+                                    causal, 0, lse, None)
+        out = mt.varlen_attention(qm, km, vm, cq.cuda(), ck.cuda(), max(ql), causal=causal)
+        out.backward(dout.cuda())
+        torch.cuda.synchronize()
+        ro, rl, rq, rk, rv = oracle.varlen_forward_backward(q, k, v, dout, cq, ck, None, causal, 0, None)
+        assert torch.equal(torch.isfinite(lse.cpu()), torch.isfinite(rl)), f"{name}: LSE -inf pattern"
+        for nm, a, r in (("out", out, ro), ("dQ", qm.grad, rq), ("dK", km.grad, rk), ("dV", vm.grad, rv)):
+            st = err_stats(a, r, dt)
+            print(f"  {nm}: rel={st['rel']:.3e} rms_rel={st['rms_rel']:.3e} max_abs={st['max_abs']:.3e}", flush=True)
+            assert torch.isfinite(a.float()).all(), f"{name}: non-finite {nm}"
+            assert st["ok_elem"] or st["max_abs"] < REF_ATOL[dt], f"{name}: {nm} {st}"
+        assert torch.equal(o1.cpu(), out.detach().cpu()), f"{name}: _C and public API disagree"
+        # keys no query sees (the empty-query sequence's 50 keys) get exactly zero gradient
+        assert km.grad[:kl[0]].abs().max().item() == 0.0 and vm.grad[:kl[0]].abs().max().item() == 0.0
+    _banner("empty sequences: empty batch")
+    q = torch.zeros((0, 8, 128), dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    k = torch.zeros((0, 2, 128), dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    v = torch.zeros((0, 2, 128), dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    cu = torch.zeros(3, dtype=torch.int32, device="cuda")
+    out = mt.varlen_attention(q, k, v, cu, cu, 0, causal=True)
+    out.backward(torch.zeros_like(out))
+    torch.cuda.synchronize()
+    assert out.shape == (0, 8, 128) and q.grad.shape == q.shape and k.grad.shape == k.shape
+
+
 def test_scale_modes(mt):
     """Explicit scales (mtlattn/__init__.py:82-83 only defaults it): a custom
     positive scale takes the raw-max softmax (with a bias, the biased raw max;
