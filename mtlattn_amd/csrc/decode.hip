@@ -13,6 +13,9 @@
 //     of bytes whatever the spread of KV lengths; the explicit num_splits entry
 //     cuts each sequence into that many equal parts instead. Waves never
 //     synchronise with each other, so a workgroup is just 4 independent waves.
+//     The kv head varies fastest over the wave index: the Hkv waves of one
+//     item start together and read whole K/V rows (all heads) between them,
+//     rather than one head's 2*D bytes of each row (1.6% faster at C5).
 //   * Per 32-key tile: K goes straight from HBM into MFMA A-operand registers
 //     (16 B per lane); V is loaded coalesced and transposed through a per-wave
 //     LDS buffer for the P.V product. The next tile's loads are issued before
@@ -113,10 +116,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
     char* vt = smem + w * (D * kDecKT * 2);
 
     int wid = blockIdx.x * kDecWaves + w;
-    const int slot = wid % p.n_slots; wid /= p.n_slots;
+    const int hk = wid % p.hkv; wid /= p.hkv;
     const int hgi = wid % p.n_hg;
-    const int hk = wid / p.n_hg;
-    if (hk >= p.hkv) return;
+    const int slot = wid / p.n_hg;
+    if (slot >= p.n_slots) return;
     int s, ks, ke;
     const bool has_keys = item_range(p, slot, s, ks, ke);
     // fixed chunks past a sequence's end are not read by the combine
