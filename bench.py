@@ -131,7 +131,9 @@ def bench_c3(args):
         state["o"] = C.varlen_attention(q, k, v, cu, cu, L, scale, True, 0, lse, None)
         state["g"] = C.varlen_attention_bwd(q, k, v, state["o"], do, lse, cu, cu, scale, True, 0, None)
 
-    # the same step as four C-ABI calls (one kernel each) on torch's stream
+    # the same step as four C-ABI calls (one kernel each) on torch's stream;
+    # the step proper runs dQ with delta fused in (no preprocess launch), the
+    # separate entries time the preprocess and a dQ that reads delta
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
     p = capi.problem_for(q, k, cu, cu, L, scale, causal=True)

@@ -2,7 +2,9 @@
 // and a dK/dV kernel (counterparts of the reference's bwd_dq_mpp /
 // bwd_dkv_mpp, src/attn_mpp.metal:546-799, and the delta reduction at
 // src/ext.mm:518). No atomics anywhere: every output element is written by
-// exactly one lane, so results are bitwise run-to-run deterministic.
+// exactly one lane, so results are bitwise run-to-run deterministic. At head
+// dims 64 and 128 the full backward has the dQ kernel compute delta itself
+// (bitwise equal to the preprocess) and hand it to the dK/dV kernel.
 //
 // Shared mathematics (src/attention.metal:707-717):
 //   P = exp(scale q.k + bias - lse), dP = dO.v, dS = P (dP - delta),
@@ -48,7 +50,20 @@ struct BwdKParams {
     int causal, window;
     int bias_v4;      // bias rows 16-byte aligned (pointer and strides)
     int bias_b32;     // 64 bias rows plus a row's columns span < 2^32 bytes (32-bit buffer offsets)
+    const uint16_t* o; int64_t o_rs;   // forward output (dQ with delta_w)
+    float* delta_w;   // non-null: the dQ kernel computes delta and writes it here
 };
+
+// Sum of the 8 products of one 16-byte chunk of O and dO. The preprocess and
+// the dQ kernel's fused delta both use it and combine chunks in the same tree,
+// so the two give bitwise equal deltas.
+template <typename T>
+__device__ inline float dot8(const u32x4_t a, const u32x4_t b) {
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc += lo16<T>(a[e]) * lo16<T>(b[e]) + hi16<T>(a[e]) * hi16<T>(b[e]);
+    return acc;
+}
 
 template <typename T, bool OUT_F32>
 __device__ inline void store4(void* base, int64_t off, float a, float b, float c, float d) {
@@ -135,10 +150,34 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         }
     }
     float lse2 = kPosInf, dlt = 0.f;
+    // fused delta (single launch over the whole head): this lane holds chunks
+    // 2 kc + hi (8 columns each) of its row, so the preprocess's butterfly
+    // over 16-column-group lanes (partners i ^ DC, ..., i ^ 1) becomes an
+    // in-register tree over kc followed by one exchange across hi.
+    constexpr bool kFuseDelta = C0 == 0 && DO == DV && DV == D && D <= 128;
+    bool fused = false;
+    if constexpr (kFuseDelta) {
+        if (p.delta_w != nullptr) {
+            fused = true;
+            const uint16_t* op = p.o + grow * p.o_rs + (int64_t)head * D + 8 * hi;
+            float cs[DC];
+#pragma unroll
+            for (int kc = 0; kc < DC; ++kc) cs[kc] = dot8<T>(ld16(op + 16 * kc), df[kc]);
+#pragma unroll
+            for (int off = DC / 2; off > 0; off >>= 1)
+#pragma unroll
+                for (int kc = 0; kc < off; ++kc) cs[kc] = cs[kc] + cs[kc + off];
+            const float dsum = cs[0] + __shfl_xor(cs[0], 32);
+            if (row_ok) {
+                dlt = dsum;
+                if (hi == 0) p.delta_w[grow * p.hq + head] = dsum;
+            }
+        }
+    }
     if (row_ok) {
         const float l = p.lse[grow * p.hq + head];
         lse2 = l == kNegInf ? kPosInf : l * kLog2e;   // empty rows: P = 0
-        dlt = p.delta[grow * p.hq + head];
+        if (!fused) dlt = p.delta[grow * p.hq + head];
     }
     // bias row of this lane's query (rows past the end read the last row);
     // columns at or past bias_cols read as 0
@@ -667,11 +706,7 @@ __global__ __launch_bounds__(256) void bwd_preprocess_row_kernel(const uint16_t*
     for (int c0 = 0; c0 < chunks; c0 += 64) {
         const int c = c0 + lane;
         float acc = 0.f;
-        if (c < chunks) {
-            const u32x4_t a = ld16(op + 8 * c), b = ld16(dp + 8 * c);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc += lo16<T>(a[e]) * lo16<T>(b[e]) + hi16<T>(a[e]) * hi16<T>(b[e]);
-        }
+        if (c < chunks) acc = dot8<T>(ld16(op + 8 * c), ld16(dp + 8 * c));
         for (int off = lpg >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
         if (c < chunks && (c % lpg) == 0) delta[row * hq + c / lpg] = acc;
     }
@@ -739,12 +774,16 @@ BwdKParams make_params(const BwdArgs& a) {
     p.bias_b32 = g.bias != nullptr && (64 * g.bias_qs + g.bias_cols) * 4 < ((int64_t)1 << 32);
     p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0 &&
                 (g.bias_ss < 0 || g.bias_ss % 4 == 0);
+    p.o = (const uint16_t*)a.o; p.o_rs = a.o_rs;
+    p.delta_w = a.delta_out;
     return p;
 }
 
 template <typename T, int D, int DV, int DO, int C0, int KB, bool OUT_F32>
 hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     constexpr int NW = kWaves;
+    // the fused delta needs the whole head in one launch
+    if (a.delta_out != nullptr && !(C0 == 0 && DO == DV && DV == D && D <= 128)) return hipErrorInvalidValue;
     BwdKParams p = make_params(a);
     p.hpw = gcd_int(a.geo.g, NW);
     const int QT = 32 * (NW / p.hpw);

@@ -410,7 +410,25 @@ int mtlattn_varlen_bwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
         return fail(MTLATTN_ERR_WORKSPACE, "mtlattn: backward workspace too small (%zu < %zu bytes)",
                     workspace_bytes, need);
     float* delta = (float*)workspace;
-    if (p->total_q > 0) {
+    // Head dims 64 and 128 on the matrix-core path: the dQ kernel computes
+    // delta from O and dO itself (bitwise equal to the preprocess) and leaves
+    // it in the workspace for dK/dV, which saves the preprocess's pass over dO.
+    const bool fuse_delta = p->total_q > 0 && (p->head_dim == 64 || p->head_dim == 128) &&
+                            bwd_mfma_ok(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout,
+                                        dout_row_stride) &&
+                            ((uintptr_t)out & 15u) == 0 && out_row_stride % 8 == 0;
+    if (fuse_delta) {
+        if (q == nullptr || out == nullptr || dout == nullptr || lse == nullptr || dq == nullptr ||
+            (p->total_kv > 0 && (k == nullptr || v == nullptr)))
+            return fail(MTLATTN_ERR_INVALID, "mtlattn: null pointer argument");
+        BwdArgs a = make_bwd(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride, lse, delta);
+        a.dq = dq;
+        a.o = out;
+        a.o_rs = out_row_stride;
+        a.delta_out = delta;
+        rc = launch_status(launch_bwd_dq_mfma(p->dtype, a, (hipStream_t)stream), "dQ");
+        if (rc != MTLATTN_OK) return rc;
+    } else if (p->total_q > 0) {
         rc = mtlattn_bwd_preprocess(p, out, out_row_stride, dout, dout_row_stride, delta, stream);
         if (rc != MTLATTN_OK) return rc;
         rc = mtlattn_bwd_dq(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride, lse,

@@ -43,6 +43,11 @@ struct BwdArgs {
     void* dk;                     // contiguous [total_kv, hkv, d]
     void* dv;
     int out_f32;                  // 1: dq/dk/dv are fp32, 0: input dtype
+    // dQ only: with delta_out set, the dQ kernel computes delta = rowsum(dO * O)
+    // itself from o (the forward's output) and writes it to delta_out for the
+    // dK/dV kernel, in place of the separate preprocess (head dims 64 and 128)
+    const void* o = nullptr; int64_t o_rs = 0;
+    float* delta_out = nullptr;
 };
 
 struct DecodeArgs {

@@ -15,6 +15,8 @@ from tests.helpers import LSE_TOL, cu_of, err_stats, randn
 
 pytestmark = pytest.mark.gpu
 
+_DT = {torch.float16: capi.DTYPE_F16, torch.bfloat16: capi.DTYPE_BF16}
+
 
 def _case(q_lens, kv_lens, Hq, Hkv, D, dtype, seed=0):
     g = torch.Generator().manual_seed(seed)
@@ -100,6 +102,67 @@ def test_capi_backward_kernels_fp32_out():
     assert torch.allclose(delta, od, rtol=1e-5, atol=1e-4)
     ro, _, rq, rk, rv = oracle.varlen_forward_backward(q, k, v, do, cq, ck, scale, True, 50)
     _check("capi-kern", [("dq", dq.cpu(), rq), ("dk", dk.cpu(), rk), ("dv", dv.cpu(), rv)], torch.bfloat16)
+
+
+@pytest.mark.parametrize("D,dtype,causal,window,bias", [
+    (128, torch.bfloat16, True, 0, False),
+    (64, torch.float16, False, 0, False),
+    (128, torch.float16, True, 40, True),
+    (64, torch.bfloat16, True, 0, True),
+])
+def test_capi_fused_delta_matches_separate_kernels(D, dtype, causal, window, bias):
+    """At head dims 64 and 128 mtlattn_varlen_bwd lets the dQ kernel compute
+    delta = rowsum(dO * O) itself and leave it in the workspace for dK/dV.
+    The delta, dQ, dK and dV it produces must be bitwise equal to those of the
+    separate mtlattn_bwd_preprocess + mtlattn_bwd_dq + mtlattn_bwd_dkv calls,
+    on ragged GQA input with an empty sequence and rows outside every sequence;
+    and the gradients must match the oracle."""
+    print(f"\n[case] capi fused delta D={D} {dtype} causal={causal} window={window} bias={bias}", flush=True)
+    q_lens, kv_lens, Hq, Hkv = [70, 0, 131, 1, 64], [90, 5, 131, 33, 64], 8, 2
+    q, k, v, do, cq, ck = _case(q_lens, kv_lens, Hq, Hkv, D, dtype, seed=11)
+    # 3 trailing rows in q/k/v that no sequence owns
+    g = torch.Generator().manual_seed(12)
+    q, do = (torch.cat([t, randn((3, Hq, D), dtype, g)]) for t in (q, do))
+    k, v = (torch.cat([t, randn((3, Hkv, D), dtype, g)]) for t in (k, v))
+    scale = 1.0 / math.sqrt(D)
+    bias_t = None
+    if bias:
+        bias_t = torch.randn(q.shape[0], 1, max(kv_lens), generator=g)
+    qd, kd, vd, dod, cqd, ckd = (t.cuda() for t in (q, k, v, do, cq, ck))
+    bd = bias_t.cuda() if bias else None
+    p = capi.problem_for(qd, kd, cqd, ckd, max(q_lens), scale, causal=causal, window=window, bias=bd)
+    out = torch.empty_like(qd)
+    lse = torch.empty(qd.shape[0], Hq, dtype=torch.float32, device="cuda")
+    s = _stream()
+    capi.call("mtlattn_varlen_fwd", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
+              out.data_ptr(), lse.data_ptr(), None, 0, s)
+    ws_n = capi.lib().mtlattn_varlen_bwd_workspace_size(p)
+    ws = torch.full((ws_n // 4,), float("nan"), dtype=torch.float32, device="cuda")
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    capi.call("mtlattn_varlen_bwd", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
+              out.data_ptr(), Hq * D, dod.data_ptr(), Hq * D, lse.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+              dv.data_ptr(), ws.data_ptr(), ws_n, s)
+    delta = torch.full((qd.shape[0], Hq), float("nan"), dtype=torch.float32, device="cuda")
+    capi.call("mtlattn_bwd_preprocess", p, out.data_ptr(), Hq * D, dod.data_ptr(), Hq * D, delta.data_ptr(), s)
+    dq2, dk2, dv2 = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    capi.call("mtlattn_bwd_dq", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
+              dod.data_ptr(), Hq * D, lse.data_ptr(), delta.data_ptr(), dq2.data_ptr(), _DT[dtype], s)
+    capi.call("mtlattn_bwd_dkv", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
+              dod.data_ptr(), Hq * D, lse.data_ptr(), delta.data_ptr(), dk2.data_ptr(), dv2.data_ptr(),
+              _DT[dtype], s)
+    torch.cuda.synchronize()
+    # every row a sequence owns: delta bitwise equal (rows outside are not read)
+    owned = int(cq[-1])
+    wsd = ws.view(-1, Hq)[:owned].cpu()
+    assert torch.equal(wsd, delta[:owned].cpu()), (wsd - delta[:owned].cpu()).abs().max()
+    for nm, a, b, n in (("dq", dq, dq2, owned), ("dk", dk, dk2, int(ck[-1])), ("dv", dv, dv2, int(ck[-1]))):
+        assert torch.equal(a[:n].cpu(), b[:n].cpu()), nm
+    assert not dq[owned:].any() and not dk[int(ck[-1]):].any() and not dv[int(ck[-1]):].any()
+    ro, _, rq, rk, rv = oracle.varlen_forward_backward(q[:owned], k[:int(ck[-1])], v[:int(ck[-1])], do[:owned],
+                                                       cq, ck, scale, causal, window,
+                                                       bias=bias_t[:owned] if bias else None)
+    _check("fused-delta", [("dq", dq[:owned].cpu(), rq), ("dk", dk[:int(ck[-1])].cpu(), rk),
+                           ("dv", dv[:int(ck[-1])].cpu(), rv)], dtype)
 
 
 def test_capi_splitkv_and_workspace_errors():
