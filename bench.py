@@ -4,8 +4,8 @@
 
 Headline (BASELINE.json metric): fwd+bwd TFLOP/s of causal GQA prefill,
 8 x 4096 tokens, Hq=32, Hkv=8, D=128, bf16 (config C3). One step = the forward
-with LSE plus the backward (delta preprocess, dQ, dK/dV) -- the work of one
-autograd step of the op, through the same `_C` calls autograd makes. FLOPs
+with LSE plus the backward (dQ with the delta row-dot fused in, dK/dV) -- the
+work of one autograd step of the op, through the same `_C` calls autograd makes. FLOPs
 count attended pairs only (the reference's convention, mtlattn/bench.py:25-32):
 fwd 4*D*Hq*pairs, bwd 2.5x that, fwd+bwd 14*D*Hq*pairs. Inputs are synthetic
 N(0,1) and resident in HBM before timing. The secondary line item is split-KV
