@@ -373,22 +373,39 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecKParams p, typen
         count = p.ns;
     }
     const int64_t base = (int64_t)(hk * p.n_hg + hgi) * p.n_slots;
+    // max LSE: lanes over items, then across the wave
     float m = kNegInf;
-    for (int i = 0; i < count; ++i) m = fmaxf(m, p.lse_part[(base + first + i) * 16 + n]);
+    for (int i = lane; i < count; i += 64) m = fmaxf(m, p.lse_part[(base + first + i) * 16 + n]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     float wsum = 0.f;
     if (m != kNegInf) {
-        for (int i = 0; i < count; ++i) {
-            const int64_t prow = (base + first + i) * 16 + n;
-            const float l = p.lse_part[prow];
-            if (l == kNegInf) continue;
-            const float wgt = __expf(l - m);
-            wsum += wgt;
-            const float* op = p.o_part + prow * d;
+        // items in groups of 4 whose loads all go out before the first use;
+        // the sums still run in item order
+        constexpr int U = 4;
+        for (int i0 = 0; i0 < count; i0 += U) {
+            float l[U], o[U][4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int dd = lane + 64 * j;
-                if (dd < d) acc[j] += wgt * op[dd];
+            for (int u = 0; u < U; ++u) {
+                const bool in = i0 + u < count;
+                const int64_t prow = (base + first + min(i0 + u, count - 1)) * 16 + n;
+                l[u] = in ? p.lse_part[prow] : kNegInf;
+                const float* op = p.o_part + prow * d;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int dd = lane + 64 * j;
+                    o[u][j] = dd < d ? op[dd] : 0.f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (l[u] == kNegInf) continue;
+                const float wgt = __expf(l[u] - m);
+                wsum += wgt;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (lane + 64 * j < d) acc[j] += wgt * o[u][j];
             }
         }
     }
