@@ -120,7 +120,11 @@ int mtlattn_varlen_fwd(const mtlattn_problem* p,
  * inside the kernels (no atomics; bitwise run-to-run deterministic).
  * Replaces _C.varlen_attention_bwd (src/ext.mm:502-594). The reference needs
  * contiguous inputs (mtlattn/__init__.py:42-45); this entry also takes row
- * strides. dq/dk/dv are written contiguous in the input dtype.
+ * strides. dq/dk/dv are written contiguous in the input dtype. The
+ * workspace (fp32 [total_q, Hq]) holds delta = rowsum(dO * O) of every row a
+ * sequence owns when the call returns; at head dims 64 and 128 the dQ kernel
+ * computes it (no separate preprocess launch), bitwise equal to
+ * mtlattn_bwd_preprocess.
  */
 size_t mtlattn_varlen_bwd_workspace_size(const mtlattn_problem* p);
 int mtlattn_varlen_bwd(const mtlattn_problem* p,
