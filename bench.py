@@ -51,7 +51,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1/C2/C4 lines")
-    ap.add_argument("--only", choices=["c3", "c5", "copy"], default=None,
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured-ceiling kernels")
+    ap.add_argument("--only", choices=["c3", "c5", "copy", "peaks"], default=None,
                     help="run one workload (or the 1 GiB copy used to calibrate HBM byte counters) "
                          "and print only its timing: the short program profilers wrap")
     return ap.parse_args()
@@ -156,9 +157,11 @@ def bench_c3(args):
                                      dv.data_ptr(), bf, sh),
     }
 
+    # --warmup steps, and at least 100 ms of steps so the clocks have ramped
+    # (as for the other configs)
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
+    warm(step, 100.0)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
@@ -286,6 +289,7 @@ def bench_c5(args):
 
     for _ in range(max(3, args.warmup)):
         run()
+    warm(run, 100.0)
     ms = avg_launch_ms(run, max(10, args.steps), torch.cuda.current_stream())
     nbytes = Mk * Hkv * D * 2 * 2 + B * Hq * D * 2 * 2
     out = run()
@@ -307,13 +311,188 @@ def copy_calibration(args):
     return n
 
 
+def measured_peaks():
+    """Ceilings of this GPU measured with the calibration kernels
+    (mtlattn_amd/csrc/calib.hip): sustained bf16 MFMA throughput of a
+    register-only v_mfma_f32_32x32x16 stream on every CU, and HBM read
+    bandwidth of a 4 GiB 16-byte-load stream; each after 100 ms of warm-up,
+    then 10 launches between HIP events. Also the shader clock of the first
+    wave during each (s_memtime cycles over s_memrealtime 100 MHz ticks)."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(os.path.join(ROOT, "mtlattn_amd", "libmtlattn_calib.so"))
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.mtlattn_calib_mfma.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, vp]
+    lib.mtlattn_calib_read.argtypes = [vp, i64, ctypes.c_int, vp, vp, vp]
+    stream = torch.cuda.current_stream()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    clk = torch.zeros(2, dtype=torch.int64, device="cuda")
+
+    def mhz():
+        c = clk.cpu().tolist()
+        return round(c[0] / (c[1] / 100.0), 1) if c[1] > 0 else None
+
+    blocks, iters = cus * 4, 2048
+    sink = torch.empty(blocks * 512, dtype=torch.float32, device="cuda")
+    run = lambda: lib.mtlattn_calib_mfma(blocks, iters, sink.data_ptr(), clk.data_ptr(), stream.cuda_stream)
+    warm(run, 100.0)
+    ms = avg_launch_ms(run, 10, stream)
+    mfma_tf = blocks * 8 * iters * 8 * 32768.0 / (ms * 1e-3) / 1e12
+    mfma_mhz = mhz()
+    nbytes = 4 << 30
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    rblocks = cus * 8
+    rsink = torch.empty(rblocks * 4, dtype=torch.int32, device="cuda")
+    run = lambda: lib.mtlattn_calib_read(buf.data_ptr(), nbytes, rblocks, rsink.data_ptr(), clk.data_ptr(),
+                                         stream.cuda_stream)
+    warm(run, 100.0)
+    ms_r = avg_launch_ms(run, 10, stream)
+    read_gbs = nbytes / (ms_r * 1e-3) / 1e9
+    read_mhz = mhz()
+    del buf
+    torch.cuda.empty_cache()
+    return {"mfma_bf16_tflops": round(mfma_tf, 1), "mfma_clock_mhz": mfma_mhz,
+            "hbm_read_gbs": round(read_gbs, 1), "read_clock_mhz": read_mhz, "cus": cus,
+            "how": "calib.hip: register-only v_mfma_f32_32x32x16_bf16 stream (4 chains, 8 waves per CU-block, "
+                   f"{blocks} blocks) and a 4 GiB read stream (16-byte nontemporal loads, {rblocks} blocks "
+                   "of contiguous spans); "
+                   "HIP events over 10 launches after 100 ms warm-up"}
+
+
+def host_cpu():
+    """Model, sockets and physical cores of the host (from /proc/cpuinfo),
+    the CPUs this process may run on, and the torch thread count used: the
+    OMP_NUM_THREADS the GPU host sets (its CPU share for one GPU), else the
+    CPUs available, at most 16."""
+    info = {"model": platform.processor() or platform.machine(), "sockets": None, "physical_cores": None}
+    try:
+        with open("/proc/cpuinfo") as f:
+            blocks = f.read().split("\n\n")
+        phys, cores = set(), {}
+        for b in blocks:
+            kv = dict(l.split(":", 1) for l in b.splitlines() if ":" in l)
+            kv = {k.strip(): v.strip() for k, v in kv.items()}
+            if "model name" in kv:
+                info["model"] = kv["model name"]
+            if "physical id" in kv:
+                phys.add(kv["physical id"])
+                if "core id" in kv:
+                    cores.setdefault(kv["physical id"], set()).add(kv["core id"])
+        if phys:
+            info["sockets"] = len(phys)
+            info["physical_cores"] = sum(len(c) for c in cores.values()) or None
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    info["logical_cpus"] = os.cpu_count()
+    info["cpus_available"] = avail
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    info["threads"] = min(int(omp), avail) if omp.isdigit() and int(omp) > 0 else min(16, avail)
+    info["threads_from"] = "OMP_NUM_THREADS" if omp.isdigit() and int(omp) > 0 else "min(16, cpus available)"
+    return info
+
+
+def cpu_baseline_others(seed, threads, budget_s=3.0):
+    """The oracle on bounded samples of C1 (whole), C2 (sequences until the
+    budget), C4 (query blocks of one sequence until the budget) and C5
+    (forward of sequences until the budget), each reported in its metric's
+    unit: TFLOP/s of attended-pair FLOPs, or GB/s of C5's algorithmic bytes."""
+    import torch
+    import oracle
+    torch.set_num_threads(threads)
+    out = {}
+    g = torch.Generator().manual_seed(seed + 7)
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    # C1: fp32 fwd+bwd, whole config
+    lens = [17, 64, 129, 250]
+    T = sum(lens)
+    q, k, v, do = (torch.randn(T, 4, 64, generator=g) for _ in range(4))
+    cu = torch.tensor([0, 17, 81, 210, 460], dtype=torch.int32)
+    dt = timed(lambda: oracle.varlen_forward_backward(q, k, v, do, cu, cu))
+    pairs = sum(L * L for L in lens)
+    out["C1"] = {"value": round(14.0 * 64 * 4 * pairs / dt / 1e12, 5), "unit": "TFLOP/s",
+                 "sample": f"whole config, fp32 fwd+bwd, {dt:.2f} s"}
+    # C2: bf16 inputs, ragged non-causal D=64, sequences until the budget
+    gl = torch.Generator().manual_seed(seed)
+    c2 = torch.randint(256, 4097, (32,), generator=gl).tolist()
+    T = sum(c2)
+    q, k, v, do = (torch.randn(T, 16, 64, generator=g).to(torch.bfloat16) for _ in range(4))
+    cu = torch.tensor([0] + torch.tensor(c2).cumsum(0).tolist(), dtype=torch.int32)
+    done, t0 = [], time.perf_counter()
+    for s in range(32):
+        oracle.varlen_forward_backward_blocked(q, k, v, do, cu, cu, seqs=[s], q_block=1024)
+        done.append(s)
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    pairs = sum(c2[s] ** 2 for s in done)
+    out["C2"] = {"value": round(14.0 * 64 * 16 * pairs / dt / 1e12, 5), "unit": "TFLOP/s",
+                 "sample": f"{len(done)} of 32 sequences fwd+bwd, {dt:.2f} s"}
+    del q, k, v, do
+    # C4: one sequence of 16384, window 4096, fp32 bias -(i-j)/16, query
+    # blocks of 1024 from the start until the budget
+    L, W, D = 16384, 4096, 128
+    q = torch.randn(L, 32, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(L, 8, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(L, 8, D, generator=g).to(torch.bfloat16)
+    do = torch.randn(L, 32, D, generator=g).to(torch.bfloat16)
+    i = torch.arange(L)[:, None]
+    rows, t0, pairs = 0, time.perf_counter(), 0
+    while rows < L:
+        n = min(1024, L - rows)
+        cq = torch.tensor([0, n], dtype=torch.int32)
+        kv0 = max(0, rows - W + 1)
+        ck = torch.tensor([0, rows + n - kv0], dtype=torch.int32)
+        qi = i[rows:rows + n]
+        j = torch.arange(kv0, rows + n)[None, :]
+        b = torch.where(j <= qi, -(qi - j).float() / 16.0, torch.zeros(())).unsqueeze(1)
+        oracle.varlen_forward_backward_blocked(q[rows:rows + n], k[kv0:rows + n], v[kv0:rows + n], do[rows:rows + n],
+                                               cq, ck, 1 / math.sqrt(D), True, W, b, q_block=1024)
+        pairs += sum(min(r + 1, W) for r in range(rows, rows + n))
+        rows += n
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    out["C4"] = {"value": round(14.0 * D * 32 * pairs / dt / 1e12, 5), "unit": "TFLOP/s",
+                 "sample": f"first {rows} of 65536 query rows (sequence 0, its key band and bias), fwd+bwd, "
+                           f"{dt:.2f} s"}
+    del q, k, v, do
+    # C5: decode forward, sequences until the budget (oracle time only)
+    kv_lens = c5_inputs(seed)
+    dt, done_kv, n = 0.0, 0, 0
+    for L in kv_lens:
+        q = torch.randn(1, 64, D, generator=g).to(torch.bfloat16)
+        k = torch.randn(L, 8, D, generator=g).to(torch.bfloat16)
+        v = torch.randn(L, 8, D, generator=g).to(torch.bfloat16)
+        cq, ck = torch.tensor([0, 1], dtype=torch.int32), torch.tensor([0, L], dtype=torch.int32)
+        dt += timed(lambda: oracle.varlen_forward_backward_blocked(q, k, v, None, cq, ck, 1 / math.sqrt(D), True,
+                                                                   backward=False, q_block=1))
+        done_kv += L
+        n += 1
+        if dt >= budget_s:
+            break
+    nbytes = done_kv * 8 * D * 2 * 2 + n * 64 * D * 2 * 2
+    out["C5"] = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s",
+                 "sample": f"{n} of 64 sequences (sum kv {done_kv}), forward, {dt:.2f} s"}
+    return out
+
+
 def cpu_baseline(seed, budget_s=12.0):
     """The oracle (torch CPU fp32, explicit fwd+bwd formulas) on C3, one
     sequence (all 8 kv heads, 32 query heads) at a time until `budget_s` of
     CPU time is spent: a bounded sample of the same workload."""
     import torch
     import oracle
-    threads = min(16, os.cpu_count() or 1)
+    host = host_cpu()
+    threads = host["threads"]
     torch.set_num_threads(threads)
     B, L, Hq, Hkv, D = (C3[x] for x in ("B", "L", "Hq", "Hkv", "D"))
     q, k, v, do, cu = c3_inputs(seed)
@@ -327,16 +506,11 @@ def cpu_baseline(seed, budget_s=12.0):
     dt = time.perf_counter() - t0
     sample_pairs = L * (L + 1) // 2 * done
     flops = 14.0 * D * Hq * sample_pairs
-    cpu = platform.processor() or platform.machine()
-    try:
-        with open("/proc/cpuinfo") as f:
-            cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
-    except (OSError, StopIteration):
-        pass
     return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"C3 fwd+bwd, {done} of {B} sequences (all 32 query heads), "
                       f"{sample_pairs * Hq} attended pairs, {dt:.1f} s; oracle "
-                      f"varlen_forward_backward_blocked fp32, torch {threads} threads on {cpu}"}
+                      f"varlen_forward_backward_blocked fp32, torch {threads} threads",
+            "host": host, "other_configs": cpu_baseline_others(seed, threads)}
 
 
 def load_traffic(kernel):
@@ -371,9 +545,13 @@ def main():
         dec = bench_c5(args)
         print(json.dumps({"c5_ms": dec["ms"], "GBps": dec["GBps"]}), flush=True)
         return
+    if args.only == "peaks":
+        print(json.dumps(measured_peaks()), flush=True)
+        return
     c3 = bench_c3(args)
     dec = None if args.no_decode else bench_c5(args)
     others = None if args.no_configs else bench_configs(args)
+    peaks = None if args.no_peaks else measured_peaks()
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.seed)
     km, algo = c3["kern_ms"], c3["algo_flop"]
     dom = max(km, key=km.get)
@@ -396,7 +574,13 @@ def main():
                    "flop_per_step": c3["flops"]},
         "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": load_traffic(dom), "kernel": dom,
-                     "kernel_ms": round(km[dom], 4), "algorithmic_flop": algo[dom]},
+                     "kernel_ms": round(km[dom], 4), "algorithmic_flop": algo[dom],
+                     "peak_measured": None if peaks is None else peaks["mfma_bf16_tflops"],
+                     "frac_measured": None if peaks is None else round(ach / peaks["mfma_bf16_tflops"], 4),
+                     "step_frac": round(c3["tflops"] / PEAK_BF16_TFLOPS, 4),
+                     "step_frac_measured": None if peaks is None else round(c3["tflops"] / peaks["mfma_bf16_tflops"],
+                                                                             4)},
+        "measured_peaks": peaks,
         "kernels": {n: {"ms": round(t, 4),
                         "tflops": round(algo[n] / (t * 1e-3) / 1e12, 2) if algo[n] else None}
                     for n, t in km.items()},
@@ -404,7 +588,9 @@ def main():
             "workload": C5_WORKLOAD,
             "ms": round(dec["ms"], 4), "GBps": round(dec["GBps"], 1), "bytes": dec["bytes"],
             "roofline": {"bound": "hbm", "achieved": round(dec["GBps"], 1), "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": round(dec["GBps"] / PEAK_HBM_GBS, 4)},
+                         "unit": "GB/s", "frac": round(dec["GBps"] / PEAK_HBM_GBS, 4),
+                         "peak_measured": None if peaks is None else peaks["hbm_read_gbs"],
+                         "frac_measured": None if peaks is None else round(dec["GBps"] / peaks["hbm_read_gbs"], 4)},
             "outputs_finite": dec["finite"]},
         "other_configs": others,
         "outputs_finite": c3["finite"],

@@ -202,12 +202,18 @@ int mtlattn_attn_splitkv(const mtlattn_problem* p,
  *   k_cache / v_cache : [num_pages, page_size, Hkv, D], token row strides
  *                       k_row_stride / v_row_stride (elements); a page is
  *                       page_size consecutive token rows
- *   block_table       : int32 [num_seqs, block_table_stride] on the device;
- *                       logical key j of sequence s is row j % page_size of
- *                       page block_table[s * block_table_stride + j / page_size]
- *                       (page indices are clamped to [0, num_pages))
+ *   block_table       : int32 [num_seqs, block_table_stride] on the device
+ *                       (block_table_stride entries per sequence, all of
+ *                       them readable); logical key j of sequence s is row
+ *                       j % page_size of page
+ *                       block_table[s * block_table_stride + min(j / page_size,
+ *                       block_table_stride - 1)] (page indices are clamped
+ *                       to [0, num_pages)), so the table needs
+ *                       ceil(kv_len / page_size) entries per sequence
  *   p->cu_seqlens_kv  : logical KV lengths (prefix sums); p->total_kv is an
- *                       upper bound on cu_seqlens_kv[num_seqs]
+ *                       upper bound on cu_seqlens_kv[num_seqs], the sum of
+ *                       the logical lengths (pages may be shared between
+ *                       sequences, so it can exceed the cache capacity)
  *   page_size         : a multiple of 16
  *   max_seqlen_kv     : bound on the logical KV lengths (sizes the window
  *                       splits)

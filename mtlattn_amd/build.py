@@ -7,7 +7,9 @@ Produces, next to this file:
                            by hipcc from csrc/*.hip for --offload-arch=gfx950;
   * _C<EXT_SUFFIX>      -- the pybind11 torch extension (csrc/torch_ext.cpp),
                            built by g++ against torch's headers and linked to
-                           libmtlattn_hip.so through an $ORIGIN rpath.
+                           libmtlattn_hip.so through an $ORIGIN rpath;
+  * libmtlattn_calib.so -- measured-ceiling kernels (csrc/calib.hip) that
+                           bench.py divides by; not part of the C ABI.
 Object files go to _build/ (git-ignored). Always recompiles.
 """
 
@@ -23,6 +25,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmtlattn_hip.so")
 EXT = os.path.join(HERE, "_C" + sysconfig.get_config_var("EXT_SUFFIX"))
+CALIB = os.path.join(HERE, "libmtlattn_calib.so")
 HIP_SOURCES = ["fwd.hip", "bwd.hip", "decode.hip", "generic.hip", "pad.hip", "capi.hip"]
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
@@ -83,10 +86,18 @@ def build_ext(verbose=False):
     return EXT
 
 
+def build_calib(verbose=False):
+    tmp = CALIB + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "calib.hip"), "-o", tmp], verbose)
+    os.replace(tmp, CALIB)
+    return CALIB
+
+
 def build(verbose=False):
     build_lib(verbose)
     build_ext(verbose)
-    return LIB, EXT
+    build_calib(verbose)
+    return LIB, EXT, CALIB
 
 
 if __name__ == "__main__":

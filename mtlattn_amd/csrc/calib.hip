@@ -1,0 +1,106 @@
+// Measured ceilings of the GPU this runs on, for bench.py's fractions of
+// roofline (libmtlattn_calib.so; not part of the attention library's ABI).
+//
+//  * mtlattn_calib_mfma: sustained v_mfma_f32_32x32x16_bf16 throughput. Every
+//    wave streams `iters` x 8 MFMAs over four independent accumulator chains
+//    (operands in registers, no memory traffic in the loop) -- the matrix-core
+//    rate the attention kernels' own instruction stream could at best reach
+//    at the clock the GPU holds under such load. One block of 8 waves per
+//    `blocks`; use a multiple of the CU count.
+//  * mtlattn_calib_read: HBM read bandwidth. Each block streams a contiguous
+//    span of `bytes` / blocks with 16-byte nontemporal loads, folded into one
+//    word per lane and written once per block, so the only traffic is the
+//    stream itself.
+//
+// Both report shader-clock cycles and reference-clock ticks of the first wave
+// (s_memtime / s_memrealtime, the latter at 100 MHz) so the caller can derive
+// the shader clock during the run.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(512, 1) void calib_mfma_kernel(int iters, float* sink, unsigned long long* clk) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const u32x4_t a = {0x3f803f80u ^ (uint32_t)lane, 0x3f803f80u, 0x3c003c00u, 0x3f803f80u ^ (uint32_t)w};
+    const u32x4_t b = {0x3c003c00u, 0x3f803f80u ^ (uint32_t)lane, 0x3f803f80u, 0x3c003c00u};
+    const bf16x8_t A = __builtin_bit_cast(bf16x8_t, a), B = __builtin_bit_cast(bf16x8_t, b);
+    f32x16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    unsigned long long t0 = 0, r0 = 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        t0 = __builtin_amdgcn_s_memtime();
+        r0 = __builtin_amdgcn_s_memrealtime();
+    }
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, c3, 0, 0, 0);
+        }
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += c0[r] + c1[r] + c2[r] + c3[r];
+    if (s == 1.2345f) sink[blockIdx.x * 512 + threadIdx.x] = s;   // keeps the chains live
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        clk[0] = __builtin_amdgcn_s_memtime() - t0;
+        clk[1] = __builtin_amdgcn_s_memrealtime() - r0;
+    }
+}
+
+// Each block streams one contiguous span; every lane keeps eight 16-byte
+// nontemporal loads in flight (each wave instruction covers 1 KB).
+constexpr int kReadUnroll = 8;
+__global__ __launch_bounds__(256) void calib_read_kernel(const u32x4_t* __restrict__ src, int64_t per_block,
+                                                         uint32_t* __restrict__ sink, unsigned long long* clk) {
+    unsigned long long t0 = 0, r0 = 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        t0 = __builtin_amdgcn_s_memtime();
+        r0 = __builtin_amdgcn_s_memrealtime();
+    }
+    const u32x4_t* p = src + (int64_t)blockIdx.x * per_block + threadIdx.x;
+    uint32_t acc = 0;
+    for (int64_t i = 0; i < per_block; i += kReadUnroll * 256) {
+        u32x4_t x[kReadUnroll];
+#pragma unroll
+        for (int j = 0; j < kReadUnroll; ++j) x[j] = __builtin_nontemporal_load(p + i + j * 256);
+#pragma unroll
+        for (int j = 0; j < kReadUnroll; ++j) acc ^= x[j][0] ^ x[j][1] ^ x[j][2] ^ x[j][3];
+    }
+    for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
+    if ((threadIdx.x & 63) == 0) sink[blockIdx.x * 4 + (threadIdx.x >> 6)] = acc;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        clk[0] = __builtin_amdgcn_s_memtime() - t0;
+        clk[1] = __builtin_amdgcn_s_memrealtime() - r0;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+// blocks x 8 waves x iters x 8 MFMAs of 32x32x16 (32768 FLOP each).
+// sink: blocks * 512 floats; clk: 2 u64. Returns a hipError_t code.
+int mtlattn_calib_mfma(int blocks, int iters, float* sink, unsigned long long* clk, void* stream) {
+    if (blocks < 1 || iters < 1) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(calib_mfma_kernel, dim3(blocks), dim3(512), 0, (hipStream_t)stream, iters, sink, clk);
+    return (int)hipGetLastError();
+}
+
+// Reads `bytes` (a multiple of blocks * 32 KiB) from src. sink: blocks * 4 words.
+int mtlattn_calib_read(const void* src, int64_t bytes, int blocks, uint32_t* sink, unsigned long long* clk,
+                       void* stream) {
+    const int64_t span = (int64_t)kReadUnroll * 256 * 16;
+    if (blocks < 1 || bytes < span || bytes % (span * blocks) != 0) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(calib_read_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const u32x4_t*)src, bytes / 16 / blocks, sink, clk);
+    return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -151,9 +151,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
     const uint16_t* kbase = p.k + (PAGED ? 0 : (int64_t)kr.start * p.k_rs) + (int64_t)hk * D;
     const uint16_t* vbase = p.v + (PAGED ? 0 : (int64_t)kr.start * p.v_rs) + (int64_t)hk * D;
     const int* bt = PAGED ? p.block_table + (int64_t)s * p.bt_stride : nullptr;
-    // cache row of logical key `key` (wave-uniform), page index clamped
+    // cache row of logical key `key` (wave-uniform): the table column is
+    // clamped to the row's bt_stride entries and the page index to the cache
     auto page_row = [&](int key) -> int64_t {
-        const int pg = min(max(bt[key / p.page_size], 0), p.num_pages - 1);
+        const int col = min(key / p.page_size, (int)min(p.bt_stride, (int64_t)0x7fffffff) - 1);
+        const int pg = min(max(bt[col], 0), p.num_pages - 1);
         return (int64_t)pg * p.page_size + key % p.page_size;
     };
 

@@ -62,6 +62,13 @@ void check_cu(const at::Tensor& cu_q, const at::Tensor& cu_kv, const at::Tensor&
                 "mtlattn: cu_seqlens_q/kv must both be [B+1]");
 }
 
+// lse / delta of the backward test entries: [total_q, Hq] on q's device.
+void check_rowhead(const at::Tensor& t, const at::Tensor& q, const char* name) {
+    TORCH_CHECK(t.is_cuda() && t.get_device() == q.get_device() && t.dim() == 2 && t.size(0) == q.size(0) &&
+                    t.size(1) == q.size(1),
+                "mtlattn: ", name, " must be a [total_q, H] GPU tensor");
+}
+
 int64_t row_stride(const at::Tensor& t) { return t.size(0) > 1 ? t.stride(0) : t.size(1) * t.size(2); }
 
 // Bias checks of src/ext.mm:348-365, plus the key-dim extent for bounds.
@@ -249,7 +256,12 @@ at::Tensor paged_decode(const at::Tensor& q, const at::Tensor& k_cache, const at
                 "mtlattn: block_table must be an int32 [B, max_pages] GPU tensor");
     const c10::OptionalDeviceGuard guard(q.device());
     auto cu_q = cu_seqlens_q.contiguous(), cu_kv = cu_seqlens_kv.contiguous();
-    auto bt = block_table.stride(1) == 1 ? block_table : block_table.contiguous();
+    TORCH_CHECK(max_seqlen_kv >= 0 && block_table.size(1) * page_size >= max_seqlen_kv,
+                "mtlattn: block_table has ", block_table.size(1), " pages of ", page_size,
+                " tokens per sequence, fewer than max_seqlen_kv (", max_seqlen_kv, ")");
+    // one row of block_table.size(1) entries per sequence (the kernel clamps
+    // its column reads to the row stride, so the rows must be dense)
+    auto bt = block_table.contiguous();
     auto out = at::empty({q.size(0), q.size(1), q.size(2)}, q.options());
     float* lse = nullptr;
     if (defined(lse_out)) {
@@ -265,10 +277,10 @@ at::Tensor paged_decode(const at::Tensor& q, const at::Tensor& k_cache, const at
     p.dtype = dtype_code(q.scalar_type());
     p.num_seqs = (int32_t)(cu_q.numel() - 1);
     p.total_q = q.size(0);
-    // an upper bound on the logical KV total (cu_seqlens_kv[B]): the cache's
-    // capacity or B * max_seqlen_kv, whichever is smaller
-    p.total_kv = std::min<int64_t>({(int64_t)p.num_seqs * std::max<int64_t>(max_seqlen_kv, 0),
-                                    k_cache.size(0) * page_size, 0x7fffffff});
+    // an upper bound on the logical KV total (cu_seqlens_kv[B]) from the
+    // logical lengths alone: sequences may share pages (prefix caching, beam
+    // search), so the sum can exceed the cache's capacity
+    p.total_kv = std::min<int64_t>((int64_t)p.num_seqs * std::max<int64_t>(max_seqlen_kv, 0), 0x7fffffff);
     p.num_heads_q = (int32_t)q.size(1);
     p.num_heads_kv = (int32_t)Hkv;
     p.head_dim = (int32_t)D;
@@ -301,6 +313,8 @@ at::Tensor mpp_bwd_dq(const at::Tensor& q, const at::Tensor& k, const at::Tensor
     const c10::OptionalDeviceGuard guard(q.device());
     auto cu_q = cu_q_in.contiguous(), cu_kv = cu_kv_in.contiguous();
     auto dOc = dO.contiguous();
+    check_rowhead(lse, q, "lse");
+    check_rowhead(delta, q, "delta");
     auto lsec = lse.to(at::kFloat).contiguous(), deltac = delta.to(at::kFloat).contiguous();
     auto dQ = at::zeros({q.size(0), q.size(1), q.size(2)}, q.options().dtype(at::kFloat));
     mtlattn_problem p = make_problem(q, k, cu_q, cu_kv, max_seqlen_q, scale, causal, window);
@@ -325,6 +339,8 @@ std::tuple<at::Tensor, at::Tensor> mpp_bwd_dkv(const at::Tensor& q, const at::Te
     const c10::OptionalDeviceGuard guard(q.device());
     auto cu_q = cu_q_in.contiguous(), cu_kv = cu_kv_in.contiguous();
     auto dOc = dO.contiguous();
+    check_rowhead(lse, q, "lse");
+    check_rowhead(delta, q, "delta");
     auto lsec = lse.to(at::kFloat).contiguous(), deltac = delta.to(at::kFloat).contiguous();
     auto dK = at::zeros({k.size(0), k.size(1), k.size(2)}, k.options().dtype(at::kFloat));
     auto dV = at::zeros_like(dK);

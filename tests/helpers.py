@@ -11,7 +11,9 @@ Two criteria are used:
     (the "floor", e.g. ~0.1 for causal 4096-token rows). The kernels, like the
     reference's, also round P and dS to the input type before the second
     products, a second rounding of the same size. For fp16/bf16 the asserted
-    criterion is therefore: RMS(err) / RMS(ref) <= tol, and
+    criterion is therefore: RMS(err) / RMS(ref) <= RMS_BOUND (about twice
+    the largest RMS(err) / RMS(ref) the GPU suite shows: 3.8e-3 bf16,
+    4.9e-4 fp16, so a 3x regression of the worst case fails), and
     max|err| / RMS(ref) <= 2 * floor + tol; both the literal metric and the
     floor are reported from the same run.
 
@@ -28,6 +30,8 @@ import math
 import torch
 
 TOL_RMS = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+# RMS(err) / RMS(ref) bound of the 16-bit criterion (module doc)
+RMS_BOUND = {torch.float16: 1e-3, torch.bfloat16: 8e-3}
 REF_ATOL = {torch.float32: 1e-4, torch.float16: 5e-3, torch.bfloat16: 3e-2}
 # LSE (natural log) absolute bound. The 16-bit kernels sum P after rounding it
 # to the input type (the values the P.V product consumes); each term carries a
@@ -71,6 +75,6 @@ def err_stats(out, ref, dtype, floor32=0.0):
     if dtype == torch.float32:
         ok = rel <= tol + 2.0 * floor32
     else:
-        ok = rms_rel <= tol and rel <= 2.0 * floor + tol
+        ok = rms_rel <= RMS_BOUND[dtype] and rel <= 2.0 * floor + tol
     ok = ok and bool(torch.isfinite(o).all()) and bool(torch.equal(torch.isfinite(out), finite))
     return {"max_abs": max_abs, "rms_ref": rms, "rel": rel, "rms_rel": rms_rel, "floor": floor, "ok_elem": ok}

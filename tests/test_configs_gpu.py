@@ -100,9 +100,23 @@ def test_c3_causal_gqa_bf16():
                    ("dv", err_stats(sel_k(dv), sel_k(rv), torch.bfloat16))])
 
 
+class _SeqLocalRows:
+    """A [L, H, K] per-sequence mask addressed by global query row (the
+    oracle slices bias[global rows, :, keys]): global row r reads row r % L.
+    Slices never cross a sequence, since the oracle works per sequence."""
+
+    def __init__(self, blk, L):
+        self.blk, self.L = blk, L
+
+    def __getitem__(self, idx):
+        r, *rest = idx
+        s0 = (r.start // self.L) * self.L
+        return self.blk[(slice(r.start - s0, r.stop - s0),) + tuple(rest)]
+
+
 def test_c4_swa_bias_bf16():
     print("\n[case] C4 bf16 4x16384 Hq=32 Hkv=8 D=128 causal W=4096 ALiBi-like bias fwd+bwd "
-          "(seq 0 x kv head 0 checked)", flush=True)
+          "(seqs 0,3 x kv heads 0,7 checked)", flush=True)
     B, L, Hq, Hkv, D, W = 4, 16384, 32, 8, 128, 4096
     g = torch.Generator().manual_seed(0)
     M = B * L
@@ -118,18 +132,62 @@ def test_c4_swa_bias_bf16():
     del i, j
     o, dq, dk, dv = _run_gpu(q, k, v, do, cu, cu, L, True, W, bias)
     del bias
-    bcpu = blk.unsqueeze(1).cpu()                       # rows of sequence 0 only
+    bcpu = _SeqLocalRows(blk.unsqueeze(1).cpu(), L)     # every sequence's rows hold the same block
     del blk
+    # sequence 3's bias rows sit at byte offsets 3.2-4.29 GB of the mask
+    seqs, heads = [0, 3], [0, 7]
     ro, _, rq, rk, rv = oracle.varlen_forward_backward_blocked(q, k, v, do, cu, cu, 1 / math.sqrt(D), True, W,
-                                                               bcpu, seqs=[0], heads=[0], q_block=1024)
-    qh, kh = torch.arange(4), torch.tensor([0])
-    rows = torch.arange(L)
+                                                               bcpu, seqs=seqs, heads=heads, q_block=1024)
+    rows = torch.cat([torch.arange(s * L, (s + 1) * L) for s in seqs])
+    qh = torch.tensor([h * 4 + j for h in heads for j in range(4)])
+    kh = torch.tensor(heads)
     sel_q = lambda t: t[rows][:, qh]
     sel_k = lambda t: t[rows][:, kh]
     _report("C4", [("out", err_stats(sel_q(o), sel_q(ro), torch.bfloat16)),
                    ("dq", err_stats(sel_q(dq), sel_q(rq), torch.bfloat16)),
                    ("dk", err_stats(sel_k(dk), sel_k(rk), torch.bfloat16)),
                    ("dv", err_stats(sel_k(dv), sel_k(rv), torch.bfloat16))])
+
+
+def test_bias_rows_past_4gib():
+    """C4's sliding-window bias path with every sequence's rows distinct and
+    the mask's last rows past byte 2^32: bias rows of 17408 floats (16384
+    used, the padding NaN, so a read past bias_kv_cols shows), sequence s
+    with slope (s + 1) / 16. Sequence 3 (rows at bytes 3.4-4.56 GB) is checked
+    fwd+bwd, so a row base computed in 32 bits or from the wrong sequence
+    fails."""
+    print("\n[case] 4x16384 Hq=8 Hkv=2 D=128 causal W=4096, 4.56 GB bias with per-sequence slopes "
+          "(seq 3 checked)", flush=True)
+    B, L, Hq, Hkv, D, W, PAD = 4, 16384, 8, 2, 128, 4096, 17408
+    g = torch.Generator().manual_seed(3)
+    M = B * L
+    q = _gen((M, Hq, D), g, torch.bfloat16)
+    k = _gen((M, Hkv, D), g, torch.bfloat16)
+    v = _gen((M, Hkv, D), g, torch.bfloat16)
+    do = _gen((M, Hq, D), g, torch.bfloat16)
+    cu = cu_of([L] * B)
+    store = torch.full((M, 1, PAD), float("nan"), device="cuda")
+    i = torch.arange(L, device="cuda")[:, None]
+    j = torch.arange(L, device="cuda")[None, :]
+    for s in range(B):
+        store[s * L:(s + 1) * L, 0, :L] = torch.where(j <= i, -(i - j).float() * ((s + 1) / 16.0),
+                                                        torch.zeros((), device="cuda"))
+    del i, j
+    bias = store[:, :, :L]
+    assert bias.stride(0) == PAD and (M - 1) * PAD * 4 > 2 ** 32
+    o, dq, dk, dv = _run_gpu(q, k, v, do, cu, cu, L, True, W, bias)
+    bcpu = _SeqLocalRows(store[3 * L:, :, :L].cpu(), L)   # sequence 3's rows
+    del bias, store
+    ro, _, rq, rk, rv = oracle.varlen_forward_backward_blocked(q, k, v, do, cu, cu, 1 / math.sqrt(D), True, W,
+                                                               bcpu, seqs=[3], heads=[1], q_block=1024)
+    rows = torch.arange(3 * L, 4 * L)
+    qh, kh = torch.arange(4, 8), torch.tensor([1])
+    sel_q = lambda t: t[rows][:, qh]
+    sel_k = lambda t: t[rows][:, kh]
+    _report("bias>4GiB", [("out", err_stats(sel_q(o), sel_q(ro), torch.bfloat16)),
+                          ("dq", err_stats(sel_q(dq), sel_q(rq), torch.bfloat16)),
+                          ("dk", err_stats(sel_k(dk), sel_k(rk), torch.bfloat16)),
+                          ("dv", err_stats(sel_k(dv), sel_k(rv), torch.bfloat16))])
 
 
 def test_c5_split_kv_decode_bf16():
