@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1/C2/C4 lines")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured-ceiling kernels")
-    ap.add_argument("--only", choices=["c3", "c5", "copy", "peaks"], default=None,
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "peaks"], default=None,
                     help="run one workload (or the 1 GiB copy used to calibrate HBM byte counters) "
                          "and print only its timing: the short program profilers wrap")
     return ap.parse_args()
@@ -196,7 +196,7 @@ def _attended_pairs(lens, causal, window):
     return pairs
 
 
-def bench_configs(args):
+def bench_configs(args, only=None):
     """The other prefill configs of BASELINE.json (C1, C2, C4): fwd+bwd per
     step through `_C`, as for C3. Synthetic N(0,1) inputs generated on the
     device; C2's lengths and C4's bias follow the config sheet."""
@@ -215,6 +215,8 @@ def bench_configs(args):
     ]
     out = {}
     for name, desc, lens, hq, hkv, d, dt, causal, window, with_bias in cfgs:
+        if only is not None and name != only:
+            continue
         g = torch.Generator(device="cuda").manual_seed(args.seed + 7)
         T = sum(lens)
         q = torch.randn(T, hq, d, device="cuda", generator=g).to(dt)
@@ -544,6 +546,9 @@ def main():
     if args.only == "c5":
         dec = bench_c5(args)
         print(json.dumps({"c5_ms": dec["ms"], "GBps": dec["GBps"]}), flush=True)
+        return
+    if args.only in ("c1", "c2", "c4"):
+        print(json.dumps(bench_configs(args, args.only.upper())), flush=True)
         return
     if args.only == "peaks":
         print(json.dumps(measured_peaks()), flush=True)
