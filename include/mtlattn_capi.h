@@ -115,6 +115,29 @@ int mtlattn_varlen_fwd(const mtlattn_problem* p,
                        void* stream);
 
 /*
+ * The forward above, allocating nothing and taking no workspace. No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving (decode) loops,
+ * harnesses that forbid allocation. Same routing, kernels and results as
+ * mtlattn_varlen_fwd (bitwise); the split-KV partials of calls routed to
+ * decode live in a static device array of MTLATTN_NOALLOC_SCRATCH_BYTES per
+ * GPU, set up on the first call on each GPU (do that call outside capture)
+ * and held until the process ends. Calls whose partials would exceed it
+ * (mtlattn_varlen_fwd_workspace_size(p) > MTLATTN_NOALLOC_SCRATCH_BYTES)
+ * return MTLATTN_ERR_WORKSPACE. Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other threads) race
+ * and must be serialised by the caller. Each call rewrites every partial it
+ * reads, so nothing carries over from earlier calls.
+ */
+#define MTLATTN_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int mtlattn_varlen_fwd_noalloc(const mtlattn_problem* p,
+                               const void* q, int64_t q_row_stride,
+                               const void* k, int64_t k_row_stride,
+                               const void* v, int64_t v_row_stride,
+                               void* out, float* lse,
+                               void* stream);
+
+/*
  * Backward: (dq, dk, dv) of the forward above given dout and the forward's
  * out and lse. dk/dv of a kv head are summed over its Hq/Hkv query heads
  * inside the kernels (no atomics; bitwise run-to-run deterministic).

@@ -52,6 +52,7 @@ SIGNATURES = {
     "mtlattn_gpu_core_count": (ctypes.c_int, [ctypes.c_int]),
     "mtlattn_varlen_fwd_workspace_size": (_sz, [_P]),
     "mtlattn_varlen_fwd": (ctypes.c_int, [_P, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _sz, _vp]),
+    "mtlattn_varlen_fwd_noalloc": (ctypes.c_int, [_P, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp]),
     "mtlattn_varlen_bwd_workspace_size": (_sz, [_P]),
     "mtlattn_varlen_bwd": (ctypes.c_int, [_P, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp,
                                           _vp, _vp, _vp, _vp, _sz, _vp]),

@@ -8,12 +8,22 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/mtlattn_capi.h"
 #include "kernels.h"
 
 using namespace mtlattn;
+
+// Scratch of mtlattn_varlen_fwd_noalloc: the split-KV partials live in this
+// file-scope device array instead of a caller's workspace. Each GPU the
+// library runs on holds its own copy (MTLATTN_NOALLOC_SCRATCH_BYTES) from the
+// first call on that GPU until the process ends. In host code `scratch` is
+// only a symbol handle: its device address comes from hipGetSymbolAddress,
+// once per device (device_scratch below), and only that address is ever
+// passed to kernels.
+static __device__ __align__(256) char scratch[MTLATTN_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -262,6 +272,34 @@ DecodePlan paged_plan(const mtlattn_problem* p, int64_t max_seqlen_kv) {
     return plan;
 }
 
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch (set up on the first call
+// on that device), or nullptr with the error recorded.
+void* device_scratch(int* code) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        *code = fail(MTLATTN_ERR_LAUNCH, "mtlattn: no current HIP device for the static scratch (%s)",
+                     hipGetErrorString(e));
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr) {
+            *code = fail(MTLATTN_ERR_LAUNCH, "mtlattn: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                         hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -315,6 +353,27 @@ int mtlattn_varlen_fwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
         tile_stride_ok(v_row_stride) && !force_generic())
         return launch_status(launch_fwd_mfma(p->dtype, a, st), "flash forward");
     return launch_status(launch_fwd_generic(p->dtype, a, st), "generic forward");
+}
+
+int mtlattn_varlen_fwd_noalloc(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
+                               int64_t k_row_stride, const void* v, int64_t v_row_stride, void* out, float* lse,
+                               void* stream) {
+    int rc = check_problem(p);
+    if (rc != MTLATTN_OK) return rc;
+    if (p->total_q == 0) return ok();
+    // the workspace mtlattn_varlen_fwd would need: split-KV partials when the
+    // call is routed to decode, nothing for the flash forward
+    const size_t need = mtlattn_varlen_fwd_workspace_size(p);
+    if (need == 0)
+        return mtlattn_varlen_fwd(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, nullptr, 0, stream);
+    if (need > (size_t)MTLATTN_NOALLOC_SCRATCH_BYTES)
+        return fail(MTLATTN_ERR_WORKSPACE,
+                    "mtlattn: varlen_fwd_noalloc: this call needs %zu bytes of split-KV scratch, more than the "
+                    "static %lld bytes; use mtlattn_varlen_fwd with a workspace",
+                    need, (long long)MTLATTN_NOALLOC_SCRATCH_BYTES);
+    void* ws = device_scratch(&rc);
+    if (ws == nullptr) return rc;
+    return mtlattn_varlen_fwd(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, ws, need, stream);
 }
 
 size_t mtlattn_varlen_bwd_workspace_size(const mtlattn_problem* p) {
