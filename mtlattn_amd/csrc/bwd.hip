@@ -430,8 +430,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     // tiles run top-down with the heads inner, so every workgroup of a
     // sequence reads the same (tile, head) at the same time and the L2 serves
     // the repeats (each workgroup stops at its own causal start q_lo).
-    auto stage_head = [&](int st) { return hk * p.g + st % p.g; };
-    auto stage_q0 = [&](int st) { return q_lo + (n_q_tiles - 1 - st / p.g) * QTL; };
+    // Stages are visited in order, so each per-stage quantity (head, first
+    // query, ring slot, source rows) is a cursor advanced one stage at a time:
+    // no division by g or by the ring depth in the loop.
+    const int qt_first = q_lo + (n_q_tiles - 1) * QTL;
     // Direct loads of stage `st`: Q and dO tiles by four loader waves
     // (ldw = 0..3), lse by loader 0, delta by loader 1 (4 bytes per lane,
     // lane l -> row l).
@@ -441,27 +443,49 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         qst.init(p.q_rs, ldw, lane);
         dost.init(p.do_rs, ldw, lane);
     }
-    auto stage = [&](int st) {
-        char* buf = smem + (st % NBUF) * STAGE;
-        const int h = stage_head(st);
-        const int qt = stage_q0(st);
-        const int64_t hoff = (int64_t)qr.start * p.q_rs + (int64_t)h * DV;
-        // Without a bias the A waves issue the tile loads: wave B, one stage
-        // behind, is the longer of the two and should not stall on issue.
-        // With a bias the A waves keep their own bias loads in flight, and
-        // the wait for those would also cover tile loads issued after them,
-        // so the B waves load the tiles.
-        if (ldw >= 0) {
-            qst.issue(buf, p.q + hoff, p.q_rs, qt, q_len, ldw, lane);
-            dost.issue(buf + TILE, p.dout + (int64_t)qr.start * p.do_rs + (int64_t)h * DV, p.do_rs, qt, q_len, ldw,
-                       lane);
+    // Loader cursor: the next stage to issue. Advancing to the next head
+    // moves the rows by DV columns (lse / delta by one); past the group's
+    // last head they move to head 0 of the tile QTL rows up.
+    int ld_hl = 0, ld_qt = qt_first, ld_slot = 0;
+    const uint16_t* ld_q = p.q + (int64_t)(qr.start + qt_first) * p.q_rs + (int64_t)hk * p.g * DV;
+    const uint16_t* ld_do = p.dout + (int64_t)(qr.start + qt_first) * p.do_rs + (int64_t)hk * p.g * DV;
+    const float* ld_l = (ldw == 0 ? p.lse : p.delta) + (int64_t)(qr.start + qt_first) * p.hq + hk * p.g;
+    const int64_t q_wrap = -(int64_t)(p.g - 1) * DV - (int64_t)QTL * p.q_rs;
+    const int64_t do_wrap = -(int64_t)(p.g - 1) * DV - (int64_t)QTL * p.do_rs;
+    const int64_t l_wrap = -(int64_t)(p.g - 1) - (int64_t)QTL * p.hq;
+    const uint32_t l_voff = (uint32_t)lane * (uint32_t)p.hq * 4u;
+    // Issues the loader cursor's stage and advances the cursor.
+    // Without a bias the A waves issue the tile loads: wave B, one stage
+    // behind, is the longer of the two and should not stall on issue. With
+    // a bias the A waves keep their own bias loads in flight, and the wait
+    // for those would also cover tile loads issued after them, so the B
+    // waves load the tiles.
+    auto stage = [&]() {
+        if (ldw < 0) return;
+        char* buf = smem + ld_slot * STAGE;
+        const int avail = q_len - ld_qt;                    // >= 1
+        qst.issue_at(buf, ld_q, p.q_rs, avail, ldw, lane);
+        dost.issue_at(buf + TILE, ld_do, p.do_rs, avail, ldw, lane);
+        if (ldw < 2) {   // rows past the end repeat the last row (masked)
+            const uint32_t voff = avail >= 64 ? l_voff : (uint32_t)min(lane, avail - 1) * (uint32_t)p.hq * 4u;
+            lds_dma4s(ld_l, voff, buf + 2 * TILE + ldw * 64 * 4);
         }
-        if (ldw == 0 || ldw == 1) {
-            const int q = min(qt + lane, q_len - 1);        // rows past the end are masked
-            const float* src = (ldw == 0 ? p.lse : p.delta) + (int64_t)(qr.start + q) * p.hq + h;
-            lds_dma4(src, buf + 2 * TILE + ldw * 64 * 4);
+        ld_slot = ld_slot == NBUF - 1 ? 0 : ld_slot + 1;
+        if (++ld_hl == p.g) {
+            ld_hl = 0;
+            ld_qt -= QTL;
+            ld_q += q_wrap;
+            ld_do += do_wrap;
+            ld_l += l_wrap;
+        } else {
+            ld_q += DV;
+            ld_do += DV;
+            ld_l += 1;
         }
     };
+    // Compute cursor: stage st (wave A, and wave B's dP) and the ring slot of
+    // stage st - 1 (wave B's dS and dK).
+    int c_hl = 0, c_qt = qt_first, c_slot = 0, p_slot = NBUF - 1;
 
     const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
     const float c2 = p.scale_log2;
@@ -479,8 +503,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     // masking? Blocks entirely outside the band (nothing to add) are also
     // "masked": they are computed with P = 0 rather than skipped, because a
     // branch around the MFMAs costs accumulator copies.
-    auto block_needs_mask = [&](int st, int qb) {
-        const int qf0 = stage_q0(st) + 32 * qb;
+    auto block_needs_mask = [&](int qb) {
+        const int qf0 = c_qt + 32 * qb;
         const int qf1 = min(q_len, qf0 + 32) - 1;
         return (kw + kKW > kv_len) | (qf0 + 32 > q_len) | ((p.causal != 0) & (wk_last > qf0 + coff)) |
                ((p.window > 0) & (kw < qf1 + coff - p.window + 1));
@@ -488,22 +512,22 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     const Band band = query_band(key, coff, q_len, kv_len, p.causal, p.window);
 
     if (n_stages > 0) {
-        stage(0);
+        stage();
         wait_vmcnt<0>();
         if (ldw == 0 || ldw == 1) neg_col(reinterpret_cast<float*>(smem + 2 * TILE) + 64 * ldw + lane, ldw);
         __syncthreads();
     }
     for (int st = 0; n_stages > 0 && st <= n_stages; ++st) {
-        if (st + 1 < n_stages) stage(st + 1);
+        if (st + 1 < n_stages) stage();
         if (role_a && st < n_stages) {
-            const char* Qs = smem + (st % NBUF) * STAGE;
+            const char* Qs = smem + c_slot * STAGE;
             const char* Ds = Qs + TILE;
             const float* ls = reinterpret_cast<const float*>(Qs + 2 * TILE);   // -lse log2(e)
             const char* qrb = opaque(Qs + rbase);
             const char* dtb = opaque(Ds + tbase);
             char* pb = smem + NBUF * STAGE + (st & 1) * PSTAGE + pair * NQB * PBLK;
-            const int h = stage_head(st);
-            const int qt = stage_q0(st);
+            const int h = hk * p.g + c_hl;
+            const int qt = c_qt;
             // S of both 32-query blocks on the matrix cores; block 0's
             // exponentials then overlap block 1's MFMAs, and block 1's
             // exponentials overlap block 0's dV products.
@@ -582,7 +606,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) {
                 // out-of-band elements (and rows with no allowed key) -> P = 0
-                if (block_needs_mask(st, qb)) {
+                if (block_needs_mask(qb)) {
                     asm volatile("");   // keep a real branch (no speculated selects on every block)
                     const int d0 = qt + 32 * qb + 4 * hi - band.lo;   // query - band.lo at r = 0
 #pragma unroll
@@ -614,10 +638,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             // exponentials, instead of both waves of a SIMD issuing matrix
             // work and then VALU work at the same time.
             if (st > 0) {
-                const int sp = st - 1;
-                const char* Qs = smem + (sp % NBUF) * STAGE;
+                const char* Qs = smem + p_slot * STAGE;
                 const char* qtb = opaque(Qs + tbase);
-                const char* pb = smem + NBUF * STAGE + (sp & 1) * PSTAGE + pair * NQB * PBLK;
+                const char* pb = smem + NBUF * STAGE + ((st - 1) & 1) * PSTAGE + pair * NQB * PBLK;
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
@@ -640,8 +663,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             if (st < n_stages) {
                 // dP - delta: the products accumulate onto -delta (the staged
                 // delta column is negated), so dS is one multiply per element
-                const char* drb = opaque(smem + (st % NBUF) * STAGE + TILE + rbase);
-                const float* dls = reinterpret_cast<const float*>(smem + (st % NBUF) * STAGE + 2 * TILE) + 64;
+                const char* drb = opaque(smem + c_slot * STAGE + TILE + rbase);
+                const float* dls = reinterpret_cast<const float*>(smem + c_slot * STAGE + 2 * TILE) + 64;
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
@@ -660,12 +683,19 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         // stage st + 1 landed for this wave; loaders 0 and 1 turn their lse
         // and delta columns into -lse log2 e and -delta before the barrier
         // publishes the stage
+        const int n_slot = c_slot == NBUF - 1 ? 0 : c_slot + 1;
         wait_vmcnt<0>();
         if ((ldw == 0 || ldw == 1) && st + 1 < n_stages) {
-            float* l = reinterpret_cast<float*>(smem + ((st + 1) % NBUF) * STAGE + 2 * TILE);
+            float* l = reinterpret_cast<float*>(smem + n_slot * STAGE + 2 * TILE);
             neg_col(l + 64 * ldw + lane, ldw);
         }
         __syncthreads();
+        p_slot = c_slot;
+        c_slot = n_slot;
+        if (++c_hl == p.g) {
+            c_hl = 0;
+            c_qt -= QTL;
+        }
     }
 
     if (pair_active && key_ok) {

@@ -218,8 +218,13 @@ __device__ inline void lds_dma4(const void* gptr, const char* lds) {
     const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
     asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(gptr), "{m0}"(a) : "memory");
 }
-// 16 bytes per lane from a wave-uniform base plus a 32-bit per-lane byte
+// 4 bytes per lane from a wave-uniform base plus a 32-bit per-lane byte
 // offset (the instruction's SADDR form: no 64-bit address arithmetic).
+__device__ inline void lds_dma4s(const void* sbase, uint32_t voff, const char* lds) {
+    const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(a) : "memory");
+}
+// 16 bytes per lane, SADDR form as above.
 __device__ inline void lds_dma16s(const void* sbase, uint32_t voff, const char* lds) {
     const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(a) : "memory");
@@ -265,8 +270,14 @@ struct TileStager {
     // rows [row0, row0 + ROWS) of base (row0 < row_end) into tile
     __device__ void issue(char* tile, const uint16_t* base, int64_t rs, int row0, int row_end, int w,
                           int lane) const {
-        const char* tb = reinterpret_cast<const char*>(base + (int64_t)row0 * rs);
-        if (row0 + ROWS <= row_end) {
+        issue_at(tile, base + (int64_t)row0 * rs, rs, row_end - row0, w, lane);
+    }
+    // ROWS rows from tile_row0 (the tile's first row) into tile, when only
+    // the first `avail` >= 1 of them exist
+    __device__ void issue_at(char* tile, const uint16_t* tile_row0, int64_t rs, int avail, int w,
+                             int lane) const {
+        const char* tb = reinterpret_cast<const char*>(tile_row0);
+        if (avail >= ROWS) {
 #pragma unroll
             for (int j = 0; j < N; ++j) {
                 const int i = w + j * NW;
@@ -274,7 +285,7 @@ struct TileStager {
                 lds_dma16s(tb, off[j], tile + i * 1024);
             }
         } else {
-            const int rmax = max(row_end - 1 - row0, 0);
+            const int rmax = max(avail - 1, 0);
 #pragma unroll
             for (int j = 0; j < N; ++j) {
                 const int i = w + j * NW;
