@@ -486,6 +486,11 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     // Compute cursor: stage st (wave A, and wave B's dP) and the ring slot of
     // stage st - 1 (wave B's dS and dK).
     int c_hl = 0, c_qt = qt_first, c_slot = 0, p_slot = NBUF - 1;
+    float bvals[NQB][16];                       // wave A: bias of the current query tile
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bvals[qb][r] = 0.f;
 
     const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
     const float c2 = p.scale_log2;
@@ -528,21 +533,21 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             char* pb = smem + NBUF * STAGE + (st & 1) * PSTAGE + pair * NQB * PBLK;
             const int h = hk * p.g + c_hl;
             const int qt = c_qt;
-            // S of both 32-query blocks on the matrix cores; block 0's
-            // exponentials then overlap block 1's MFMAs, and block 1's
-            // exponentials overlap block 0's dV products.
-            // the stage's bias (this lane's key column, 32 query rows), all
-            // loads in flight together under the S products; columns at or
-            // past bias_cols read as 0, rows past the end read the last row
-            float bvals[NQB][16];
-            // Whole stage inside the sequence (and its bias rows) and every key
-            // of the pair inside the bias columns: buffer loads from the
-            // stage's first bias row, the lane's column and 4 hi rows in the
-            // per-lane offset, each element's row in the scalar offset (no
-            // per-element address arithmetic, no column select).
+            // The stage's bias (this lane's key column, 32 query rows per
+            // block), all loads in flight together under the S products;
+            // columns at or past bias_cols read as 0, rows past the end read
+            // the last row. A bias shared by all heads is loaded at the first
+            // head of each query tile and kept for the group's other heads.
+            // Fast path -- whole stage inside the sequence (and its bias
+            // rows), every key of the pair inside the bias columns: buffer
+            // loads from the stage's first bias row, the lane's column and 4
+            // hi rows in the per-lane offset, each element's row in the
+            // scalar offset (no per-element address arithmetic, no select).
             const bool fast_bias = BIAS && p.bias_b32 && (qt + QTL <= q_len) &&
                                    ((p.bias_ss < 0) | (qt + QTL <= p.bias_rows)) && (kw + kKW <= p.bias_cols);
-            if (fast_bias) {
+            const bool load_bias = BIAS && ((c_hl == 0) | (p.bias_hs != 0));
+            if (!load_bias) {
+            } else if (fast_bias) {
                 const float* b0 = p.bias + bias_row_offset(qr.start + qt, s, qr.start, p.bias_qs, p.bias_ss,
                                                            p.bias_rows) + (int64_t)h * p.bias_hs;
                 const __amdgpu_buffer_rsrc_t rs =
