@@ -213,12 +213,20 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         bst.init(row_off, w, lane);
         brow0 = p.bias + row_off(0);
     }
-    auto stage = [&](int it) {
-        char* buf = smem + (it % NBUF) * STAGE;
-        const int kt = kv_lo + it * KT;
-        kst.issue(buf, kbase, p.k_rs, kt, kv_len, w, lane);
-        vst.issue(buf + TILE, vbase, p.v_rs, kt, kv_len, w, lane);
-        if (LDSB) bst.issue(buf + 2 * TILE, brow0, kt, (int)p.bias_cols, w);
+    // Tiles are staged in order: the next tile's ring slot, first key and
+    // K / V rows advance by one tile per call (no division, no row product).
+    int ld_slot = 0, ld_kt = kv_lo;
+    const uint16_t* ld_k = kbase + (int64_t)kv_lo * p.k_rs;
+    const uint16_t* ld_v = vbase + (int64_t)kv_lo * p.v_rs;
+    auto stage = [&]() {
+        char* buf = smem + ld_slot * STAGE;
+        kst.issue_at(buf, ld_k, p.k_rs, kv_len - ld_kt, w, lane);
+        vst.issue_at(buf + TILE, ld_v, p.v_rs, kv_len - ld_kt, w, lane);
+        if (LDSB) bst.issue(buf + 2 * TILE, brow0, ld_kt, (int)p.bias_cols, w);
+        ld_slot = ld_slot == NBUF - 1 ? 0 : ld_slot + 1;
+        ld_kt += KT;
+        ld_k += (int64_t)KT * p.k_rs;
+        ld_v += (int64_t)KT * p.v_rs;
     };
 
     const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
@@ -227,21 +235,28 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     f32x16_t dqacc[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) dqacc[db] = f32x16_t{};
+    // Without a bias dP^T accumulates onto -delta (this lane's query in all
+    // 16 C slots), so dS^T = P^T (dP^T - delta) is one multiply per element.
+    // (The biased variants have no registers to spare for the block.)
+    f32x16_t ndlt;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ndlt[r] = -dlt;
 
-    if (n_kv_tiles > 0) stage(0);
-    if (n_kv_tiles > 1) stage(1);
-    for (int it = 0; it < n_kv_tiles; ++it) {
+    if (n_kv_tiles > 0) stage();
+    if (n_kv_tiles > 1) stage();
+    int slot = 0;                                // ring slot of tile it
+    for (int it = 0; it < n_kv_tiles; ++it, slot = slot == NBUF - 1 ? 0 : slot + 1) {
         if (it + 1 < n_kv_tiles) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
         __syncthreads();
         // (with a bias, the tile loads go out after the bias is consumed: the
         // bias loads' wait would otherwise also wait for them)
-        if (!reg_bias && it + 2 < n_kv_tiles) stage(it + 2);
+        if (!reg_bias && it + 2 < n_kv_tiles) stage();
         const int kt = kv_lo + it * KT;
         // the bias of the whole tile, all loads in flight together (4-key
         // groups at 32 kb + 8 g + 4 hi)
         f32x4_t bv[4 * KB];
         if (LDSB) {   // from the staged tile: this lane's query row
-            const char* bt = opaque(smem + (it % NBUF) * STAGE + 2 * TILE + bias_base(32 * (w % wph) + l32, hi));
+            const char* bt = opaque(smem + slot * STAGE + 2 * TILE + bias_base(32 * (w % wph) + l32, hi));
 #pragma unroll
             for (int i = 0; i < 4 * KB; ++i)
                 bv[i] = *reinterpret_cast<const f32x4_t*>(lds_xor(bt, 16 * (8 * (i >> 2) + 2 * (i & 3))));
@@ -278,7 +293,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         // which would split the loop body into separately scheduled blocks)
         const bool skip = !wave_active | ((p.causal != 0) & (kt > wq_last + coff)) |
                           ((p.window > 0) & (kt + KT - 1 < qa + coff - p.window + 1));
-        const char* Ks = smem + (it % NBUF) * STAGE;
+        const char* Ks = smem + slot * STAGE;
         const char* krb = opaque(Ks + rbase);
         const char* ktb = opaque(Ks + tbase);
         const bool need_mask = skip | (kt + KT > kv_len) | ((p.causal != 0) & (kt + KT - 1 > qa + coff)) |
@@ -290,7 +305,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
         // half 0's dQ products. P = exp2(S - lse) needs no running max.
         f32x16_t sacc[KB], pacc[KB];
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) sacc[kb] = pacc[kb] = f32x16_t{};
+        for (int kb = 0; kb < KB; ++kb) sacc[kb] = pacc[kb] = BIAS ? f32x16_t{} : ndlt;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) sacc[kb] = f32x16_t{};
 #pragma unroll
         for (int kc = 0; kc < DC; ++kc) {
             const char* a = lds_xor(krb, 32 * kc);
@@ -309,7 +326,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
                 if (BIAS) x = fmaf(bv[4 * kb + (r >> 2)][r & 3], kLog2e, x);
                 sacc[kb][r] = __builtin_amdgcn_exp2f(x);
             }
-            if (reg_bias && kb == KB - 1 && it + 2 < n_kv_tiles) stage(it + 2);
+            if (reg_bias && kb == KB - 1 && it + 2 < n_kv_tiles) stage();
             if (need_mask) {     // out-of-band keys -> P = 0
                 asm volatile("");   // keep a real branch (no speculated selects on every tile)
 #pragma unroll
@@ -319,7 +336,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
                 }
             }
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[kb][r] *= pacc[kb][r] - dlt;   // dS^T
+            for (int r = 0; r < 16; ++r) sacc[kb][r] *= BIAS ? pacc[kb][r] - dlt : pacc[kb][r];   // dS^T
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 const int c = 2 * kb + cc, r0 = 8 * cc;
