@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1/C2/C4 lines")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured-ceiling kernels")
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "peaks"], default=None,
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "peaks", "rates"], default=None,
                     help="run one workload (or the 1 GiB copy used to calibrate HBM byte counters) "
                          "and print only its timing: the short program profilers wrap")
     return ap.parse_args()
@@ -361,6 +361,51 @@ def measured_peaks():
                    "HIP events over 10 launches after 100 ms warm-up"}
 
 
+def issue_rates():
+    """Per-SIMD issue rates measured with the rate probes of
+    mtlattn_amd/csrc/calib.hip: one block of 8 waves per CU, waves 0-3 in one
+    role and waves 4-7 (the other wave of each SIMD) in another. For each
+    pairing, the shader cycles per instruction of each side and the clock."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(os.path.join(ROOT, "mtlattn_amd", "libmtlattn_calib.so"))
+    vp = ctypes.c_void_p
+    lib.mtlattn_calib_rates.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, vp]
+    lib.mtlattn_calib_rate_ops.argtypes = [ctypes.c_int]
+    names = {0: "idle", 1: "v_exp_f32", 2: "v_fmac_f32", 3: "mfma32x32x16 (VGPR acc)", 4: "mfma32x32x16 (AGPR acc)",
+             5: "ds_read_b128"}
+    iters = {1: 2000, 2: 4000, 3: 1000, 4: 1000, 5: 1000}
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.empty(cus * 512, dtype=torch.float32, device="cuda")
+    cyc = torch.zeros(cus * 16, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream()
+    pairs = [(1, 0), (1, 1), (2, 0), (2, 2), (3, 0), (4, 0), (3, 3), (4, 4), (3, 1), (4, 1), (3, 2), (4, 2),
+             (5, 0), (5, 5), (3, 5)]
+    out = []
+    for ra, rb in pairs:
+        n = max(iters.get(ra, 1), iters.get(rb, 1))
+        for _ in range(3):   # the first launches run while the clock ramps
+            rc = lib.mtlattn_calib_rates(ra, rb, n, cus, sink.data_ptr(), cyc.data_ptr(), stream.cuda_stream)
+            assert rc == 0, rc
+        torch.cuda.synchronize()
+        c = cyc.view(cus, 8, 2).double()
+        side = []
+        for role, waves in ((ra, slice(0, 4)), (rb, slice(4, 8))):
+            if role == 0:
+                side.append(None)
+                continue
+            cycles = c[:, waves, 0].mean().item()
+            ops = n * lib.mtlattn_calib_rate_ops(role)
+            side.append({"role": names[role], "cycles_per_instr": round(cycles / ops, 2)})
+        ticks = c[:, 0:4, 1].mean().item() if ra else c[:, 4:8, 1].mean().item()
+        cyc_a = c[:, 0:4, 0].mean().item() if ra else c[:, 4:8, 0].mean().item()
+        out.append({"waves_0_3": side[0], "waves_4_7": side[1], "iters": n,
+                    "clock_mhz": round(cyc_a / (ticks / 100.0), 0) if ticks > 0 else None})
+    return {"cus": cus, "pairs": out,
+            "how": "calib.hip calib_rates_kernel: inline-asm streams, one 8-wave block per CU, "
+                   "s_memtime cycles per wave over the instruction count; third of three launches"}
+
+
 def host_cpu():
     """Model, sockets and physical cores of the host (from /proc/cpuinfo),
     the CPUs this process may run on, and the torch thread count used: the
@@ -552,6 +597,9 @@ def main():
         return
     if args.only == "peaks":
         print(json.dumps(measured_peaks()), flush=True)
+        return
+    if args.only == "rates":
+        print(json.dumps(issue_rates()), flush=True)
         return
     c3 = bench_c3(args)
     dec = None if args.no_decode else bench_c5(args)

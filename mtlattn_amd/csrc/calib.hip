@@ -81,6 +81,93 @@ __global__ __launch_bounds__(256) void calib_read_kernel(const u32x4_t* __restri
     }
 }
 
+// Issue-rate probes. One block of 8 waves per CU; waves w and w + 4 share a
+// SIMD. Waves 0-3 run role ra, waves 4-7 role rb, each `iters` iterations:
+//   0 idle
+//   1 v_exp_f32: 16 independent chains per iteration
+//   2 v_fmac_f32: 16 independent chains per iteration
+//   3 v_mfma_f32_32x32x16_bf16, accumulators in VGPRs: 8 per iteration over 4
+//     independent accumulators
+//   4 the same with the accumulators in AGPRs
+//   5 ds_read_b128: 16 reads (16 KB per wave) in flight, then a wait
+// The instructions are inline asm so that their number and order are
+// exactly these. Each wave records its s_memtime cycles (shader clock) and
+// s_memrealtime ticks (100 MHz).
+constexpr int kRateOps[6] = {0, 16, 16, 8, 8, 16};
+
+__device__ float rate_role(int role, int iters, int lane, const char* lds) {
+    float x[18];
+#pragma unroll
+    for (int j = 0; j < 18; ++j) x[j] = 0.3f + 0.01f * j + 1e-4f * lane;
+    const u32x4_t a = {0x3f803f80u ^ (uint32_t)lane, 0x3f803f80u, 0x3c003c00u, 0x3f803f80u};
+    const u32x4_t b = {0x3c003c00u, 0x3f803f80u ^ (uint32_t)lane, 0x3f803f80u, 0x3c003c00u};
+    f32x16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    u32x4_t r[16];
+    if (role == 1) {
+        for (int i = 0; i < iters; ++i)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) asm volatile("v_exp_f32 %0, %0" : "+v"(x[j]));
+    } else if (role == 2) {
+        for (int i = 0; i < iters; ++i)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(x[j]) : "v"(x[16]), "v"(x[17]));
+    } else if (role == 3) {
+        for (int i = 0; i < iters; ++i)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c0) : "v"(a), "v"(b));
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c1) : "v"(a), "v"(b));
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c2) : "v"(a), "v"(b));
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c3) : "v"(a), "v"(b));
+            }
+    } else if (role == 4) {
+        for (int i = 0; i < iters; ++i)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c0) : "v"(a), "v"(b));
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c1) : "v"(a), "v"(b));
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c2) : "v"(a), "v"(b));
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c3) : "v"(a), "v"(b));
+            }
+    } else if (role == 5) {
+        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
+        for (int i = 0; i < iters; ++i) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                // 16-byte chunk of lane `lane` in KB j of the 32 KB buffer: every
+                // address is a multiple of 16 below 32768 - 16 + 16
+                const uint32_t addr = base + (uint32_t)((lane * 16 + j * 1024 + i * 2048) & 32767);
+                asm volatile("ds_read_b128 %0, %1" : "=v"(r[j]) : "v"(addr) : "memory");
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int j = 0; j < 16; ++j) x[j & 15] += __uint_as_float(r[j][0] & 0x3fffffffu);
+        }
+    }
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");   // MFMA results settle before the reads below
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sum += x[j] + c0[j] + c1[j] + c2[j] + c3[j];
+    return sum;
+}
+
+__global__ __launch_bounds__(512, 1) void calib_rates_kernel(int ra, int rb, int iters, float* sink,
+                                                             unsigned long long* cyc) {
+    __shared__ __attribute__((aligned(1024))) char lds[32768];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int i = threadIdx.x; i < 32768 / 4; i += 512) reinterpret_cast<uint32_t*>(lds)[i] = (uint32_t)i * 0x9e3779b9u;
+    __syncthreads();
+    const int role = w < 4 ? ra : rb;
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    const float s = role ? rate_role(role, iters, lane, lds) : 0.f;
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    if (s == 1.2345f) sink[blockIdx.x * 512 + threadIdx.x] = s;   // keeps the streams live
+    if (lane == 0) {
+        cyc[(blockIdx.x * 8 + w) * 2] = t1 - t0;
+        cyc[(blockIdx.x * 8 + w) * 2 + 1] = r1 - r0;
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -102,5 +189,16 @@ int mtlattn_calib_read(const void* src, int64_t bytes, int blocks, uint32_t* sin
                        (const u32x4_t*)src, bytes / 16 / blocks, sink, clk);
     return (int)hipGetLastError();
 }
+
+// Issue-rate probe (see calib_rates_kernel): roles ra (waves 0-3) and rb
+// (waves 4-7), `iters` iterations, one block per CU (`blocks` = CU count).
+// sink: blocks * 512 floats; cyc: blocks * 8 * 2 u64 (per wave: shader
+// cycles, 100 MHz ticks). Operations per iteration of role r: ops_per_iter.
+int mtlattn_calib_rates(int ra, int rb, int iters, int blocks, float* sink, unsigned long long* cyc, void* stream) {
+    if (ra < 0 || ra > 5 || rb < 0 || rb > 5 || iters < 1 || blocks < 1) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(calib_rates_kernel, dim3(blocks), dim3(512), 0, (hipStream_t)stream, ra, rb, iters, sink, cyc);
+    return (int)hipGetLastError();
+}
+int mtlattn_calib_rate_ops(int role) { return role >= 0 && role <= 5 ? kRateOps[role] : 0; }
 
 }  // extern "C"
