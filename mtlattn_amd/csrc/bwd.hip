@@ -857,12 +857,15 @@ hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
             return hipGetLastError();
         }
     }
-    if (a.geo.bias != nullptr)
+    if constexpr (KB > 2) {
+        if (a.geo.bias != nullptr) return hipErrorInvalidValue;   // (not dispatched: registers)
+    } else if (a.geo.bias != nullptr) {
         hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64),
                            0, st, p);
-    else
-        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, false, OUT_F32>), dim3((unsigned)blocks),
-                           dim3(NW * 64), 0, st, p);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, false, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0,
+                       st, p);
     return hipGetLastError();
 }
 
@@ -945,7 +948,14 @@ hipError_t dispatch_dims(const BwdArgs& a, hipStream_t st) {
 template <typename T, int D, int DV, bool F>
 struct DqLaunch {
     static hipError_t run(const BwdArgs& a, hipStream_t st) {
-        if constexpr (D <= 128) {
+        if constexpr (D <= 64) {
+            // 128-key tiles without a bias: at D = 64 a 64-key tile is half
+            // the MFMAs of the D = 128 one against the same per-tile overhead
+            // (barrier, staging and wait bookkeeping), and the registers hold
+            // twice the keys (the bias of a 128-key tile would not fit)
+            if (a.geo.bias == nullptr) return launch_dq_typed<T, D, DV, DV, 0, 4, F>(a, st);
+            return launch_dq_typed<T, D, DV, DV, 0, 2, F>(a, st);
+        } else if constexpr (D <= 128) {
             return launch_dq_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else {
             // 256-wide tiles: 32-key tiles (three K + V stages fit the LDS)
