@@ -393,11 +393,21 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     constexpr int NP = kWaves / 2;                      // wave pairs
     constexpr int KB = NP * kKW;                        // keys per workgroup
     constexpr int TILE = QTL * D * 2;
-    constexpr int STAGE = 2 * TILE + 2 * 64 * 4;        // Q, dO, lse, delta (64 rows each)
+    constexpr int LROWS = QTL > 64 ? QTL : 64;          // rows of a staged lse / delta column
+    constexpr int LPIECES = LROWS / 64;                 // 64-row loads per column
+    static_assert(2 * LPIECES <= NP, "one loader wave per lse / delta piece");
+    // Q ring: Q tile, lse and delta columns of a stage. Wave B reads Q one
+    // stage behind wave A, and stage st + 1 loads meanwhile: three slots.
+    constexpr int QSTAGE = TILE + 2 * LROWS * 4;
     constexpr int NBUF = 3;
+    // dO ring: a stage's dO is read only during that stage (wave A's dV,
+    // wave B's dP), so the loads of stage st + 1 reuse the slot of st - 1.
+    constexpr int NDO = 2;
+    constexpr int DO_OFF = NBUF * QSTAGE;
     constexpr int PBLK = 2 * 1024;                      // packed P of one 32x32 block
     constexpr int PSTAGE = NP * NQB * PBLK;             // one stage, all pairs
-    __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE + 2 * PSTAGE];
+    constexpr int P_OFF = DO_OFF + NDO * TILE;
+    __shared__ __attribute__((aligned(1024))) char smem[P_OFF + 2 * PSTAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
@@ -452,8 +462,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     // no division by g or by the ring depth in the loop.
     const int qt_first = q_lo + (n_q_tiles - 1) * QTL;
     // Direct loads of stage `st`: Q and dO tiles by four loader waves
-    // (ldw = 0..3), lse by loader 0, delta by loader 1 (4 bytes per lane,
-    // lane l -> row l).
+    // (ldw = 0..3); lse by loaders 0 (and 2), delta by loaders 1 (and 3):
+    // column ldw & 1, rows 64 (ldw >> 1) + lane, 4 bytes per lane.
     const int ldw = BIAS ? (role_a ? -1 : w - NP) : (role_a ? w : -1);
     TileStager<D, QTL, NP, DV> qst, dost;
     if (ldw >= 0) {
@@ -463,14 +473,16 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     // Loader cursor: the next stage to issue. Advancing to the next head
     // moves the rows by DV columns (lse / delta by one); past the group's
     // last head they move to head 0 of the tile QTL rows up.
-    int ld_hl = 0, ld_qt = qt_first, ld_slot = 0;
+    int ld_hl = 0, ld_qt = qt_first, ld_slot = 0, ld_dslot = 0;
+    const int l_col = ldw & 1, l_piece = ldw >> 1;   // (loaders with ldw < 2 * LPIECES)
     const uint16_t* ld_q = p.q + (int64_t)(qr.start + qt_first) * p.q_rs + (int64_t)hk * p.g * DV;
     const uint16_t* ld_do = p.dout + (int64_t)(qr.start + qt_first) * p.do_rs + (int64_t)hk * p.g * DV;
-    const float* ld_l = (ldw == 0 ? p.lse : p.delta) + (int64_t)(qr.start + qt_first) * p.hq + hk * p.g;
+    const float* ld_l = (l_col == 0 ? p.lse : p.delta) + (int64_t)(qr.start + qt_first) * p.hq + hk * p.g;
     const int64_t q_wrap = -(int64_t)(p.g - 1) * DV - (int64_t)QTL * p.q_rs;
     const int64_t do_wrap = -(int64_t)(p.g - 1) * DV - (int64_t)QTL * p.do_rs;
     const int64_t l_wrap = -(int64_t)(p.g - 1) - (int64_t)QTL * p.hq;
-    const uint32_t l_voff = (uint32_t)lane * (uint32_t)p.hq * 4u;
+    const int l_row = 64 * l_piece + lane;           // stage-local row this lane loads
+    const uint32_t l_voff = (uint32_t)l_row * (uint32_t)p.hq * 4u;
     // Issues the loader cursor's stage and advances the cursor.
     // Without a bias the A waves issue the tile loads: wave B, one stage
     // behind, is the longer of the two and should not stall on issue. With
@@ -479,15 +491,16 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     // waves load the tiles.
     auto stage = [&]() {
         if (ldw < 0) return;
-        char* buf = smem + ld_slot * STAGE;
+        char* buf = smem + ld_slot * QSTAGE;
         const int avail = q_len - ld_qt;                    // >= 1
         qst.issue_at(buf, ld_q, p.q_rs, avail, ldw, lane);
-        dost.issue_at(buf + TILE, ld_do, p.do_rs, avail, ldw, lane);
-        if (ldw < 2) {   // rows past the end repeat the last row (masked)
-            const uint32_t voff = avail >= 64 ? l_voff : (uint32_t)min(lane, avail - 1) * (uint32_t)p.hq * 4u;
-            lds_dma4s(ld_l, voff, buf + 2 * TILE + ldw * 64 * 4);
+        dost.issue_at(smem + DO_OFF + ld_dslot * TILE, ld_do, p.do_rs, avail, ldw, lane);
+        if (ldw < 2 * LPIECES) {   // rows past the end repeat the last row (masked)
+            const uint32_t voff = avail >= LROWS ? l_voff : (uint32_t)min(l_row, avail - 1) * (uint32_t)p.hq * 4u;
+            lds_dma4s(ld_l, voff, buf + TILE + (l_col * LROWS + 64 * l_piece) * 4);
         }
         ld_slot = ld_slot == NBUF - 1 ? 0 : ld_slot + 1;
+        ld_dslot ^= 1;
         if (++ld_hl == p.g) {
             ld_hl = 0;
             ld_qt -= QTL;
@@ -502,7 +515,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     };
     // Compute cursor: stage st (wave A, and wave B's dP) and the ring slot of
     // stage st - 1 (wave B's dS and dK).
-    int c_hl = 0, c_qt = qt_first, c_slot = 0, p_slot = NBUF - 1;
+    int c_hl = 0, c_qt = qt_first, c_slot = 0, p_slot = NBUF - 1, c_dslot = 0;
     float bvals[NQB][16];                       // wave A: bias of the current query tile
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb)
@@ -536,18 +549,18 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     if (n_stages > 0) {
         stage();
         wait_vmcnt<0>();
-        if (ldw == 0 || ldw == 1) neg_col(reinterpret_cast<float*>(smem + 2 * TILE) + 64 * ldw + lane, ldw);
+        if (ldw >= 0 && ldw < 2 * LPIECES) neg_col(reinterpret_cast<float*>(smem + TILE) + l_col * LROWS + l_row, l_col);
         __syncthreads();
     }
     for (int st = 0; n_stages > 0 && st <= n_stages; ++st) {
         if (st + 1 < n_stages) stage();
         if (role_a && st < n_stages) {
-            const char* Qs = smem + c_slot * STAGE;
-            const char* Ds = Qs + TILE;
-            const float* ls = reinterpret_cast<const float*>(Qs + 2 * TILE);   // -lse log2(e)
+            const char* Qs = smem + c_slot * QSTAGE;
+            const char* Ds = smem + DO_OFF + c_dslot * TILE;
+            const float* ls = reinterpret_cast<const float*>(Qs + TILE);   // -lse log2(e)
             const char* qrb = opaque(Qs + rbase);
             const char* dtb = opaque(Ds + tbase);
-            char* pb = smem + NBUF * STAGE + (st & 1) * PSTAGE + pair * NQB * PBLK;
+            char* pb = smem + P_OFF + (st & 1) * PSTAGE + pair * NQB * PBLK;
             const int h = hk * p.g + c_hl;
             const int qt = c_qt;
             // The stage's bias (this lane's key column, 32 query rows per
@@ -660,9 +673,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             // exponentials, instead of both waves of a SIMD issuing matrix
             // work and then VALU work at the same time.
             if (st > 0) {
-                const char* Qs = smem + p_slot * STAGE;
+                const char* Qs = smem + p_slot * QSTAGE;
                 const char* qtb = opaque(Qs + tbase);
-                const char* pb = smem + NBUF * STAGE + ((st - 1) & 1) * PSTAGE + pair * NQB * PBLK;
+                const char* pb = smem + P_OFF + ((st - 1) & 1) * PSTAGE + pair * NQB * PBLK;
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
@@ -685,8 +698,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             if (st < n_stages) {
                 // dP - delta: the products accumulate onto -delta (the staged
                 // delta column is negated), so dS is one multiply per element
-                const char* drb = opaque(smem + c_slot * STAGE + TILE + rbase);
-                const float* dls = reinterpret_cast<const float*>(smem + c_slot * STAGE + 2 * TILE) + 64;
+                const char* drb = opaque(smem + DO_OFF + c_dslot * TILE + rbase);
+                const float* dls = reinterpret_cast<const float*>(smem + c_slot * QSTAGE + TILE) + LROWS;
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
@@ -702,18 +715,19 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                         pacc[qb] = mfma32<T>(row_operand<D>(drb, kc, 32 * qb), kvf[kc], pacc[qb]);
             }
         }
-        // stage st + 1 landed for this wave; loaders 0 and 1 turn their lse
-        // and delta columns into -lse log2 e and -delta before the barrier
+        // stage st + 1 landed for this wave; the lse / delta loaders turn
+        // their pieces into -lse log2 e and -delta before the barrier
         // publishes the stage
         const int n_slot = c_slot == NBUF - 1 ? 0 : c_slot + 1;
         wait_vmcnt<0>();
-        if ((ldw == 0 || ldw == 1) && st + 1 < n_stages) {
-            float* l = reinterpret_cast<float*>(smem + n_slot * STAGE + 2 * TILE);
-            neg_col(l + 64 * ldw + lane, ldw);
+        if (ldw >= 0 && ldw < 2 * LPIECES && st + 1 < n_stages) {
+            float* l = reinterpret_cast<float*>(smem + n_slot * QSTAGE + TILE);
+            neg_col(l + l_col * LROWS + l_row, l_col);
         }
         __syncthreads();
         p_slot = c_slot;
         c_slot = n_slot;
+        c_dslot ^= 1;
         if (++c_hl == p.g) {
             c_hl = 0;
             c_qt -= QTL;
@@ -876,12 +890,15 @@ hipError_t launch_dkv_typed(const BwdArgs& a, hipStream_t st) {
     p.n_tiles = (int)(a.geo.total_kv / (NW / 2 * kKW)) + a.geo.num_seqs + 1;
     const int64_t blocks = (int64_t)p.n_tiles * a.geo.hkv;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    if (a.geo.bias != nullptr)
+    if constexpr (NQB > 2) {
+        if (a.geo.bias != nullptr) return hipErrorInvalidValue;   // (not dispatched: registers)
+    } else if (a.geo.bias != nullptr) {
         hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, DO, C0, NQB, true, OUT_F32>), dim3((unsigned)blocks),
                            dim3(NW * 64), 0, st, p);
-    else
-        hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, DO, C0, NQB, false, OUT_F32>), dim3((unsigned)blocks),
-                           dim3(NW * 64), 0, st, p);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, DO, C0, NQB, false, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64),
+                       0, st, p);
     return hipGetLastError();
 }
 
@@ -978,7 +995,12 @@ struct DqLaunch {
 template <typename T, int D, int DV, bool F>
 struct DkvLaunch {
     static hipError_t run(const BwdArgs& a, hipStream_t st) {
-        if constexpr (D <= 128) {
+        if constexpr (D <= 64) {
+            // 128-query stages without a bias (twice the MFMAs per stage's
+            // fixed cost; the bias of a 128-query stage would not fit)
+            if (a.geo.bias == nullptr) return launch_dkv_typed<T, D, DV, DV, 0, 4, F>(a, st);
+            return launch_dkv_typed<T, D, DV, DV, 0, 2, F>(a, st);
+        } else if constexpr (D <= 128) {
             return launch_dkv_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else {
             // 256-wide tiles: 32-query stages (three fit the LDS) and the
