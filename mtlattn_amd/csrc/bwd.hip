@@ -544,6 +544,14 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         return (kw + kKW > kv_len) | (qf0 + 32 > q_len) | ((p.causal != 0) & (wk_last > qf0 + coff)) |
                ((p.window > 0) & (kw < qf1 + coff - p.window + 1));
     };
+    // Does any block of the stage need masking? Each term is the per-block
+    // test at the block that decides it (the first block for the causal
+    // edge, the last for the sequence end and the window edge), so the
+    // common unmasked stage costs one test, not one per block.
+    auto stage_needs_mask = [&]() {
+        return (kw + kKW > kv_len) | (c_qt + QTL > q_len) | ((p.causal != 0) & (wk_last > c_qt + coff)) |
+               ((p.window > 0) & (kw < min(q_len, c_qt + QTL) + coff - p.window));
+    };
     const Band band = query_band(key, coff, q_len, kv_len, p.causal, p.window);
 
     if (n_stages > 0) {
@@ -638,15 +646,18 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
                     }
                 }
             }
+            if (stage_needs_mask()) {
+                asm volatile("");
 #pragma unroll
-            for (int qb = 0; qb < NQB; ++qb) {
-                // out-of-band elements (and rows with no allowed key) -> P = 0
-                if (block_needs_mask(qb)) {
-                    asm volatile("");   // keep a real branch (no speculated selects on every block)
-                    const int d0 = qt + 32 * qb + 4 * hi - band.lo;   // query - band.lo at r = 0
+                for (int qb = 0; qb < NQB; ++qb) {
+                    // out-of-band elements (and rows with no allowed key) -> P = 0
+                    if (block_needs_mask(qb)) {
+                        asm volatile("");   // keep a real branch (no speculated selects on every block)
+                        const int d0 = qt + 32 * qb + 4 * hi - band.lo;   // query - band.lo at r = 0
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        sacc[qb][r] = (uint32_t)(d0 + 8 * (r >> 2) + (r & 3)) < band.width ? sacc[qb][r] : 0.f;
+                        for (int r = 0; r < 16; ++r)
+                            sacc[qb][r] = (uint32_t)(d0 + 8 * (r >> 2) + (r & 3)) < band.width ? sacc[qb][r] : 0.f;
+                    }
                 }
             }
 #pragma unroll
