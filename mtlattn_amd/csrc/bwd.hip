@@ -763,29 +763,31 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// delta = rowsum(dO * O). 16-bit types with D % 8 == 0 and 16 | D * 4 lanes:
-// one wave per row, every lane streams 16-byte chunks of the contiguous
-// [H * D] row (coalesced), lanes sharing a head reduce with DPP shuffles.
-// Other cases: one thread per (row, head).
+// delta = rowsum(dO * O). 16-bit types with D % 8 == 0 (D <= 512): one wave
+// per row; a head's D / 8 sixteen-byte chunks go to a group of lg lanes (the
+// next power of two, so groups never straddle), 64 / lg heads per pass, and
+// each group reduces with shuffles. Reads are coalesced: consecutive lanes
+// read consecutive chunks of the contiguous [H * D] row. Other cases: one
+// thread per (row, head).
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_preprocess_row_kernel(const uint16_t* __restrict__ o, int64_t o_rs,
                                                                  const uint16_t* __restrict__ dout, int64_t do_rs,
                                                                  float* __restrict__ delta, int64_t total_q, int hq,
-                                                                 int d) {
+                                                                 int d, int lg) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= total_q) return;
-    const int lpg = d / 8;                         // lanes per head: 8 (D=64) or 16 (D=128)
-    const int chunks = hq * lpg;                   // 16-byte chunks per row
+    const int lpg = d / 8;                         // 16-byte chunks per head
+    const int hl = lane / lg, j = lane - hl * lg;  // head within the pass, chunk
     const uint16_t* op = o + row * o_rs;
     const uint16_t* dp = dout + row * do_rs;
-    for (int c0 = 0; c0 < chunks; c0 += 64) {
-        const int c = c0 + lane;
+    for (int h0 = 0; h0 < hq; h0 += 64 / lg) {
+        const int h = h0 + hl;
         float acc = 0.f;
-        if (c < chunks) acc = dot8<T>(ld16(op + 8 * c), ld16(dp + 8 * c));
-        for (int off = lpg >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-        if (c < chunks && (c % lpg) == 0) delta[row * hq + c / lpg] = acc;
+        if (h < hq && j < lpg) acc = dot8<T>(ld16(op + h * d + 8 * j), ld16(dp + h * d + 8 * j));
+        for (int off = lg >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+        if (h < hq && j == 0) delta[row * hq + h] = acc;
     }
 }
 
@@ -919,17 +921,19 @@ hipError_t launch_bwd_preprocess(int dtype, const Geometry& geo, const void* o, 
                                  const void* dout, int64_t do_rs, float* delta, hipStream_t st) {
     const int64_t n = geo.total_q * geo.hq;
     if (n == 0) return hipSuccess;
-    const bool rowwise = dtype != MTLATTN_DTYPE_F32 && (geo.d == 64 || geo.d == 128) &&
+    const bool rowwise = dtype != MTLATTN_DTYPE_F32 && geo.d % 8 == 0 && geo.d <= 512 &&
                          ((uintptr_t)o & 15u) == 0 && ((uintptr_t)dout & 15u) == 0 && (o_rs % 8) == 0 &&
                          (do_rs % 8) == 0;
     if (rowwise) {
+        int lg = 1;
+        while (lg < geo.d / 8) lg *= 2;                 // lanes per head: a power of two <= 64
         const dim3 grid((unsigned)((geo.total_q + 3) / 4));
         if (dtype == MTLATTN_DTYPE_BF16)
             hipLaunchKernelGGL(bwd_preprocess_row_kernel<BF16>, grid, dim3(256), 0, st, (const uint16_t*)o, o_rs,
-                               (const uint16_t*)dout, do_rs, delta, geo.total_q, geo.hq, geo.d);
+                               (const uint16_t*)dout, do_rs, delta, geo.total_q, geo.hq, geo.d, lg);
         else
             hipLaunchKernelGGL(bwd_preprocess_row_kernel<F16>, grid, dim3(256), 0, st, (const uint16_t*)o, o_rs,
-                               (const uint16_t*)dout, do_rs, delta, geo.total_q, geo.hq, geo.d);
+                               (const uint16_t*)dout, do_rs, delta, geo.total_q, geo.hq, geo.d, lg);
         return hipGetLastError();
     }
     const dim3 grid((unsigned)((n + 255) / 256));
@@ -990,10 +994,8 @@ struct DqLaunch {
             // and the output in column slices (96 wide for D = 160; 64 for
             // D = 256, whose Q^T and dO^T fragments alone take 128 registers)
             if constexpr (DV > 192) {
-                hipError_t e = launch_dq_typed<T, D, DV, 64, 0, 1, F>(a, st);
-                if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 64, 64, 1, F>(a, st);
-                if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 64, 128, 1, F>(a, st);
-                if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 64, 192, 1, F>(a, st);
+                hipError_t e = launch_dq_typed<T, D, DV, 128, 0, 1, F>(a, st);
+                if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 128, 128, 1, F>(a, st);
                 return e;
             } else {
                 hipError_t e = launch_dq_typed<T, D, DV, 96, 0, 1, F>(a, st);
