@@ -990,17 +990,16 @@ struct DqLaunch {
         } else if constexpr (D <= 128) {
             return launch_dq_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else {
-            // 256-wide tiles: 32-key tiles (three K + V stages fit the LDS)
-            // and the output in column slices (96 wide for D = 160; 64 for
-            // D = 256, whose Q^T and dO^T fragments alone take 128 registers)
+            // 256-wide tiles: 32-key tiles (three K + V stages fit the LDS).
+            // D = 160 computes the whole output in one launch (249 VGPRs);
+            // D = 256 in two 128-column launches (its Q^T and dO^T fragments
+            // alone take 128 registers; S and dP are recomputed per launch)
             if constexpr (DV > 192) {
                 hipError_t e = launch_dq_typed<T, D, DV, 128, 0, 1, F>(a, st);
                 if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 128, 128, 1, F>(a, st);
                 return e;
             } else {
-                hipError_t e = launch_dq_typed<T, D, DV, 96, 0, 1, F>(a, st);
-                if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 96, 96, 1, F>(a, st);
-                return e;
+                return launch_dq_typed<T, D, DV, DV, 0, 1, F>(a, st);
             }
         }
     }
@@ -1016,12 +1015,16 @@ struct DkvLaunch {
         } else if constexpr (D <= 128) {
             return launch_dkv_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else {
-            // 256-wide tiles: 32-query stages (three fit the LDS) and the
-            // output in two column slices
-            constexpr int DO = DV > 192 ? 128 : 96;
-            hipError_t e = launch_dkv_typed<T, D, DV, DO, 0, 1, F>(a, st);
-            if (e == hipSuccess) e = launch_dkv_typed<T, D, DV, DO, DO, 1, F>(a, st);
-            return e;
+            // 256-wide tiles: 32-query stages. D = 160 computes the whole
+            // output in one launch (207 VGPRs); D = 256 in two 128-column
+            // launches (one launch would spill its accumulators)
+            if constexpr (DV > 192) {
+                hipError_t e = launch_dkv_typed<T, D, DV, 128, 0, 1, F>(a, st);
+                if (e == hipSuccess) e = launch_dkv_typed<T, D, DV, 128, 128, 1, F>(a, st);
+                return e;
+            } else {
+                return launch_dkv_typed<T, D, DV, DV, 0, 1, F>(a, st);
+            }
         }
     }
 };
