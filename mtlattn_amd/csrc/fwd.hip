@@ -62,16 +62,19 @@ struct FwdKParams {
 // workgroup covers BROWS query rows; each key tile's bias block is staged in
 // the LDS ring with the K/V tiles (read from LDS by all waves of all heads)
 // instead of every wave loading its rows from global memory.
-template <typename T, int DK, int DV, int DVL, int DO, int SM, int BROWS = 0>
+template <typename T, int DK, int DV, int DVL, int DO, int SM, int BROWS = 0, int KT = kKT>
 __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
+    static_assert(KT == 64 || (KT == 32 && SM == 0), "32-key tiles: unbiased only");
+    constexpr int NKB = KT / 32;             // 32-key blocks per tile
+    constexpr int NPC = KT / 16;             // 16-key P chunks per tile
     constexpr bool BIAS = SM != 0;
     constexpr bool LDSB = BROWS > 0;
     static_assert(!LDSB || SM == 1, "staged bias is for the biased raw-max softmax");
     constexpr int DC = (DV + 15) / 16;       // MFMA k-chunks over the head dim
     constexpr int DB = (DO + 31) / 32;       // 32-row output blocks
-    constexpr int KTILE = kKT * DK * 2;      // bytes of one K tile
-    constexpr int VTILE = kKT * DVL * 2;     // bytes of one V tile
-    constexpr int BTILE = BROWS * kKT * 4;   // bytes of one staged bias tile
+    constexpr int KTILE = KT * DK * 2;      // bytes of one K tile
+    constexpr int VTILE = KT * DVL * 2;     // bytes of one V tile
+    constexpr int BTILE = BROWS * KT * 4;   // bytes of one staged bias tile
     constexpr int STAGE = KTILE + VTILE + BTILE;   // K, V (row-major), bias
     constexpr int NBUF = 3;                  // ring of staged key tiles
     constexpr int LOADS = STAGE / 1024 / kWaves;   // direct loads per wave per tile
@@ -122,15 +125,15 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     int kv_lo = 0;
     if (p.window > 0) {
         kv_lo = max(0, q0 + coff - p.window + 1);
-        kv_lo = (kv_lo / kKT) * kKT;
+        kv_lo = (kv_lo / KT) * KT;
     }
-    const int n_kv_tiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kKT - 1) / kKT : 0;
+    const int n_kv_tiles = kv_hi > kv_lo ? (kv_hi - kv_lo + KT - 1) / KT : 0;
 
     const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * DV;
     const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * DV + p.col0;
     // All 8 waves stage each tile straight from HBM into LDS (K then V).
-    TileStager<DK, kKT, kWaves, DV> kst;
-    TileStager<DVL, kKT, kWaves, DO> vst;
+    TileStager<DK, KT, kWaves, DV> kst;
+    TileStager<DVL, KT, kWaves, DO> vst;
     kst.init(p.k_rs, w, lane);
     vst.init(p.v_rs, w, lane);
     // Staged bias: WG row r is query q0 + r (rows past the end repeat the last)
@@ -145,7 +148,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     }
     auto stage = [&](int it) {
         char* buf = smem + (it % NBUF) * STAGE;
-        const int kt = kv_lo + it * kKT;
+        const int kt = kv_lo + it * KT;
         kst.issue(buf, kbase, p.k_rs, kt, kv_len, w, lane);
         vst.issue(buf + KTILE, vbase, p.v_rs, kt, kv_len, w, lane);
         if (LDSB) bst.issue(buf + KTILE + VTILE, brow0, kt, (int)p.bias_cols, w);
@@ -175,7 +178,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     // 32 kb + 8 g + 4 hi) is loaded up front, all loads in flight together,
     // and consumed after the S products; 16-byte loads when aligned.
     auto load_bias = [&](int kt, f32x4_t (&bv)[8]) {
-        if (kt + kKT <= p.bias_cols && p.bias_v4) {
+        if (kt + KT <= p.bias_cols && p.bias_v4) {
 #pragma unroll
             for (int i = 0; i < 8; ++i)
                 bv[i] = *reinterpret_cast<const f32x4_t*>(brow + kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi);
@@ -222,7 +225,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         // bias, the tile loads go out after the bias is consumed: the bias
         // loads' wait would otherwise also wait for them)
         if (!reg_bias && it + 2 < n_kv_tiles) stage(it + 2);
-        const int kt = kv_lo + it * kKT;
+        const int kt = kv_lo + it * KT;
         f32x4_t bv[8];
         if (reg_bias) load_bias(kt, bv);
         if (LDSB) {
@@ -231,7 +234,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
 #pragma unroll
             for (int i = 0; i < 8; ++i)
                 bv[i] = *reinterpret_cast<const f32x4_t*>(lds_xor(bt, 16 * (8 * (i >> 2) + 2 * (i & 3))));
-            if (kt + kKT > p.bias_cols) {   // keys at or past the bias columns read as 0
+            if (kt + KT > p.bias_cols) {   // keys at or past the bias columns read as 0
                 asm volatile("");
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
@@ -249,11 +252,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         // (bitwise | and &: these uniform tests must not become branches,
         // which would split the loop body into separately scheduled blocks)
         const bool skip = !wave_active | ((p.causal != 0) & (kt > wq_last + coff)) |
-                          ((p.window > 0) & (kt + kKT - 1 < qa + coff - p.window + 1));
+                          ((p.window > 0) & (kt + KT - 1 < qa + coff - p.window + 1));
         const char* Ks = smem + (it % NBUF) * STAGE;
         const char* kb_ = opaque(Ks + rbase);
         const char* vtb = opaque(Ks + KTILE + tbase);
-        f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
+        f32x16_t sacc[NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) sacc[kb] = f32x16_t{};
         // raised priority while issuing the S products: when the other wave
         // of the SIMD is in its softmax, the matrix core gets the issue slot
         // (measured +1%)
@@ -261,17 +266,17 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
 #pragma unroll
         for (int kc = 0; kc < DC; ++kc) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < NKB; ++kb) {
                 const u32x4_t a = row_operand<DK>(kb_, kc, 32 * kb);
                 sacc[kb] = mfma32<T>(a, qf[kc], sacc[kb]);
             }
         }
-        pipe_reads<1, 2 * DC, 4>();
+        pipe_reads<1, NKB * DC, 4>();
         // keep the V^T reads of the P.V phase from being hoisted above the
         // softmax (they would pin 64 registers across it)
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
-        const bool need_mask = skip | (kt + kKT > kv_len) | ((p.causal != 0) & (kt + kKT - 1 > qa + coff)) |
+        const bool need_mask = skip | (kt + KT > kv_len) | ((p.causal != 0) & (kt + KT - 1 > qa + coff)) |
                                ((p.window > 0) & (kt < wq_last + coff - p.window + 1));
         if (need_mask) {
             // (the empty asm keeps this a real branch: speculating the selects
@@ -280,7 +285,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
             const int d0 = kt + 4 * hi - band.lo;
             const uint32_t wdt = skip ? 0u : band.width;
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int c = 32 * kb + 8 * (r >> 2) + (r & 3);    // key - (kt + 4 hi)
@@ -290,10 +295,10 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         }
         // P (rounded to T) as B operands; chunk c covers tile keys
         // 16c + 8(j/4) + 4hi + j%4. The row sum adds the rounded values.
-        u32x4_t pf[4];
+        u32x4_t pf[NPC];
         auto weights = [&](float m_use, float sum) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
+            for (int c = 0; c < NPC; ++c) {
                 const int kb = c >> 1, r0 = 8 * (c & 1);
                 float e[8];
 #pragma unroll
@@ -311,13 +316,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         };
         if (SM == 1) {   // x = s * scale + bias (masked s = -inf stays -inf: scale > 0)
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) sacc[kb][r] = fmaf(sacc[kb][r], p.scale, bv[4 * kb + (r >> 2)][r & 3]);
         }
         if (SM == 2) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const float sv = sacc[kb][r];
@@ -332,7 +337,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         auto update_max = [&](float slack) {
             float mx = kNegInf;
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
             if (raw_max) mx *= cmul;
@@ -362,7 +367,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         }
         // O^T += V^T P^T; V^T operands are transposed reads of the row-major V tile
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < NPC; ++c) {
 #pragma unroll
             for (int db = 0; db < DB; ++db)
                 oacc[db] = mfma32<T>(tr_operand<DVL>(vtb, c, db), pf[c], oacc[db]);
@@ -423,6 +428,18 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     if (DK <= 128 && sm == 1 && g.bias_hs == 0 && p.bias_v4 && g.bias_cols >= 4 && g.bias_cols % 4 == 0 &&
         (QT == 32 || QT == 64) && ((int64_t)QT * g.bias_qs + g.bias_cols) * 4 < ((int64_t)1 << 32))
         brows = QT;
+    if constexpr (DK > 128) {
+        // Without a bias the wide head dims take the whole output in one
+        // launch on 32-key tiles (three 256-wide K + V stages fit the LDS),
+        // instead of recomputing S for each output slice.
+        if (sm == 0) {
+            p.col0 = 0;
+            p.lse = a.lse;
+            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DK, DV, 0, 0, 32>), dim3((unsigned)blocks), dim3(kThreads),
+                               0, st, p);
+            return hipGetLastError();
+        }
+    }
     // DO < DV: one launch per DO-column slice; the first writes the LSE
     for (int c0 = 0; c0 < DV; c0 += DO) {
         p.col0 = c0;
