@@ -84,9 +84,10 @@ __device__ inline void neg_col(float* x, int which) {
 
 // ---------------------------------------------------------------------------
 // dQ.  8 waves (2 per SIMD), 32 query rows x 1 head per wave, the heads of a
-// GQA group packed as in the forward. Key tiles of 64 rows go straight from
-// HBM into a 3-deep LDS ring (K and V row-major, swizzled); K^T operands of
-// the dQ product are transposed LDS reads of the same K tile.
+// GQA group packed as in the forward. Key tiles of 32 * KB rows (64; 128 at
+// D = 64 without a bias; 32 for the 256-wide tiles) go straight from HBM
+// into a 3-deep LDS ring (K and V row-major, swizzled); K^T operands of the
+// dQ product are transposed LDS reads of the same K tile.
 // ---------------------------------------------------------------------------
 // D is the tile width (64, 128 or 256) and DV <= D the head dim, as in the
 // forward. This launch outputs the DO columns from C0 (head dims above 128
@@ -377,10 +378,11 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
 // one stage behind A, so one barrier per stage orders everything. Each wave
 // holds one operand (K or V) and one accumulator set in registers, which keeps
 // both waves of a SIMD resident: one's softmax overlaps the other's MFMAs.
-// A stage is (query head h of the group, 64-query tile): Q, dO, lse and delta
-// go straight from HBM into a 3-deep LDS ring (row-major, swizzled); Q^T and
-// dO^T operands are transposed LDS reads. The loop covers the g heads of the
-// group, so the GQA reduction of dK/dV happens in registers.
+// A stage is (query head h of the group, tile of 32 * NQB queries): Q, lse
+// and delta go straight from HBM into a 3-deep LDS ring, dO into a 2-deep one
+// (row-major, swizzled); Q^T and dO^T operands are transposed LDS reads. The
+// loop covers the g heads of the group, so the GQA reduction of dK/dV
+// happens in registers.
 // ---------------------------------------------------------------------------
 // D is the tile width (64, 128 or 256) and DV <= D the head dim; this launch
 // outputs the DO columns of dK and dV from C0 (several launches above 128,

@@ -6,7 +6,8 @@
 //     query rows of one query head. The workgroup packs `hpw` = gcd(g, 8) query
 //     heads of one GQA group, so every K/V tile staged in LDS serves
 //     hpw * (8 / hpw) * 32 = 256 query-head rows.
-//   * Key tiles of 64 rows go straight from HBM into a 3-deep LDS ring with
+//   * Key tiles of 64 rows (32 for the 256-wide head dims in one launch) go
+//     straight from HBM into a 3-deep LDS ring with
 //     global_load_lds_dwordx4 (no register staging), K and V both row-major
 //     and swizzled; the P.V product reads V^T operands with
 //     ds_read_b64_tr_b16 transposed loads.
