@@ -83,8 +83,9 @@ __device__ inline void neg_col(float* x, int which) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ.  8 waves (2 per SIMD), 32 query rows x 1 head per wave, the heads of a
-// GQA group packed as in the forward. Key tiles of 32 * KB rows (64; 128 at
+// dQ.  8 waves (2 per SIMD; 4 waves, one per SIMD, for the one-launch
+// D = 256 variant), 32 query rows x 1 head per wave, the heads of a GQA group
+// packed as in the forward. Key tiles of 32 * KB rows (64; 128 at
 // D = 64 without a bias; 32 for the 256-wide tiles) go straight from HBM
 // into a 3-deep LDS ring (K and V row-major, swizzled); K^T operands of the
 // dQ product are transposed LDS reads of the same K tile.
@@ -95,24 +96,24 @@ __device__ inline void neg_col(float* x, int which) {
 // accumulators would not fit otherwise). Key tiles hold 32 * KB keys.
 // BROWS > 0: a head-broadcast bias staged in the LDS ring with the K/V tiles
 // (workgroups of BROWS query rows, 64-key tiles), as in the forward.
-template <typename T, int D, int DV, int DO, int C0, int KB, bool BIAS, bool OUT_F32, int BROWS = 0>
-__global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
+template <typename T, int D, int DV, int DO, int C0, int KB, bool BIAS, bool OUT_F32, int BROWS = 0, int NW = kWaves>
+__global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(BwdKParams p) {
     constexpr int DC = (DV + 15) / 16, DB = (DO + 31) / 32;
     constexpr int KT = 32 * KB;               // keys per tile
     static_assert(C0 % 32 == 0 && C0 + DO <= D, "output slice");
     constexpr bool LDSB = BROWS > 0;
-    static_assert(!LDSB || (BIAS && KT == 64), "staged bias: 64-key tiles");
+    static_assert(!LDSB || (BIAS && KT == 64 && NW == 8), "staged bias: 64-key tiles, 8 waves");
     constexpr int TILE = KT * D * 2;
     constexpr int BTILE = BROWS * KT * 4;
     constexpr int STAGE = 2 * TILE + BTILE;   // K, V, staged bias
     constexpr int NBUF = 3;
-    constexpr int LOADS = STAGE / 1024 / kWaves;
+    constexpr int LOADS = STAGE / 1024 / NW;
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
     const int l32 = lane & 31, hi = lane >> 5;
-    const int QT = 32 * (kWaves / p.hpw);
+    const int QT = 32 * (NW / p.hpw);
     const int L = xcd_remap(blockIdx.x, p.n_tiles * p.n_hg);
     const int hg = L / p.n_tiles;
     const int t = p.n_tiles - 1 - (L - hg * p.n_tiles);   // late (heavier) tiles first
@@ -125,7 +126,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     const int q0 = (t - tb) * QT;
     if (q0 >= q_len) return;
 
-    const int wph = kWaves / p.hpw;
+    const int wph = NW / p.hpw;
     const int head = hg * p.hpw + w / wph;
     const int hk = head / p.g;
     const int qa = q0 + 32 * (w % wph);
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdKParams p) {
     const int n_kv_tiles = kv_hi > kv_lo ? (kv_hi - kv_lo + KT - 1) / KT : 0;
     const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * DV;
     const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * DV;
-    TileStager<D, KT, kWaves, DV> kst, vst;
+    TileStager<D, KT, NW, DV> kst, vst;
     kst.init(p.k_rs, w, lane);
     vst.init(p.v_rs, w, lane);
     // staged bias: WG row r is query q0 + r (rows past the end repeat the last)
@@ -860,9 +861,8 @@ BwdKParams make_params(const BwdArgs& a) {
     return p;
 }
 
-template <typename T, int D, int DV, int DO, int C0, int KB, bool OUT_F32>
+template <typename T, int D, int DV, int DO, int C0, int KB, bool OUT_F32, int NW = kWaves>
 hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
-    constexpr int NW = kWaves;
     // the fused delta needs the whole head in one launch
     if (a.delta_out != nullptr && !(C0 == 0 && DO == DV && DV == D && D <= 128)) return hipErrorInvalidValue;
     BwdKParams p = make_params(a);
@@ -874,14 +874,14 @@ hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     // head-broadcast bias staged in LDS: the forward's conditions
     const Geometry& g = a.geo;
-    if (KB == 2 && D <= 128 && g.bias != nullptr && g.bias_hs == 0 && p.bias_v4 && g.bias_cols >= 4 &&
+    if (NW == 8 && KB == 2 && D <= 128 && g.bias != nullptr && g.bias_hs == 0 && p.bias_v4 && g.bias_cols >= 4 &&
         g.bias_cols % 4 == 0 && (QT == 32 || QT == 64) && ((int64_t)QT * g.bias_qs + g.bias_cols) * 4 < ((int64_t)1 << 32)) {
-        if constexpr (KB == 2 && D <= 128) {
+        if constexpr (NW == 8 && KB == 2 && D <= 128) {
             if (QT == 32)
-                hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32, 32>), dim3((unsigned)blocks),
+                hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32, 32, NW>), dim3((unsigned)blocks),
                                    dim3(NW * 64), 0, st, p);
             else
-                hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32, 64>), dim3((unsigned)blocks),
+                hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32, 64, NW>), dim3((unsigned)blocks),
                                    dim3(NW * 64), 0, st, p);
             return hipGetLastError();
         }
@@ -889,11 +889,11 @@ hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     if constexpr (KB > 2) {
         if (a.geo.bias != nullptr) return hipErrorInvalidValue;   // (not dispatched: registers)
     } else if (a.geo.bias != nullptr) {
-        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64),
+        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32, 0, NW>), dim3((unsigned)blocks), dim3(NW * 64),
                            0, st, p);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, false, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64), 0,
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, false, OUT_F32, 0, NW>), dim3((unsigned)blocks), dim3(NW * 64), 0,
                        st, p);
     return hipGetLastError();
 }
@@ -993,10 +993,14 @@ struct DqLaunch {
             return launch_dq_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else {
             // 256-wide tiles: 32-key tiles (three K + V stages fit the LDS).
-            // D = 160 computes the whole output in one launch (249 VGPRs);
-            // D = 256 in two 128-column launches (its Q^T and dO^T fragments
-            // alone take 128 registers; S and dP are recomputed per launch)
+            // D = 160 computes the whole output in one launch (249 VGPRs).
+            // At D = 256 the Q^T and dO^T fragments alone take 128 registers:
+            // without a bias, workgroups of 4 waves (one per SIMD, 512
+            // registers each, the accumulators in AGPRs) compute the whole
+            // output in one launch; with a bias, 8 waves in two 128-column
+            // launches that each recompute S and dP.
             if constexpr (DV > 192) {
+                if (a.geo.bias == nullptr) return launch_dq_typed<T, D, DV, DV, 0, 1, F, 4>(a, st);
                 hipError_t e = launch_dq_typed<T, D, DV, 128, 0, 1, F>(a, st);
                 if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 128, 128, 1, F>(a, st);
                 return e;
