@@ -995,15 +995,10 @@ struct DqLaunch {
             // 256-wide tiles: 32-key tiles (three K + V stages fit the LDS).
             // D = 160 computes the whole output in one launch (249 VGPRs).
             // At D = 256 the Q^T and dO^T fragments alone take 128 registers:
-            // without a bias, workgroups of 4 waves (one per SIMD, 512
-            // registers each, the accumulators in AGPRs) compute the whole
-            // output in one launch; with a bias, 8 waves in two 128-column
-            // launches that each recompute S and dP.
+            // workgroups of 4 waves (one per SIMD, 512 registers each, the
+            // accumulators in AGPRs) compute the whole output in one launch.
             if constexpr (DV > 192) {
-                if (a.geo.bias == nullptr) return launch_dq_typed<T, D, DV, DV, 0, 1, F, 4>(a, st);
-                hipError_t e = launch_dq_typed<T, D, DV, 128, 0, 1, F>(a, st);
-                if (e == hipSuccess) e = launch_dq_typed<T, D, DV, 128, 128, 1, F>(a, st);
-                return e;
+                return launch_dq_typed<T, D, DV, DV, 0, 1, F, 4>(a, st);
             } else {
                 return launch_dq_typed<T, D, DV, DV, 0, 1, F>(a, st);
             }

@@ -65,7 +65,7 @@ struct FwdKParams {
 // instead of every wave loading its rows from global memory.
 template <typename T, int DK, int DV, int DVL, int DO, int SM, int BROWS = 0, int KT = kKT>
 __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
-    static_assert(KT == 64 || (KT == 32 && SM == 0), "32-key tiles: unbiased only");
+    static_assert(KT == 64 || (KT == 32 && BROWS == 0), "32-key tiles: no staged bias");
     constexpr int NKB = KT / 32;             // 32-key blocks per tile
     constexpr int NPC = KT / 16;             // 16-key P chunks per tile
     constexpr bool BIAS = SM != 0;
@@ -181,11 +181,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     auto load_bias = [&](int kt, f32x4_t (&bv)[8]) {
         if (kt + KT <= p.bias_cols && p.bias_v4) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < 4 * NKB; ++i)
                 bv[i] = *reinterpret_cast<const f32x4_t*>(brow + kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi);
         } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < 4 * NKB; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int key = kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi + j;
@@ -430,12 +430,25 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
         (QT == 32 || QT == 64) && ((int64_t)QT * g.bias_qs + g.bias_cols) * 4 < ((int64_t)1 << 32))
         brows = QT;
     if constexpr (DK > 128) {
-        // Without a bias the wide head dims take the whole output in one
-        // launch on 32-key tiles (three 256-wide K + V stages fit the LDS),
-        // instead of recomputing S for each output slice.
-        if (sm == 0) {
+        // The wide head dims take the whole output in one launch on 32-key
+        // tiles (three 256-wide K + V stages fit the LDS), instead of
+        // recomputing S for each output slice; a bias is loaded per row.
+        // (D = 256 with a bias keeps the slices: one launch would spill.)
+        if (sm == 0 || DV <= 192) {
             p.col0 = 0;
             p.lse = a.lse;
+            if constexpr (DV <= 192) {
+                if (sm == 2) {
+                    hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DK, DV, 2, 0, 32>), dim3((unsigned)blocks),
+                                       dim3(kThreads), 0, st, p);
+                    return hipGetLastError();
+                }
+                if (sm == 1) {
+                    hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DK, DV, 1, 0, 32>), dim3((unsigned)blocks),
+                                       dim3(kThreads), 0, st, p);
+                    return hipGetLastError();
+                }
+            }
             hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DK, DV, 0, 0, 32>), dim3((unsigned)blocks), dim3(kThreads),
                                0, st, p);
             return hipGetLastError();
