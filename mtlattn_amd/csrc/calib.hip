@@ -90,10 +90,18 @@ __global__ __launch_bounds__(256) void calib_read_kernel(const u32x4_t* __restri
 //     independent accumulators
 //   4 the same with the accumulators in AGPRs
 //   5 ds_read_b128: 16 reads (16 KB per wave) in flight, then a wait
+//   6 one wave interleaving both: role 3's 8 MFMAs, each followed by two
+//     v_exp_f32 and two v_fmac_f32 of independent chains
+//   7 the same with four v_exp_f32 after each MFMA
+//   8 role 6 with the MFMA's first operand read from LDS (ds_read_b128 four
+//     MFMAs ahead, s_waitcnt lgkmcnt(3) before each MFMA)
+//   9 role 6 with the attention softmax's dependences: per MFMA two
+//     v_fma_f32 -> v_exp_f32 pairs, one v_cvt_pk_bf16_f32 of the previous
+//     pair and one v_dot2c_f32_bf16 row-sum step on the pair before that
 // The instructions are inline asm so that their number and order are
 // exactly these. Each wave records its s_memtime cycles (shader clock) and
 // s_memrealtime ticks (100 MHz).
-constexpr int kRateOps[6] = {0, 16, 16, 8, 8, 16};
+constexpr int kRateOps[10] = {0, 16, 16, 8, 8, 16, 8, 8, 8, 8};   // roles 6-9: MFMAs
 
 __device__ float rate_role(int role, int iters, int lane, const char* lds) {
     float x[18];
@@ -129,6 +137,79 @@ __device__ float rate_role(int role, int iters, int lane, const char* lds) {
                 asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c2) : "v"(a), "v"(b));
                 asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c3) : "v"(a), "v"(b));
             }
+    } else if (role == 6) {
+        for (int i = 0; i < iters; ++i)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    f32x16_t& c = m == 0 ? c0 : m == 1 ? c1 : m == 2 ? c2 : c3;
+                    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+                    const int j = 4 * m + 2 * u;
+                    asm volatile("v_exp_f32 %0, %0" : "+v"(x[j]));
+                    asm volatile("v_exp_f32 %0, %0" : "+v"(x[j + 1]));
+                    asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(x[(j + 8) & 15]) : "v"(x[16]), "v"(x[17]));
+                    asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(x[(j + 9) & 15]) : "v"(x[16]), "v"(x[17]));
+                }
+    } else if (role == 7) {
+        for (int i = 0; i < iters; ++i)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    f32x16_t& c = m == 0 ? c0 : m == 1 ? c1 : m == 2 ? c2 : c3;
+                    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+                    const int j = 4 * m + 2 * u;
+                    asm volatile("v_exp_f32 %0, %0" : "+v"(x[j]));
+                    asm volatile("v_exp_f32 %0, %0" : "+v"(x[j + 1]));
+                    asm volatile("v_exp_f32 %0, %0" : "+v"(x[(j + 8) & 15]));
+                    asm volatile("v_exp_f32 %0, %0" : "+v"(x[(j + 9) & 15]));
+                }
+    } else if (role == 8) {
+        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
+        // operand g of 8 rotating registers: KB (g & 7) + lane chunk, every
+        // address a multiple of 16 below 8 KB
+        auto rd = [&](int g) { return base + (uint32_t)(((g & 7) * 1024 + lane * 16) & 8191); };
+#pragma unroll
+        for (int g = 0; g < 4; ++g) asm volatile("ds_read_b128 %0, %1" : "=v"(r[g]) : "v"(rd(g)) : "memory");
+        for (int i = 0; i < iters; ++i)
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                f32x16_t& c = (g & 3) == 0 ? c0 : (g & 3) == 1 ? c1 : (g & 3) == 2 ? c2 : c3;
+                asm volatile("s_waitcnt lgkmcnt(3)" ::: "memory");
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(r[g]), "v"(b));
+                asm volatile("ds_read_b128 %0, %1" : "=v"(r[(g + 4) & 7]) : "v"(rd(g + 4)) : "memory");
+                const int j = 2 * g;
+                asm volatile("v_exp_f32 %0, %0" : "+v"(x[j]));
+                asm volatile("v_exp_f32 %0, %0" : "+v"(x[j + 1]));
+                asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(x[(j + 8) & 15]) : "v"(x[16]), "v"(x[17]));
+                asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(x[(j + 9) & 15]) : "v"(x[16]), "v"(x[17]));
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    } else if (role == 9) {
+        float e[16], sum = 0.f;
+        uint32_t pk[8];
+        const uint32_t ones = 0x3f803f80u;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) e[j] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pk[j] = 0u;
+        for (int i = 0; i < iters; ++i)
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                f32x16_t& c = (g & 3) == 0 ? c0 : (g & 3) == 1 ? c1 : (g & 3) == 2 ? c2 : c3;
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+                const int j = 2 * g;
+                float t0, t1;
+                asm volatile("v_fma_f32 %0, %1, %2, %3" : "=v"(t0) : "v"(x[j]), "v"(x[16]), "v"(x[17]));
+                asm volatile("v_exp_f32 %0, %1" : "=v"(e[j]) : "v"(t0));
+                asm volatile("v_fma_f32 %0, %1, %2, %3" : "=v"(t1) : "v"(x[j + 1]), "v"(x[16]), "v"(x[17]));
+                asm volatile("v_exp_f32 %0, %1" : "=v"(e[j + 1]) : "v"(t1));
+                const int pj = (j + 14) & 15;   // the previous pair
+                asm volatile("s_nop 0\n\tv_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(pk[g]) : "v"(e[pj]), "v"(e[pj + 1]));
+                asm volatile("v_dot2c_f32_bf16 %0, %1, %2" : "+v"(sum) : "v"(ones), "v"(pk[(g + 7) & 7]));
+            }
+        x[0] += sum;
     } else if (role == 5) {
         const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
         for (int i = 0; i < iters; ++i) {
@@ -157,7 +238,7 @@ __global__ __launch_bounds__(512, 1) void calib_rates_kernel(int ra, int rb, int
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int i = threadIdx.x; i < 32768 / 4; i += 512) reinterpret_cast<uint32_t*>(lds)[i] = (uint32_t)i * 0x9e3779b9u;
     __syncthreads();
-    const int role = w < 4 ? ra : rb;
+    const int role = __builtin_amdgcn_readfirstlane(w < 4 ? ra : rb);   // wave-uniform
     const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
     const float s = role ? rate_role(role, iters, lane, lds) : 0.f;
     const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
@@ -195,10 +276,10 @@ int mtlattn_calib_read(const void* src, int64_t bytes, int blocks, uint32_t* sin
 // sink: blocks * 512 floats; cyc: blocks * 8 * 2 u64 (per wave: shader
 // cycles, 100 MHz ticks). Operations per iteration of role r: ops_per_iter.
 int mtlattn_calib_rates(int ra, int rb, int iters, int blocks, float* sink, unsigned long long* cyc, void* stream) {
-    if (ra < 0 || ra > 5 || rb < 0 || rb > 5 || iters < 1 || blocks < 1) return (int)hipErrorInvalidValue;
+    if (ra < 0 || ra > 9 || rb < 0 || rb > 9 || iters < 1 || blocks < 1) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(calib_rates_kernel, dim3(blocks), dim3(512), 0, (hipStream_t)stream, ra, rb, iters, sink, cyc);
     return (int)hipGetLastError();
 }
-int mtlattn_calib_rate_ops(int role) { return role >= 0 && role <= 5 ? kRateOps[role] : 0; }
+int mtlattn_calib_rate_ops(int role) { return role >= 0 && role <= 9 ? kRateOps[role] : 0; }
 
 }  // extern "C"
