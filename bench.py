@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1/C2/C4 lines")
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured-ceiling kernels")
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "peaks", "rates"], default=None,
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c4nb", "c5", "copy", "peaks", "rates"], default=None,
                     help="run one workload (or the 1 GiB copy used to calibrate HBM byte counters) "
                          "and print only its timing: the short program profilers wrap")
     return ap.parse_args()
@@ -213,6 +213,9 @@ def bench_configs(args, only=None):
         ("C4", "bf16 4x16384, Hq=32, Hkv=8, D=128, causal, window 4096, fp32 bias [65536,1,16384] = -(i-j)/16",
          [16384] * 4, 32, 8, 128, torch.bfloat16, True, 4096, True),
     ]
+    if only == "C4NB":   # C4's shape without the bias (for the bias's cost; not a bench line)
+        cfgs = [("C4NB", "bf16 4x16384, Hq=32, Hkv=8, D=128, causal, window 4096, no bias", [16384] * 4, 32, 8, 128,
+                 torch.bfloat16, True, 4096, False)]
     out = {}
     for name, desc, lens, hq, hkv, d, dt, causal, window, with_bias in cfgs:
         if only is not None and name != only:
@@ -595,7 +598,7 @@ def main():
         dec = bench_c5(args)
         print(json.dumps({"c5_ms": dec["ms"], "GBps": dec["GBps"]}), flush=True)
         return
-    if args.only in ("c1", "c2", "c4"):
+    if args.only in ("c1", "c2", "c4", "c4nb"):
         print(json.dumps(bench_configs(args, args.only.upper())), flush=True)
         return
     if args.only == "peaks":
