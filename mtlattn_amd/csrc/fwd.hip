@@ -10,7 +10,9 @@
 //     straight from HBM into a 3-deep LDS ring with
 //     global_load_lds_dwordx4 (no register staging), K and V both row-major
 //     and swizzled; the P.V product reads V^T operands with
-//     ds_read_b64_tr_b16 transposed loads.
+//     ds_read_b64_tr_b16 transposed loads. Without a bias, each wave's loads
+//     of tile i + 2 are issued one at a time between its S products of
+//     tile i rather than all at once after the tile barrier.
 //   * Per wave and key tile:  S^T = K Q^T  (v_mfma_f32_32x32x16, 2 x D/16
 //     instructions), online softmax in base 2 on the C registers (each lane
 //     holds one query column, so max/sum need one cross-half exchange), then
@@ -20,6 +22,8 @@
 //     sliding-window cost is O(W) (src/attn_mpp.metal:216-225).
 //   * Varlen tiles are numbered without a host sync (common.h), blocks are
 //     remapped so neighbouring query tiles of one (sequence, head) share an XCD.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 #include "../../include/mtlattn_capi.h"
@@ -225,7 +229,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         // the buffer of tile it + 2 was last read in iteration it - 1 (with a
         // bias, the tile loads go out after the bias is consumed: the bias
         // loads' wait would otherwise also wait for them)
-        if (!reg_bias && it + 2 < n_kv_tiles) stage(it + 2);
+        // Without a bias, the loads of tile it + 2 go out one by one between
+        // the S products below instead of in a burst here, where every wave
+        // of the CU would queue its loads at the same moment (not at D = 256
+        // in one launch: its O and Q registers leave no room for the operand
+        // reads held ahead).
+        constexpr bool SPREAD = SM == 0 && DB * 16 + DC * 4 <= 160;
+        if (!SPREAD && !reg_bias && it + 2 < n_kv_tiles) stage(it + 2);
         const int kt = kv_lo + it * KT;
         f32x4_t bv[8];
         if (reg_bias) load_bias(kt, bv);
@@ -264,15 +274,73 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         // of the SIMD is in its softmax, the matrix core gets the issue slot
         // (measured +1%)
         __builtin_amdgcn_s_setprio(1);
+        if constexpr (SPREAD) {
+            // One group per S product: the MFMA, the operand read four
+            // products ahead and, at evenly spaced products, one of this
+            // wave's tile loads; groups are kept in this order by scheduling
+            // barriers (the loads' memory clobber would otherwise stop the
+            // reads from being issued ahead of them).
+            constexpr int NS = NKB * DC;
+            constexpr int LK = decltype(kst)::N, LV = decltype(vst)::N, NL = LK + LV;
+            static_assert(decltype(kst)::PER % kWaves == 0 && decltype(vst)::PER % kWaves == 0 && NL <= NS,
+                          "whole loads per wave");
+            const bool load_next = it + 2 < n_kv_tiles;
+            const int kt2 = kt + 2 * KT;
+            char* buf2 = smem + ((it + 2) % NBUF) * STAGE;
+            const char* ksrc = reinterpret_cast<const char*>(kbase + (int64_t)kt2 * p.k_rs);
+            const char* vsrc = reinterpret_cast<const char*>(vbase + (int64_t)kt2 * p.v_rs);
+            uint32_t lo[NL];   // per-lane source offsets (rows past the end read the last row)
+            if (kv_len - kt2 >= KT) {
 #pragma unroll
-        for (int kc = 0; kc < DC; ++kc) {
+                for (int j = 0; j < LK; ++j) lo[j] = kst.off[j];
 #pragma unroll
-            for (int kb = 0; kb < NKB; ++kb) {
-                const u32x4_t a = row_operand<DK>(kb_, kc, 32 * kb);
-                sacc[kb] = mfma32<T>(a, qf[kc], sacc[kb]);
+                for (int j = 0; j < LV; ++j) lo[LK + j] = vst.off[j];
+            } else {
+                const int rmax = max(kv_len - kt2 - 1, 0);
+#pragma unroll
+                for (int j = 0; j < LK; ++j) {
+                    const int i = w + j * kWaves;
+                    lo[j] = decltype(kst)::lane_off(i, lane, min(decltype(kst)::row_of(i, lane), rmax),
+                                                    (uint32_t)(2 * p.k_rs));
+                }
+#pragma unroll
+                for (int j = 0; j < LV; ++j) {
+                    const int i = w + j * kWaves;
+                    lo[LK + j] = decltype(vst)::lane_off(i, lane, min(decltype(vst)::row_of(i, lane), rmax),
+                                                         (uint32_t)(2 * p.v_rs));
+                }
             }
+            auto products = [&](auto with_loads) {
+                u32x4_t ka[NS];
+#pragma unroll
+                for (int i = 0; i < 4 && i < NS; ++i) ka[i] = row_operand<DK>(kb_, i / NKB, 32 * (i % NKB));
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    sacc[i % NKB] = mfma32<T>(ka[i], qf[i / NKB], sacc[i % NKB]);
+                    if (i + 4 < NS) ka[i + 4] = row_operand<DK>(kb_, (i + 4) / NKB, 32 * ((i + 4) % NKB));
+                    if (decltype(with_loads)::value && i % (NS / NL) == 1 % (NS / NL) && i / (NS / NL) < NL) {
+                        const int j = i / (NS / NL);
+                        const int row = w + (j < LK ? j : j - LK) * kWaves;   // 1 KB instruction of the tile
+                        if (j < LK) lds_dma16s(ksrc, lo[j], buf2 + row * 1024);
+                        else lds_dma16s(vsrc, lo[j], buf2 + KTILE + row * 1024);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            };
+            if (load_next) products(std::integral_constant<bool, true>{});
+            else products(std::integral_constant<bool, false>{});
+        } else {
+#pragma unroll
+            for (int kc = 0; kc < DC; ++kc) {
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) {
+                    const u32x4_t a = row_operand<DK>(kb_, kc, 32 * kb);
+                    sacc[kb] = mfma32<T>(a, qf[kc], sacc[kb]);
+                }
+            }
+            pipe_reads<1, NKB * DC, 4>();
         }
-        pipe_reads<1, NKB * DC, 4>();
         // keep the V^T reads of the P.V phase from being hoisted above the
         // softmax (they would pin 64 registers across it)
         __builtin_amdgcn_sched_barrier(0);
