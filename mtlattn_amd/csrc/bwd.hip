@@ -23,7 +23,9 @@
 //   S = Q K^T, P, dV^T += dO^T P; wave B, one stage behind: dP = dO V^T,
 //   dS = P (dP - delta) with P handed over through LDS, dK^T += Q^T dS.
 //   Causal and window bands skip whole query blocks (the reference skips
-//   causal only, src/attn_mpp.metal:591).
+//   causal only, src/attn_mpp.metal:591). At head dims <= 64 without a bias
+//   a variant runs 4-wave workgroups (two per CU) in which every wave
+//   computes all four products for its own 32 keys.
 #include "common.h"
 #include "kernels.h"
 #include "../../include/mtlattn_capi.h"
@@ -766,6 +768,250 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// dK/dV at head dims <= 64 without a bias: every wave computes all four
+// products for its own 32 keys -- S = Q K^T, P, dV^T += dO^T P,
+// dP = dO V^T, dS = P (dP - delta), dK^T += Q^T dS -- so nothing passes
+// between waves. A wave's dK and dV accumulators take 64 registers at
+// D = 64, which leaves room at 2 waves per SIMD; at D = 128 they would not
+// fit, and the wave-pair kernel above splits the products between two
+// waves instead. Workgroups of NW = 4 waves (128 keys), two per CU: the two
+// waves of a SIMD belong to different workgroups, so their tile barriers do
+// not hold them in step (measured 5-8% faster than 8-wave workgroups at
+// D = 64, which stage each Q / dO tile for 256 keys but keep both waves of
+// a SIMD in step). The arithmetic is that of the wave-pair kernel (P
+// rounded to T, dP accumulated onto -delta, dS = P * (dP - delta) rounded
+// to T), visited in 64-query stages.
+// ---------------------------------------------------------------------------
+template <typename T, int D, int DV, bool OUT_F32, int NW>
+__global__ __launch_bounds__(NW * 64, kWaves / NW) void bwd_dkv_sym_kernel(BwdKParams p) {
+    static_assert(D == 64, "64-wide tiles");
+    constexpr int NQB = 2;
+    constexpr int DC = (DV + 15) / 16, DB = (DV + 31) / 32;
+    constexpr int QTL = 32 * NQB;                       // queries per stage
+    constexpr int KB = NW * kKW;                        // keys per workgroup
+    constexpr int TILE = QTL * D * 2;
+    constexpr int SLOT = (2 * TILE + 2 * QTL * 4 + 1023) / 1024 * 1024;   // Q, dO, lse, delta
+    constexpr int NBUF = 2;
+    __shared__ __attribute__((aligned(1024))) char smem[NBUF * SLOT];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int L = xcd_remap(blockIdx.x, p.n_tiles * p.hkv);
+    const int hk = L / p.n_tiles;
+    const int t = L - hk * p.n_tiles;                  // early key blocks (heavier when causal) first
+    const int s = find_seq_for_tile(p.cu_kv, p.num_seqs, KB, t, p.total_kv);
+    const int tb = tile_base(p.cu_kv, s, KB, p.total_kv);
+    if (t < tb) return;
+    const SeqRange qr = seq_range(p.cu_q, s, p.total_q);
+    const SeqRange kr = seq_range(p.cu_kv, s, p.total_kv);
+    const int q_len = qr.end - qr.start, kv_len = kr.end - kr.start;
+    const int k0 = (t - tb) * KB;
+    if (k0 >= kv_len) return;
+    const int coff = kv_len - q_len;
+
+    const int kw = k0 + kKW * w;                 // first key of this wave (seq-local)
+    const bool wave_active = kw < kv_len;
+    const int wk_last = min(kv_len, kw + kKW) - 1;
+    const int key = kw + l32;                    // this lane's key column
+    const bool key_ok = key < kv_len;
+
+    // B operands of the S and dP products: K^T and V^T, lane = key,
+    // d = 16 kc + 8 hi + j (rows past the end read the last key: masked)
+    u32x4_t kf[DC], vf[DC];
+    {
+        const int64_t grow = kr.start + min(key, kv_len - 1);
+        const uint16_t* kp = p.k + grow * p.k_rs + (int64_t)hk * DV + 8 * hi;
+        const uint16_t* vp = p.v + grow * p.v_rs + (int64_t)hk * DV + 8 * hi;
+#pragma unroll
+        for (int kc = 0; kc < DC; ++kc) {   // columns past DV are zero
+            const bool in = DV % 16 == 0 || 16 * kc + 8 * hi < DV;
+            kf[kc] = in ? ld16(kp + 16 * kc) : u32x4_t{};
+            vf[kc] = in ? ld16(vp + 16 * kc) : u32x4_t{};
+        }
+    }
+
+    // Query tiles that can see any key of the workgroup, visited top-down
+    // with the GQA group's heads inner (as in the wave-pair kernel).
+    const int k_last_wg = min(kv_len, k0 + KB) - 1;
+    const int q_lo = p.causal ? max(0, k0 - coff) / QTL * QTL : 0;
+    const int q_hi = p.window > 0 ? min(q_len, k_last_wg - coff + p.window) : q_len;
+    const int n_q_tiles = q_hi > q_lo ? (q_hi - q_lo + QTL - 1) / QTL : 0;
+    const int n_stages = n_q_tiles * p.g;
+    const int qt_first = q_lo + (n_q_tiles - 1) * QTL;
+
+    // Direct loads of a stage: the Q and dO tiles by all NW waves, the lse
+    // column by wave 0 and the delta column by wave 1 (one row per lane).
+    TileStager<D, QTL, NW, DV> qst, dost;
+    qst.init(p.q_rs, w, lane);
+    dost.init(p.do_rs, w, lane);
+    int ld_hl = 0, ld_qt = qt_first, ld_slot = 0;
+    const uint16_t* ld_q = p.q + (int64_t)(qr.start + qt_first) * p.q_rs + (int64_t)hk * p.g * DV;
+    const uint16_t* ld_do = p.dout + (int64_t)(qr.start + qt_first) * p.do_rs + (int64_t)hk * p.g * DV;
+    const float* ld_l = (w == 0 ? p.lse : p.delta) + (int64_t)(qr.start + qt_first) * p.hq + hk * p.g;
+    const int64_t q_wrap = -(int64_t)(p.g - 1) * DV - (int64_t)QTL * p.q_rs;
+    const int64_t do_wrap = -(int64_t)(p.g - 1) * DV - (int64_t)QTL * p.do_rs;
+    const int64_t l_wrap = -(int64_t)(p.g - 1) - (int64_t)QTL * p.hq;
+    const uint32_t l_voff = (uint32_t)lane * (uint32_t)p.hq * 4u;
+    auto stage = [&]() {
+        char* buf = smem + ld_slot * SLOT;
+        const int avail = q_len - ld_qt;                    // >= 1
+        qst.issue_at(buf, ld_q, p.q_rs, avail, w, lane);
+        dost.issue_at(buf + TILE, ld_do, p.do_rs, avail, w, lane);
+        if (w < 2) {   // rows past the end repeat the last row (masked)
+            const uint32_t voff = avail >= QTL ? l_voff : (uint32_t)min(lane, avail - 1) * (uint32_t)p.hq * 4u;
+            lds_dma4s(ld_l, voff, buf + 2 * TILE + w * QTL * 4);
+        }
+        ld_slot ^= 1;
+        if (++ld_hl == p.g) {
+            ld_hl = 0;
+            ld_qt -= QTL;
+            ld_q += q_wrap;
+            ld_do += do_wrap;
+            ld_l += l_wrap;
+        } else {
+            ld_q += DV;
+            ld_do += DV;
+            ld_l += 1;
+        }
+    };
+
+    int c_hl = 0, c_qt = qt_first, c_slot = 0;
+    const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
+    const float c2 = p.scale_log2;
+    f32x16_t accv[DB], acck[DB];                 // dV^T, dK^T
+#pragma unroll
+    for (int db = 0; db < DB; ++db) accv[db] = acck[db] = f32x16_t{};
+
+    // masking tests, as in the wave-pair kernel (for this wave's keys)
+    auto block_needs_mask = [&](int qb) {
+        const int qf0 = c_qt + 32 * qb;
+        const int qf1 = min(q_len, qf0 + 32) - 1;
+        return (kw + kKW > kv_len) | (qf0 + 32 > q_len) | ((p.causal != 0) & (wk_last > qf0 + coff)) |
+               ((p.window > 0) & (kw < qf1 + coff - p.window + 1));
+    };
+    auto stage_needs_mask = [&]() {
+        return (kw + kKW > kv_len) | (c_qt + QTL > q_len) | ((p.causal != 0) & (wk_last > c_qt + coff)) |
+               ((p.window > 0) & (kw < min(q_len, c_qt + QTL) + coff - p.window));
+    };
+    const Band band = query_band(key, coff, q_len, kv_len, p.causal, p.window);
+
+    if (n_stages > 0) {
+        stage();
+        wait_vmcnt<0>();
+        if (w < 2) neg_col(reinterpret_cast<float*>(smem + 2 * TILE) + w * QTL + lane, w);
+        __syncthreads();
+    }
+    for (int st = 0; st < n_stages; ++st) {
+        // the other slot was read in the previous stage, which every wave
+        // has finished (barrier below)
+        if (st + 1 < n_stages) stage();
+        const char* Qs = smem + c_slot * SLOT;
+        const char* Ds = Qs + TILE;
+        const float* ls = reinterpret_cast<const float*>(Qs + 2 * TILE);   // -lse log2(e)
+        const float* dls = ls + QTL;                                         // -delta
+        const char* qrb = opaque(Qs + rbase);
+        const char* drb = opaque(Ds + rbase);
+        const int qt = c_qt;
+        f32x16_t sacc[NQB], pacc[NQB];
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) sacc[qb] = f32x16_t{};
+#pragma unroll
+        for (int kc = 0; kc < DC; ++kc)
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) sacc[qb] = mfma32<T>(row_operand<D>(qrb, kc, 32 * qb), kf[kc], sacc[qb]);
+        // dP - delta: the products accumulate onto -delta
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb)
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(dls + 32 * qb + 8 * rg + 4 * hi);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) pacc[qb][4 * rg + e] = d4[e];
+            }
+#pragma unroll
+        for (int kc = 0; kc < DC; ++kc)
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) pacc[qb] = mfma32<T>(row_operand<D>(drb, kc, 32 * qb), vf[kc], pacc[qb]);
+        // P (rows with no allowed key have lse = -inf: P = 0)
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb)
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(ls + 32 * qb + 8 * rg + 4 * hi);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    sacc[qb][4 * rg + e] = __builtin_amdgcn_exp2f(fmaf(sacc[qb][4 * rg + e], c2, l4[e]));
+            }
+        if (stage_needs_mask()) {
+            asm volatile("");
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) {
+                if (block_needs_mask(qb)) {   // out-of-band elements -> P = 0
+                    asm volatile("");
+                    const int d0 = qt + 32 * qb + 4 * hi - band.lo;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        sacc[qb][r] = (uint32_t)(d0 + 8 * (r >> 2) + (r & 3)) < band.width ? sacc[qb][r] : 0.f;
+                }
+            }
+        }
+        const char* dtb = opaque(Ds + tbase);
+        const char* qtb = opaque(Qs + tbase);
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                const int r0 = 8 * cc;
+                const u32x4_t bp = u32x4_t{T::pack2(sacc[qb][r0 + 0], sacc[qb][r0 + 1]),
+                                           T::pack2(sacc[qb][r0 + 2], sacc[qb][r0 + 3]),
+                                           T::pack2(sacc[qb][r0 + 4], sacc[qb][r0 + 5]),
+                                           T::pack2(sacc[qb][r0 + 6], sacc[qb][r0 + 7])};
+#pragma unroll
+                for (int db = 0; db < DB; ++db) accv[db] = mfma32<T>(tr_operand<D>(dtb, 2 * qb + cc, db), bp, accv[db]);
+                float dsv[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float pr = (j & 1) ? hi16<T>(bp[j >> 1]) : lo16<T>(bp[j >> 1]);
+                    dsv[j] = pr * pacc[qb][r0 + j];
+                }
+                const u32x4_t bs = u32x4_t{T::pack2(dsv[0], dsv[1]), T::pack2(dsv[2], dsv[3]),
+                                           T::pack2(dsv[4], dsv[5]), T::pack2(dsv[6], dsv[7])};
+#pragma unroll
+                for (int db = 0; db < DB; ++db) acck[db] = mfma32<T>(tr_operand<D>(qtb, 2 * qb + cc, db), bs, acck[db]);
+            }
+        }
+        // the next stage landed for this wave; the lse / delta loaders turn
+        // their columns into -lse log2 e and -delta before the barrier
+        // publishes it
+        wait_vmcnt<0>();
+        if (w < 2 && st + 1 < n_stages) neg_col(reinterpret_cast<float*>(smem + (c_slot ^ 1) * SLOT + 2 * TILE) + w * QTL + lane, w);
+        __syncthreads();
+        c_slot ^= 1;
+        if (++c_hl == p.g) {
+            c_hl = 0;
+            c_qt -= QTL;
+        }
+    }
+
+    if (wave_active && key_ok) {
+        const int64_t off = (int64_t)(kr.start + key) * ((int64_t)p.hkv * DV) + (int64_t)hk * DV;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const int d = 32 * db + 8 * rg + 4 * hi;
+                if (DV % 32 != 0 && d >= DV) continue;
+                store4<T, OUT_F32>(p.dv, off + d, accv[db][4 * rg], accv[db][4 * rg + 1], accv[db][4 * rg + 2],
+                                   accv[db][4 * rg + 3]);
+                store4<T, OUT_F32>(p.dk, off + d, acck[db][4 * rg] * p.scale, acck[db][4 * rg + 1] * p.scale,
+                                   acck[db][4 * rg + 2] * p.scale, acck[db][4 * rg + 3] * p.scale);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // delta = rowsum(dO * O). 16-bit types with D % 8 == 0 (D <= 512): one wave
 // per row; a head's D / 8 sixteen-byte chunks go to a group of lg lanes (the
 // next power of two, so groups never straddle), 64 / lg heads per pass, and
@@ -917,6 +1163,16 @@ hipError_t launch_dkv_typed(const BwdArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <typename T, int D, int DV, bool OUT_F32, int NW>
+hipError_t launch_dkv_sym(const BwdArgs& a, hipStream_t st) {
+    BwdKParams p = make_params(a);
+    p.n_tiles = (int)(a.geo.total_kv / (NW * kKW)) + a.geo.num_seqs + 1;
+    const int64_t blocks = (int64_t)p.n_tiles * a.geo.hkv;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((bwd_dkv_sym_kernel<T, D, DV, OUT_F32, NW>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, p);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_bwd_preprocess(int dtype, const Geometry& geo, const void* o, int64_t o_rs,
@@ -1009,9 +1265,9 @@ template <typename T, int D, int DV, bool F>
 struct DkvLaunch {
     static hipError_t run(const BwdArgs& a, hipStream_t st) {
         if constexpr (D <= 64) {
-            // 128-query stages without a bias (twice the MFMAs per stage's
-            // fixed cost; the bias of a 128-query stage would not fit)
-            if (a.geo.bias == nullptr) return launch_dkv_typed<T, D, DV, DV, 0, 4, F>(a, st);
+            // without a bias: every wave computes all four products for its
+            // keys, 4-wave workgroups
+            if (a.geo.bias == nullptr) return launch_dkv_sym<T, D, DV, F, 4>(a, st);
             return launch_dkv_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else if constexpr (D <= 128) {
             return launch_dkv_typed<T, D, DV, DV, 0, 2, F>(a, st);
