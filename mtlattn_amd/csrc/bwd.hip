@@ -85,12 +85,14 @@ __device__ inline void neg_col(float* x, int which) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ.  8 waves (2 per SIMD; 4 waves, one per SIMD, for the one-launch
-// D = 256 variant), 32 query rows x 1 head per wave, the heads of a GQA group
-// packed as in the forward. Key tiles of 32 * KB rows (64; 128 at
-// D = 64 without a bias; 32 for the 256-wide tiles) go straight from HBM
-// into a 3-deep LDS ring (K and V row-major, swizzled); K^T operands of the
-// dQ product are transposed LDS reads of the same K tile.
+// dQ.  8 waves (2 per SIMD), 32 query rows x 1 head per wave, the heads of a
+// GQA group packed as in the forward; without a bias at D = 64 (and at
+// D = 128 without GQA) workgroups of 4 waves, two per CU; at D = 256 one
+// workgroup of 4 waves per CU (one per SIMD, 512 registers each). Key tiles
+// of 32 * KB rows (64; 32 for the 256-wide tiles and the 4-wave D = 128
+// variant) go straight from HBM into a 3-deep LDS ring (K and V row-major,
+// swizzled); K^T operands of the dQ product are transposed LDS reads of the
+// same K tile.
 // ---------------------------------------------------------------------------
 // D is the tile width (64, 128 or 256) and DV <= D the head dim, as in the
 // forward. This launch outputs the DO columns from C0 (head dims above 128
@@ -98,8 +100,9 @@ __device__ inline void neg_col(float* x, int which) {
 // accumulators would not fit otherwise). Key tiles hold 32 * KB keys.
 // BROWS > 0: a head-broadcast bias staged in the LDS ring with the K/V tiles
 // (workgroups of BROWS query rows, 64-key tiles), as in the forward.
-template <typename T, int D, int DV, int DO, int C0, int KB, bool BIAS, bool OUT_F32, int BROWS = 0, int NW = kWaves>
-__global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(BwdKParams p) {
+template <typename T, int D, int DV, int DO, int C0, int KB, bool BIAS, bool OUT_F32, int BROWS = 0, int NW = kWaves,
+          int OCC = 1>
+__global__ __launch_bounds__(NW * 64, OCC) void bwd_dq_kernel(BwdKParams p) {
     constexpr int DC = (DV + 15) / 16, DB = (DO + 31) / 32;
     constexpr int KT = 32 * KB;               // keys per tile
     static_assert(C0 % 32 == 0 && C0 + DO <= D, "output slice");
@@ -1107,7 +1110,7 @@ BwdKParams make_params(const BwdArgs& a) {
     return p;
 }
 
-template <typename T, int D, int DV, int DO, int C0, int KB, bool OUT_F32, int NW = kWaves>
+template <typename T, int D, int DV, int DO, int C0, int KB, bool OUT_F32, int NW = kWaves, int OCC = 1>
 hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     // the fused delta needs the whole head in one launch
     if (a.delta_out != nullptr && !(C0 == 0 && DO == DV && DV == D && D <= 128)) return hipErrorInvalidValue;
@@ -1135,11 +1138,11 @@ hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     if constexpr (KB > 2) {
         if (a.geo.bias != nullptr) return hipErrorInvalidValue;   // (not dispatched: registers)
     } else if (a.geo.bias != nullptr) {
-        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32, 0, NW>), dim3((unsigned)blocks), dim3(NW * 64),
+        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32, 0, NW, OCC>), dim3((unsigned)blocks), dim3(NW * 64),
                            0, st, p);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, false, OUT_F32, 0, NW>), dim3((unsigned)blocks), dim3(NW * 64), 0,
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, false, OUT_F32, 0, NW, OCC>), dim3((unsigned)blocks), dim3(NW * 64), 0,
                        st, p);
     return hipGetLastError();
 }
@@ -1239,13 +1242,18 @@ template <typename T, int D, int DV, bool F>
 struct DqLaunch {
     static hipError_t run(const BwdArgs& a, hipStream_t st) {
         if constexpr (D <= 64) {
-            // 128-key tiles without a bias: at D = 64 a 64-key tile is half
-            // the MFMAs of the D = 128 one against the same per-tile overhead
-            // (barrier, staging and wait bookkeeping), and the registers hold
-            // twice the keys (the bias of a 128-key tile would not fit)
-            if (a.geo.bias == nullptr) return launch_dq_typed<T, D, DV, DV, 0, 4, F>(a, st);
+            // without a bias: workgroups of 4 waves, two per CU (48 KB of
+            // LDS each), whose tile barriers do not hold the two waves of a
+            // SIMD in step; 2-3% faster than one 8-wave workgroup with
+            // 128-key tiles
+            if (a.geo.bias == nullptr) return launch_dq_typed<T, D, DV, DV, 0, 2, F, 4, 2>(a, st);
             return launch_dq_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else if constexpr (D <= 128) {
+            // the same with 32-key tiles when every query head has its own
+            // kv head (128 query rows per workgroup): 1-4% faster there; with
+            // GQA a 4-wave workgroup covers fewer rows per staged tile and
+            // the 8-wave one is as fast
+            if (a.geo.bias == nullptr && a.geo.g == 1) return launch_dq_typed<T, D, DV, DV, 0, 1, F, 4, 2>(a, st);
             return launch_dq_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else {
             // 256-wide tiles: 32-key tiles (three K + V stages fit the LDS).
