@@ -26,6 +26,8 @@
 //   causal only, src/attn_mpp.metal:591). At head dims <= 64 without a bias
 //   a variant runs 4-wave workgroups (two per CU) in which every wave
 //   computes all four products for its own 32 keys.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 #include "../../include/mtlattn_capi.h"
@@ -491,22 +493,13 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     const int64_t l_wrap = -(int64_t)(p.g - 1) - (int64_t)QTL * p.hq;
     const int l_row = 64 * l_piece + lane;           // stage-local row this lane loads
     const uint32_t l_voff = (uint32_t)l_row * (uint32_t)p.hq * 4u;
-    // Issues the loader cursor's stage and advances the cursor.
+    // stage() issues the loader cursor's stage and advance()s the cursor.
     // Without a bias the A waves issue the tile loads: wave B, one stage
     // behind, is the longer of the two and should not stall on issue. With
     // a bias the A waves keep their own bias loads in flight, and the wait
     // for those would also cover tile loads issued after them, so the B
     // waves load the tiles.
-    auto stage = [&]() {
-        if (ldw < 0) return;
-        char* buf = smem + ld_slot * QSTAGE;
-        const int avail = q_len - ld_qt;                    // >= 1
-        qst.issue_at(buf, ld_q, p.q_rs, avail, ldw, lane);
-        dost.issue_at(smem + DO_OFF + ld_dslot * TILE, ld_do, p.do_rs, avail, ldw, lane);
-        if (ldw < 2 * LPIECES) {   // rows past the end repeat the last row (masked)
-            const uint32_t voff = avail >= LROWS ? l_voff : (uint32_t)min(l_row, avail - 1) * (uint32_t)p.hq * 4u;
-            lds_dma4s(ld_l, voff, buf + TILE + (l_col * LROWS + 64 * l_piece) * 4);
-        }
+    auto advance = [&]() {
         ld_slot = ld_slot == NBUF - 1 ? 0 : ld_slot + 1;
         ld_dslot ^= 1;
         if (++ld_hl == p.g) {
@@ -521,6 +514,23 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             ld_l += 1;
         }
     };
+    auto stage = [&]() {
+        if (ldw < 0) return;
+        char* buf = smem + ld_slot * QSTAGE;
+        const int avail = q_len - ld_qt;                    // >= 1
+        qst.issue_at(buf, ld_q, p.q_rs, avail, ldw, lane);
+        dost.issue_at(smem + DO_OFF + ld_dslot * TILE, ld_do, p.do_rs, avail, ldw, lane);
+        if (ldw < 2 * LPIECES) {   // rows past the end repeat the last row (masked)
+            const uint32_t voff = avail >= LROWS ? l_voff : (uint32_t)min(l_row, avail - 1) * (uint32_t)p.hq * 4u;
+            lds_dma4s(ld_l, voff, buf + TILE + (l_col * LROWS + 64 * l_piece) * 4);
+        }
+        advance();
+    };
+    // For the 256-wide tiles without a bias, the A waves issue their loads of
+    // stage st + 1 one at a time between their S products of stage st
+    // instead of in a burst at its start (D = 256 backward -3.5%; at D <= 128
+    // within noise, so those keep the burst).
+    constexpr bool SPREAD = !BIAS && D > 128 && NQB * DC >= 4 * ((QTL * D * 2 / 1024 + NP - 1) / NP);
     // Compute cursor: stage st (wave A, and wave B's dP) and the ring slot of
     // stage st - 1 (wave B's dS and dK).
     int c_hl = 0, c_qt = qt_first, c_slot = 0, p_slot = NBUF - 1, c_dslot = 0;
@@ -569,7 +579,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         __syncthreads();
     }
     for (int st = 0; n_stages > 0 && st <= n_stages; ++st) {
-        if (st + 1 < n_stages) stage();
+        const bool load_next = st + 1 < n_stages;
+        if (load_next && !(SPREAD && role_a && st < n_stages)) stage();
         if (role_a && st < n_stages) {
             const char* Qs = smem + c_slot * QSTAGE;
             const char* Ds = smem + DO_OFF + c_dslot * TILE;
@@ -624,11 +635,68 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             f32x16_t sacc[NQB];
 #pragma unroll
             for (int qb = 0; qb < NQB; ++qb) sacc[qb] = f32x16_t{};
+            if constexpr (SPREAD) {
+                // one group per S product: the MFMA, the operand read four
+                // products ahead and, every second product, one load of
+                // stage st + 1 (groups kept in order by scheduling barriers)
+                constexpr int NS = NQB * DC;
+                constexpr int LQ = decltype(qst)::N;             // Q (and dO) loads per loader wave
+                static_assert(decltype(qst)::PER % NP == 0, "whole loads per loader wave");
+                char* lbuf = smem + ld_slot * QSTAGE;
+                char* dbuf = smem + DO_OFF + ld_dslot * TILE;
+                const int avail = q_len - ld_qt;
+                uint32_t qo[LQ], dso[LQ];
+                if (avail >= QTL) {
+#pragma unroll
+                    for (int j = 0; j < LQ; ++j) { qo[j] = qst.off[j]; dso[j] = dost.off[j]; }
+                } else {
+                    const int rmax = max(avail - 1, 0);
+#pragma unroll
+                    for (int j = 0; j < LQ; ++j) {
+                        const int i = ldw + j * NP;
+                        const int r = min(decltype(qst)::row_of(i, lane), rmax);
+                        qo[j] = decltype(qst)::lane_off(i, lane, r, (uint32_t)(2 * p.q_rs));
+                        dso[j] = decltype(dost)::lane_off(i, lane, r, (uint32_t)(2 * p.do_rs));
+                    }
+                }
+                const uint32_t lvoff = avail >= LROWS ? l_voff : (uint32_t)min(l_row, avail - 1) * (uint32_t)p.hq * 4u;
+                auto products = [&](auto with_loads) {
+                    u32x4_t qa[NS];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) qa[i] = row_operand<D>(qrb, i / NQB, 32 * (i % NQB));
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i = 0; i < NS; ++i) {
+                        sacc[i % NQB] = mfma32<T>(qa[i], kvf[i / NQB], sacc[i % NQB]);
+                        if (i + 4 < NS) qa[i + 4] = row_operand<D>(qrb, (i + 4) / NQB, 32 * ((i + 4) % NQB));
+                        if (decltype(with_loads)::value && (i == 0 || (i & 1))) {
+                            // load 0: lse / delta, 1..LQ: Q, LQ+1..2LQ: dO
+                            const int j = i == 0 ? 0 : (i + 1) >> 1;
+                            if (j == 0) {
+                                if (ldw < 2 * LPIECES)
+                                    lds_dma4s(ld_l, lvoff, lbuf + TILE + (l_col * LROWS + 64 * l_piece) * 4);
+                            } else if (j <= LQ) {
+                                lds_dma16s(ld_q, qo[j - 1], lbuf + (ldw + (j - 1) * NP) * 1024);
+                            } else if (j <= 2 * LQ) {
+                                lds_dma16s(ld_do, dso[j - 1 - LQ], dbuf + (ldw + (j - 1 - LQ) * NP) * 1024);
+                            }
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                };
+                if (load_next) {
+                    products(std::integral_constant<bool, true>{});
+                    advance();
+                } else {
+                    products(std::integral_constant<bool, false>{});
+                }
+            } else {
 #pragma unroll
             for (int kc = 0; kc < DC; ++kc)
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb)
                     sacc[qb] = mfma32<T>(row_operand<D>(qrb, kc, 32 * qb), kvf[kc], sacc[qb]);
+            }
             // exponentials of both blocks (overlapping the S MFMAs in flight),
             // then the rarely needed masks, then the dV products
 #pragma unroll
