@@ -106,6 +106,9 @@ def _bwd(mt, name, q_lens, kv_lens, Hq, Hkv, D, dtype, atol, causal=False, windo
     print("  " + " ".join(f"{k_}={v_:.3e}" for k_, v_ in errs.items()) + f" atol={atol}", flush=True)
     worst = max(errs["dQ"], errs["dK"], errs["dV"])
     assert worst < atol, f"{name}: grad err {errs}"
+    if dtype != torch.float32:   # and the relative RMS criterion of tests/helpers.py
+        for nm in ("out", "dQ", "dK", "dV"):
+            assert errs[nm + "_rms_rel"] <= RMS_BOUND[dtype], f"{name}: {nm} rms_rel {errs[nm + '_rms_rel']:.3e}"
     return qm.grad, km.grad, vm.grad
 
 
@@ -467,6 +470,22 @@ def test_bwd_fp16(mt):
     _bwd(mt, "bwd fp16 D=88 GQA", [200, 56], [200, 56], 8, 2, 88, h, 6e-3, causal=True)
     _bwd(mt, "bwd fp16 D=160", [512], [512], 8, 8, 160, h, 6e-3, causal=True)
     _bwd(mt, "bwd fp16 D=256", [512], [512], 8, 8, 256, h, 6e-3, causal=True)
+
+
+def test_bwd_d64_paths(mt):
+    """Head dim 64 backward without a bias runs its own dK/dV kernel (every
+    wave computing all four products for its keys, 4-wave workgroups) and
+    4-wave dQ workgroups: window band, cross lengths (kv longer and shorter
+    than q, causal end-aligned), GQA causal, tiny and odd lengths around the
+    128-key workgroup and 64-query stage edges, fp16 and bf16."""
+    h, b = torch.float16, torch.bfloat16
+    _bwd(mt, "D=64 window", [700, 300], [700, 300], 8, 8, 64, b, 4e-2, causal=True, window=100)
+    _bwd(mt, "D=64 window non-causal", [500], [500], 4, 4, 64, h, 5e-3, window=70)
+    _bwd(mt, "D=64 cross non-causal GQA", [100, 33], [250, 700], 8, 4, 64, h, 5e-3)
+    _bwd(mt, "D=64 cross causal", [100, 257, 300], [300, 257, 129], 8, 8, 64, b, 4e-2, causal=True)
+    _bwd(mt, "D=64 GQA causal", [600, 130], [600, 130], 16, 4, 64, b, 4e-2, causal=True)
+    _bwd(mt, "D=64 tiny and odd", [1, 17, 129, 128, 65], [1, 17, 129, 128, 65], 4, 4, 64, h, 5e-3)
+    _bwd(mt, "D=64 tiny causal", [1, 2, 63, 64, 127], [1, 2, 63, 64, 127], 4, 2, 64, h, 5e-3, causal=True)
 
 
 def test_bwd_bf16(mt):
