@@ -88,13 +88,12 @@ __device__ inline void neg_col(float* x, int which) {
 
 // ---------------------------------------------------------------------------
 // dQ.  8 waves (2 per SIMD), 32 query rows x 1 head per wave, the heads of a
-// GQA group packed as in the forward; without a bias at D = 64 (and at
-// D = 128 without GQA) workgroups of 4 waves, two per CU; at D = 256 one
-// workgroup of 4 waves per CU (one per SIMD, 512 registers each). Key tiles
-// of 32 * KB rows (64; 32 for the 256-wide tiles and the 4-wave D = 128
-// variant) go straight from HBM into a 3-deep LDS ring (K and V row-major,
-// swizzled); K^T operands of the dQ product are transposed LDS reads of the
-// same K tile.
+// GQA group packed as in the forward; without a bias at D <= 128 workgroups
+// of 4 waves, two per CU; at D = 256 one workgroup of 4 waves per CU (one
+// per SIMD, 512 registers each). Key tiles of 32 * KB rows (64; 32 for the
+// 256-wide tiles) go straight from HBM into an LDS ring of NBUF slots (3;
+// 2 for the 4-wave D = 128 workgroups) (K and V row-major, swizzled); K^T
+// operands of the dQ product are transposed LDS reads of the same K tile.
 // ---------------------------------------------------------------------------
 // D is the tile width (64, 128 or 256) and DV <= D the head dim, as in the
 // forward. This launch outputs the DO columns from C0 (head dims above 128
@@ -103,7 +102,7 @@ __device__ inline void neg_col(float* x, int which) {
 // BROWS > 0: a head-broadcast bias staged in the LDS ring with the K/V tiles
 // (workgroups of BROWS query rows, 64-key tiles), as in the forward.
 template <typename T, int D, int DV, int DO, int C0, int KB, bool BIAS, bool OUT_F32, int BROWS = 0, int NW = kWaves,
-          int OCC = 1>
+          int OCC = 1, int NBUF = 3>
 __global__ __launch_bounds__(NW * 64, OCC) void bwd_dq_kernel(BwdKParams p) {
     constexpr int DC = (DV + 15) / 16, DB = (DO + 31) / 32;
     constexpr int KT = 32 * KB;               // keys per tile
@@ -113,7 +112,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void bwd_dq_kernel(BwdKParams p) {
     constexpr int TILE = KT * D * 2;
     constexpr int BTILE = BROWS * KT * 4;
     constexpr int STAGE = 2 * TILE + BTILE;   // K, V, staged bias
-    constexpr int NBUF = 3;
+    static_assert(NBUF == 2 || NBUF == 3, "ring depth");
+    constexpr int AHEAD = NBUF - 1;           // tiles in flight ahead of the one in use
     constexpr int LOADS = STAGE / 1024 / NW;
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE];
 
@@ -252,14 +252,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void bwd_dq_kernel(BwdKParams p) {
     for (int r = 0; r < 16; ++r) ndlt[r] = -dlt;
 
     if (n_kv_tiles > 0) stage();
-    if (n_kv_tiles > 1) stage();
+    if (AHEAD > 1 && n_kv_tiles > 1) stage();
     int slot = 0;                                // ring slot of tile it
     for (int it = 0; it < n_kv_tiles; ++it, slot = slot == NBUF - 1 ? 0 : slot + 1) {
-        if (it + 1 < n_kv_tiles) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
+        if (AHEAD > 1 && it + 1 < n_kv_tiles) wait_vmcnt<LOADS * (AHEAD - 1)>(); else wait_vmcnt<0>();
         __syncthreads();
         // (with a bias, the tile loads go out after the bias is consumed: the
         // bias loads' wait would otherwise also wait for them)
-        if (!reg_bias && it + 2 < n_kv_tiles) stage();
+        if (!reg_bias && it + AHEAD < n_kv_tiles) stage();
         const int kt = kv_lo + it * KT;
         // the bias of the whole tile, all loads in flight together (4-key
         // groups at 32 kb + 8 g + 4 hi)
@@ -335,7 +335,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void bwd_dq_kernel(BwdKParams p) {
                 if (BIAS) x = fmaf(bv[4 * kb + (r >> 2)][r & 3], kLog2e, x);
                 sacc[kb][r] = __builtin_amdgcn_exp2f(x);
             }
-            if (reg_bias && kb == KB - 1 && it + 2 < n_kv_tiles) stage();
+            if (reg_bias && kb == KB - 1 && it + AHEAD < n_kv_tiles) stage();
             if (need_mask) {     // out-of-band keys -> P = 0
                 asm volatile("");   // keep a real branch (no speculated selects on every tile)
 #pragma unroll
@@ -1178,7 +1178,7 @@ BwdKParams make_params(const BwdArgs& a) {
     return p;
 }
 
-template <typename T, int D, int DV, int DO, int C0, int KB, bool OUT_F32, int NW = kWaves, int OCC = 1>
+template <typename T, int D, int DV, int DO, int C0, int KB, bool OUT_F32, int NW = kWaves, int OCC = 1, int NB = 3>
 hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     // the fused delta needs the whole head in one launch
     if (a.delta_out != nullptr && !(C0 == 0 && DO == DV && DV == D && D <= 128)) return hipErrorInvalidValue;
@@ -1206,11 +1206,11 @@ hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
     if constexpr (KB > 2) {
         if (a.geo.bias != nullptr) return hipErrorInvalidValue;   // (not dispatched: registers)
     } else if (a.geo.bias != nullptr) {
-        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32, 0, NW, OCC>), dim3((unsigned)blocks), dim3(NW * 64),
+        hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, true, OUT_F32, 0, NW, OCC, NB>), dim3((unsigned)blocks), dim3(NW * 64),
                            0, st, p);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, false, OUT_F32, 0, NW, OCC>), dim3((unsigned)blocks), dim3(NW * 64), 0,
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, DV, DO, C0, KB, false, OUT_F32, 0, NW, OCC, NB>), dim3((unsigned)blocks), dim3(NW * 64), 0,
                        st, p);
     return hipGetLastError();
 }
@@ -1317,11 +1317,10 @@ struct DqLaunch {
             if (a.geo.bias == nullptr) return launch_dq_typed<T, D, DV, DV, 0, 2, F, 4, 2>(a, st);
             return launch_dq_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else if constexpr (D <= 128) {
-            // the same with 32-key tiles when every query head has its own
-            // kv head (128 query rows per workgroup): 1-4% faster there; with
-            // GQA a 4-wave workgroup covers fewer rows per staged tile and
-            // the 8-wave one is as fast
-            if (a.geo.bias == nullptr && a.geo.g == 1) return launch_dq_typed<T, D, DV, DV, 0, 1, F, 4, 2>(a, st);
+            // the same with a 2-deep ring of 64-key tiles (64 KB of LDS per
+            // workgroup): 0-3% faster than one 8-wave workgroup with a 3-deep
+            // ring (GQA, MHA, ragged, windowed)
+            if (a.geo.bias == nullptr) return launch_dq_typed<T, D, DV, DV, 0, 2, F, 4, 2, 2>(a, st);
             return launch_dq_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else {
             // 256-wide tiles: 32-key tiles (three K + V stages fit the LDS).
