@@ -5,9 +5,11 @@
 //   * Workgroup = 8 waves (512 threads, 2 waves per SIMD). Each wave owns 32
 //     query rows of one query head. The workgroup packs `hpw` = gcd(g, 8) query
 //     heads of one GQA group, so every K/V tile staged in LDS serves
-//     hpw * (8 / hpw) * 32 = 256 query-head rows.
+//     hpw * (8 / hpw) * 32 = 256 query-head rows. Small grids at D = 128
+//     without a bias run 4-wave workgroups instead, two per CU (hpw =
+//     gcd(g, 2), a 2-deep ring).
 //   * Key tiles of 64 rows (32 for the 256-wide head dims in one launch) go
-//     straight from HBM into a 3-deep LDS ring with
+//     straight from HBM into a 3-deep (or 2-deep) LDS ring with
 //     global_load_lds_dwordx4 (no register staging), K and V both row-major
 //     and swizzled; the P.V product reads V^T operands with
 //     ds_read_b64_tr_b16 transposed loads. Without a bias, each wave's loads
@@ -67,8 +69,8 @@ struct FwdKParams {
 // workgroup covers BROWS query rows; each key tile's bias block is staged in
 // the LDS ring with the K/V tiles (read from LDS by all waves of all heads)
 // instead of every wave loading its rows from global memory.
-template <typename T, int DK, int DV, int DVL, int DO, int SM, int BROWS = 0, int KT = kKT>
-__global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
+template <typename T, int DK, int DV, int DVL, int DO, int SM, int BROWS = 0, int KT = kKT, int NW = kWaves, int NBUF = 3>
+__global__ __launch_bounds__(NW * 64, kWaves / NW) void fwd_mfma_kernel(FwdKParams p) {
     static_assert(KT == 64 || (KT == 32 && BROWS == 0), "32-key tiles: no staged bias");
     constexpr int NKB = KT / 32;             // 32-key blocks per tile
     constexpr int NPC = KT / 16;             // 16-key P chunks per tile
@@ -81,15 +83,15 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     constexpr int VTILE = KT * DVL * 2;     // bytes of one V tile
     constexpr int BTILE = BROWS * KT * 4;   // bytes of one staged bias tile
     constexpr int STAGE = KTILE + VTILE + BTILE;   // K, V (row-major), bias
-    constexpr int NBUF = 3;                  // ring of staged key tiles
-    constexpr int LOADS = STAGE / 1024 / kWaves;   // direct loads per wave per tile
-    static_assert(LOADS <= 15 && STAGE % (1024 * kWaves) == 0, "staging");
+    constexpr int AHEAD = NBUF - 1;          // tiles loading ahead of the one in use (ring of NBUF)
+    constexpr int LOADS = STAGE / 1024 / NW;   // direct loads per wave per tile
+    static_assert(LOADS <= 15 && STAGE % (1024 * NW) == 0 && (!LDSB || NW == kWaves), "staging");
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
     const int l32 = lane & 31, hi = lane >> 5;
-    const int QT = 32 * (kWaves / p.hpw);
+    const int QT = 32 * (NW / p.hpw);
     const int L = xcd_remap(blockIdx.x, p.n_tiles * p.n_hg);
     const int hg = L / p.n_tiles;
     const int t = p.n_tiles - 1 - (L - hg * p.n_tiles);   // late (heavier) tiles first
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     const int q0 = (t - tb) * QT;
     if (q0 >= q_len) return;
 
-    const int wph = kWaves / p.hpw;
+    const int wph = NW / p.hpw;
     const int head = hg * p.hpw + w / wph;
     const int hk = head / p.g;
     const int qa = q0 + 32 * (w % wph);          // first query row of this wave (seq-local)
@@ -136,9 +138,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
 
     const uint16_t* kbase = p.k + (int64_t)kr.start * p.k_rs + (int64_t)hk * DV;
     const uint16_t* vbase = p.v + (int64_t)kr.start * p.v_rs + (int64_t)hk * DV + p.col0;
-    // All 8 waves stage each tile straight from HBM into LDS (K then V).
-    TileStager<DK, KT, kWaves, DV> kst;
-    TileStager<DVL, KT, kWaves, DO> vst;
+    // The NW waves stage each tile straight from HBM into LDS (K then V).
+    TileStager<DK, KT, NW, DV> kst;
+    TileStager<DVL, KT, NW, DO> vst;
     kst.init(p.k_rs, w, lane);
     vst.init(p.v_rs, w, lane);
     // Staged bias: WG row r is query q0 + r (rows past the end repeat the last)
@@ -221,12 +223,12 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
     const bool row_live = wave_active & (band.width > 0);
 
     if (n_kv_tiles > 0) stage(0);
-    if (n_kv_tiles > 1) stage(1);
+    if (AHEAD > 1 && n_kv_tiles > 1) stage(1);
     for (int it = 0; it < n_kv_tiles; ++it) {
         // tile `it` landed (the next one may still be in flight), then publish
-        if (it + 1 < n_kv_tiles) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
+        if (AHEAD > 1 && it + 1 < n_kv_tiles) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
         __syncthreads();
-        // the buffer of tile it + 2 was last read in iteration it - 1 (with a
+        // the buffer of tile it + AHEAD was last read in iteration it - 1 (with a
         // bias, the tile loads go out after the bias is consumed: the bias
         // loads' wait would otherwise also wait for them)
         // Without a bias, the loads of tile it + 2 go out one by one between
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
         // in one launch: its O and Q registers leave no room for the operand
         // reads held ahead).
         constexpr bool SPREAD = SM == 0 && DB * 16 + DC * 4 <= 160;
-        if (!SPREAD && !reg_bias && it + 2 < n_kv_tiles) stage(it + 2);
+        if (!SPREAD && !reg_bias && it + AHEAD < n_kv_tiles) stage(it + AHEAD);
         const int kt = kv_lo + it * KT;
         f32x4_t bv[8];
         if (reg_bias) load_bias(kt, bv);
@@ -282,11 +284,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
             // reads from being issued ahead of them).
             constexpr int NS = NKB * DC;
             constexpr int LK = decltype(kst)::N, LV = decltype(vst)::N, NL = LK + LV;
-            static_assert(decltype(kst)::PER % kWaves == 0 && decltype(vst)::PER % kWaves == 0 && NL <= NS,
+            static_assert(decltype(kst)::PER % NW == 0 && decltype(vst)::PER % NW == 0 && NL <= NS,
                           "whole loads per wave");
-            const bool load_next = it + 2 < n_kv_tiles;
-            const int kt2 = kt + 2 * KT;
-            char* buf2 = smem + ((it + 2) % NBUF) * STAGE;
+            const bool load_next = it + AHEAD < n_kv_tiles;
+            const int kt2 = kt + AHEAD * KT;
+            char* buf2 = smem + ((it + AHEAD) % NBUF) * STAGE;
             const char* ksrc = reinterpret_cast<const char*>(kbase + (int64_t)kt2 * p.k_rs);
             const char* vsrc = reinterpret_cast<const char*>(vbase + (int64_t)kt2 * p.v_rs);
             uint32_t lo[NL];   // per-lane source offsets (rows past the end read the last row)
@@ -299,13 +301,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
                 const int rmax = max(kv_len - kt2 - 1, 0);
 #pragma unroll
                 for (int j = 0; j < LK; ++j) {
-                    const int i = w + j * kWaves;
+                    const int i = w + j * NW;
                     lo[j] = decltype(kst)::lane_off(i, lane, min(decltype(kst)::row_of(i, lane), rmax),
                                                     (uint32_t)(2 * p.k_rs));
                 }
 #pragma unroll
                 for (int j = 0; j < LV; ++j) {
-                    const int i = w + j * kWaves;
+                    const int i = w + j * NW;
                     lo[LK + j] = decltype(vst)::lane_off(i, lane, min(decltype(vst)::row_of(i, lane), rmax),
                                                          (uint32_t)(2 * p.v_rs));
                 }
@@ -321,7 +323,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
                     if (i + 4 < NS) ka[i + 4] = row_operand<DK>(kb_, (i + 4) / NKB, 32 * ((i + 4) % NKB));
                     if (decltype(with_loads)::value && i % (NS / NL) == 1 % (NS / NL) && i / (NS / NL) < NL) {
                         const int j = i / (NS / NL);
-                        const int row = w + (j < LK ? j : j - LK) * kWaves;   // 1 KB instruction of the tile
+                        const int row = w + (j < LK ? j : j - LK) * NW;   // 1 KB instruction of the tile
                         if (j < LK) lds_dma16s(ksrc, lo[j], buf2 + row * 1024);
                         else lds_dma16s(vsrc, lo[j], buf2 + KTILE + row * 1024);
                     }
@@ -421,7 +423,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
             m_run = m_new;
         };
         if constexpr (kDeferMax) {
-            if (reg_bias && it + 2 < n_kv_tiles) stage(it + 2);
+            if (reg_bias && it + AHEAD < n_kv_tiles) stage(it + AHEAD);
             float ts = weights(m_run == kNegInf ? 0.f : m_run, 0.f);
             if (__any(!(ts < kMaxTileSum) | ((m_run == kNegInf) & row_live))) {
                 asm volatile("");
@@ -431,7 +433,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
             l_run += ts;
         } else {
             update_max(kRescale);
-            if (reg_bias && it + 2 < n_kv_tiles) stage(it + 2);
+            if (reg_bias && it + AHEAD < n_kv_tiles) stage(it + AHEAD);
             l_run = weights(m_run == kNegInf ? 0.f : m_run, l_run);
         }
         // O^T += V^T P^T; V^T operands are transposed reads of the row-major V tile
@@ -465,6 +467,19 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_mfma_kernel(FwdKParams p) {
 
 int gcd_int(int a, int b) { while (b) { const int t = a % b; a = b; b = t; } return a; }
 
+// CUs of the current device (cached per device; 256 if unknown)
+int device_cus() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
 template <typename T, int DK, int DV, int DVL, int DO>
 hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     const Geometry& g = a.geo;
@@ -497,6 +512,26 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     if (DK <= 128 && sm == 1 && g.bias_hs == 0 && p.bias_v4 && g.bias_cols >= 4 && g.bias_cols % 4 == 0 &&
         (QT == 32 || QT == 64) && ((int64_t)QT * g.bias_qs + g.bias_cols) * 4 < ((int64_t)1 << 32))
         brows = QT;
+    if constexpr (DK == 128 && DVL == 128 && DO == 128) {
+        // Small grids (at most two 8-wave workgroups per CU) run 4-wave
+        // workgroups, two per CU, on a 2-deep ring (64 KB of LDS each), with
+        // at most 2 heads of a GQA group per workgroup: 3-25% faster there
+        // (MHA and GQA shapes of 2-4 sequences of 2-4K); on larger grids the
+        // 8-wave workgroups, whose staged tiles serve twice the query rows,
+        // are as fast or faster (C3 +1-4% with the 4-wave ones).
+        if (sm == 0 && (g.total_q / QT) * p.n_hg <= 2 * (int64_t)device_cus()) {
+            p.hpw = gcd_int(g.g, 2);
+            const int QT4 = 32 * (4 / p.hpw);
+            p.n_tiles = (int)(g.total_q / QT4) + g.num_seqs + 1;
+            p.n_hg = g.hq / p.hpw;
+            const int64_t blocks4 = (int64_t)p.n_tiles * p.n_hg;
+            if (blocks4 > 0x7fffffff) return hipErrorInvalidValue;
+            p.col0 = 0;
+            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 0, 0, 64, 4, 2>), dim3((unsigned)blocks4), dim3(256),
+                               0, st, p);
+            return hipGetLastError();
+        }
+    }
     if constexpr (DK > 128) {
         // The wide head dims take the whole output in one launch on 32-key
         // tiles (three 256-wide K + V stages fit the LDS), instead of
