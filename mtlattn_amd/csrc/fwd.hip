@@ -5,9 +5,9 @@
 //   * Workgroup = 8 waves (512 threads, 2 waves per SIMD). Each wave owns 32
 //     query rows of one query head. The workgroup packs `hpw` = gcd(g, 8) query
 //     heads of one GQA group, so every K/V tile staged in LDS serves
-//     hpw * (8 / hpw) * 32 = 256 query-head rows. Small grids at D = 128
-//     without a bias run 4-wave workgroups instead, two per CU (hpw =
-//     gcd(g, 2), a 2-deep ring).
+//     hpw * (8 / hpw) * 32 = 256 query-head rows. Small grids without a
+//     bias (D = 128; D = 64 causal) run 4-wave workgroups instead, two per
+//     CU (hpw = gcd(g, 2), a 2-deep ring).
 //   * Key tiles of 64 rows (32 for the 256-wide head dims in one launch) go
 //     straight from HBM into a 3-deep (or 2-deep) LDS ring with
 //     global_load_lds_dwordx4 (no register staging), K and V both row-major
@@ -512,14 +512,15 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
     if (DK <= 128 && sm == 1 && g.bias_hs == 0 && p.bias_v4 && g.bias_cols >= 4 && g.bias_cols % 4 == 0 &&
         (QT == 32 || QT == 64) && ((int64_t)QT * g.bias_qs + g.bias_cols) * 4 < ((int64_t)1 << 32))
         brows = QT;
-    if constexpr (DK == 128 && DVL == 128 && DO == 128) {
+    if constexpr ((DK == 128 && DVL == 128 && DO == 128) || (DK == 64 && DO == 64)) {
         // Small grids (at most two 8-wave workgroups per CU) run 4-wave
-        // workgroups, two per CU, on a 2-deep ring (64 KB of LDS each), with
-        // at most 2 heads of a GQA group per workgroup: 3-25% faster there
-        // (MHA and GQA shapes of 2-4 sequences of 2-4K); on larger grids the
-        // 8-wave workgroups, whose staged tiles serve twice the query rows,
-        // are as fast or faster (C3 +1-4% with the 4-wave ones).
-        if (sm == 0 && (g.total_q / QT) * p.n_hg <= 2 * (int64_t)device_cus()) {
+        // workgroups, two per CU, on a 2-deep ring (64 KB of LDS each at
+        // D = 128), with at most 2 heads of a GQA group per workgroup: 3-25%
+        // faster there (MHA and GQA shapes of 2-4 sequences of 2-4K; at
+        // D = 64 causal only: non-causal GQA was 8% slower); on larger grids
+        // the 8-wave workgroups, whose staged tiles serve twice the query
+        // rows, are as fast or faster (C3 +1-4% with the 4-wave ones).
+        if (sm == 0 && (DK == 128 || p.causal) && (g.total_q / QT) * p.n_hg <= 2 * (int64_t)device_cus()) {
             p.hpw = gcd_int(g.g, 2);
             const int QT4 = 32 * (4 / p.hpw);
             p.n_tiles = (int)(g.total_q / QT4) + g.num_seqs + 1;
