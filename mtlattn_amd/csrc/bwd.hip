@@ -392,13 +392,22 @@ __global__ __launch_bounds__(NW * 64, OCC) void bwd_dq_kernel(BwdKParams p) {
 // loop covers the g heads of the group, so the GQA reduction of dK/dV
 // happens in registers.
 // ---------------------------------------------------------------------------
-// D is the tile width (64, 128 or 256) and DV <= D the head dim; this launch
-// outputs the DO columns of dK and dV from C0 (several launches above 128,
-// the S and dP products recomputed in each). A stage holds 32 * NQB queries.
+// D is the tile width (64, 128 or 256) and DV <= D the head dim; a
+// workgroup outputs the DO columns of dK and dV from C0 + DO * blockIdx.y
+// (DO < DV: the slices run as workgroups of one launch, each recomputing the
+// S and dP products). A stage holds 32 * NQB queries.
 template <typename T, int D, int DV, int DO, int C0, int NQB, bool BIAS, bool OUT_F32>
 __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     constexpr int DC = (DV + 15) / 16, DB = (DO + 31) / 32;
     static_assert(C0 % 32 == 0 && C0 + DO <= D, "output slice");
+    // first output column of this workgroup's slice: C0, plus DO per slice
+    // when the columns are split (a multiple of 128 in a 256-wide tile, so
+    // the transposed reads of the slice are those of slice 0 with the byte
+    // offset's bit 8 flipped)
+    constexpr bool SLICED = DO < DV;
+    static_assert(!SLICED || (C0 == 0 && DO == 128 && D == 256), "column slices of the 256-wide tiles");
+    const int c0 = SLICED ? DO * (int)blockIdx.y : C0;
+    const uint32_t tslice = SLICED ? 2u * (uint32_t)c0 : 0u;
     constexpr int QTL = 32 * NQB;                       // queries per stage
     constexpr int NP = kWaves / 2;                      // wave pairs
     constexpr int KB = NP * kKW;                        // keys per workgroup
@@ -586,7 +595,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             const char* Ds = smem + DO_OFF + c_dslot * TILE;
             const float* ls = reinterpret_cast<const float*>(Qs + TILE);   // -lse log2(e)
             const char* qrb = opaque(Qs + rbase);
-            const char* dtb = opaque(Ds + tbase);
+            const char* dtb = opaque(Ds + (tbase ^ tslice));
             char* pb = smem + P_OFF + (st & 1) * PSTAGE + pair * NQB * PBLK;
             const int h = hk * p.g + c_hl;
             const int qt = c_qt;
@@ -761,7 +770,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             // work and then VALU work at the same time.
             if (st > 0) {
                 const char* Qs = smem + p_slot * QSTAGE;
-                const char* qtb = opaque(Qs + tbase);
+                const char* qtb = opaque(Qs + (tbase ^ tslice));
                 const char* pb = smem + P_OFF + ((st - 1) & 1) * PSTAGE + pair * NQB * PBLK;
 #pragma unroll
                 for (int qb = 0; qb < NQB; ++qb) {
@@ -822,7 +831,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     }
 
     if (pair_active && key_ok) {
-        const int64_t off = (int64_t)(kr.start + key) * ((int64_t)p.hkv * DV) + (int64_t)hk * DV + C0;
+        const int64_t off = (int64_t)(kr.start + key) * ((int64_t)p.hkv * DV) + (int64_t)hk * DV + c0;
         void* dst = role_a ? p.dv : p.dk;
         const float sc = role_a ? 1.f : p.scale;
 #pragma unroll
@@ -830,7 +839,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
                 const int d = 32 * db + 8 * rg + 4 * hi;
-                if ((DO % 32 != 0 && d >= DO) || (C0 + DO > DV && C0 + d >= DV)) continue;
+                if ((DO % 32 != 0 && d >= DO) || (c0 + d >= DV)) continue;
                 store4<T, OUT_F32>(dst, off + d, acc[db][4 * rg] * sc, acc[db][4 * rg + 1] * sc,
                                    acc[db][4 * rg + 2] * sc, acc[db][4 * rg + 3] * sc);
             }
@@ -1222,15 +1231,17 @@ hipError_t launch_dkv_typed(const BwdArgs& a, hipStream_t st) {
     p.n_tiles = (int)(a.geo.total_kv / (NW / 2 * kKW)) + a.geo.num_seqs + 1;
     const int64_t blocks = (int64_t)p.n_tiles * a.geo.hkv;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    // column slices (DO < DV) are the grid's second dimension: one launch,
+    // so the slices' workgroups share the GPU instead of running one after
+    // the other (a causal grid's tail is one heavy workgroup per CU)
+    const dim3 grid((unsigned)blocks, (unsigned)((DV - C0 + DO - 1) / DO));
     if constexpr (NQB > 2) {
         if (a.geo.bias != nullptr) return hipErrorInvalidValue;   // (not dispatched: registers)
     } else if (a.geo.bias != nullptr) {
-        hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, DO, C0, NQB, true, OUT_F32>), dim3((unsigned)blocks),
-                           dim3(NW * 64), 0, st, p);
+        hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, DO, C0, NQB, true, OUT_F32>), grid, dim3(NW * 64), 0, st, p);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, DO, C0, NQB, false, OUT_F32>), dim3((unsigned)blocks), dim3(NW * 64),
-                       0, st, p);
+    hipLaunchKernelGGL((bwd_dkv_kernel<T, D, DV, DO, C0, NQB, false, OUT_F32>), grid, dim3(NW * 64), 0, st, p);
     return hipGetLastError();
 }
 
@@ -1348,12 +1359,11 @@ struct DkvLaunch {
             return launch_dkv_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else {
             // 256-wide tiles: 32-query stages. D = 160 computes the whole
-            // output in one launch (207 VGPRs); D = 256 in two 128-column
-            // launches (one launch would spill its accumulators)
+            // output in each workgroup (207 VGPRs); D = 256 in 128-column
+            // slices, each workgroup one slice (the whole output would spill
+            // its accumulators), both slices in one launch
             if constexpr (DV > 192) {
-                hipError_t e = launch_dkv_typed<T, D, DV, 128, 0, 1, F>(a, st);
-                if (e == hipSuccess) e = launch_dkv_typed<T, D, DV, 128, 128, 1, F>(a, st);
-                return e;
+                return launch_dkv_typed<T, D, DV, 128, 0, 1, F>(a, st);
             } else {
                 return launch_dkv_typed<T, D, DV, DV, 0, 1, F>(a, st);
             }
