@@ -26,7 +26,7 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmtlattn_hip.so")
 EXT = os.path.join(HERE, "_C" + sysconfig.get_config_var("EXT_SUFFIX"))
 CALIB = os.path.join(HERE, "libmtlattn_calib.so")
-HIP_SOURCES = ["fwd.hip", "bwd.hip", "decode.hip", "generic.hip", "pad.hip", "capi.hip"]
+HIP_SOURCES = ["fwd.hip", "bwd.hip", "decode.hip", "generic.hip", "f32mfma.hip", "pad.hip", "capi.hip"]
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = os.environ.get("MTLATTN_ARCH", "gfx950")

@@ -352,6 +352,8 @@ int mtlattn_varlen_fwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
     if (is16(p->dtype) && mfma_head_dim(p->head_dim) && vec_ok && tile_stride_ok(k_row_stride) &&
         tile_stride_ok(v_row_stride) && !force_generic())
         return launch_status(launch_fwd_mfma(p->dtype, a, st), "flash forward");
+    if (p->dtype == MTLATTN_DTYPE_F32 && f32_mfma_head_dim(p->head_dim) && vec_ok && !force_generic())
+        return launch_status(launch_fwd_f32mfma(a, st), "fp32 flash forward");
     return launch_status(launch_fwd_generic(p->dtype, a, st), "generic forward");
 }
 
@@ -413,6 +415,15 @@ bool bwd_mfma_ok(const mtlattn_problem* p, const void* q, int64_t qrs, const voi
            tile_stride_ok(qrs) && tile_stride_ok(krs) && tile_stride_ok(vrs) && tile_stride_ok(dors);
 }
 
+// fp32 inputs on the fp32 matrix-core kernels (16-byte aligned operand rows
+// and output rows)
+bool bwd_f32_ok(const mtlattn_problem* p, const void* q, int64_t qrs, const void* k, int64_t krs, const void* v,
+                int64_t vrs, const void* dout, int64_t dors) {
+    return p->dtype == MTLATTN_DTYPE_F32 && f32_mfma_head_dim(p->head_dim) && !force_generic() &&
+           aligned16(q, qrs, p->dtype) && aligned16(k, krs, p->dtype) && aligned16(v, vrs, p->dtype) &&
+           aligned16(dout, dors, p->dtype);
+}
+
 }  // namespace
 
 int mtlattn_bwd_dq(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
@@ -433,6 +444,9 @@ int mtlattn_bwd_dq(const mtlattn_problem* p, const void* q, int64_t q_row_stride
     hipStream_t st = (hipStream_t)stream;
     if (bwd_mfma_ok(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride))
         return launch_status(launch_bwd_dq_mfma(p->dtype, a, st), "dQ");
+    if (bwd_f32_ok(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride) &&
+        ((uintptr_t)dq & 15u) == 0)
+        return launch_status(launch_bwd_dq_f32mfma(a, st), "fp32 dQ");
     return launch_status(launch_bwd_dq_generic(p->dtype, a, st), "generic dQ");
 }
 
@@ -455,6 +469,9 @@ int mtlattn_bwd_dkv(const mtlattn_problem* p, const void* q, int64_t q_row_strid
     hipStream_t st = (hipStream_t)stream;
     if (bwd_mfma_ok(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride))
         return launch_status(launch_bwd_dkv_mfma(p->dtype, a, st), "dK/dV");
+    if (bwd_f32_ok(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride) &&
+        ((uintptr_t)dk & 15u) == 0 && ((uintptr_t)dv & 15u) == 0)
+        return launch_status(launch_bwd_dkv_f32mfma(a, st), "fp32 dK/dV");
     return launch_status(launch_bwd_dkv_generic(p->dtype, a, st), "generic dK/dV");
 }
 

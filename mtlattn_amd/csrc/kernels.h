@@ -80,6 +80,11 @@ hipError_t launch_bwd_dq_mfma(int dtype, const BwdArgs& a, hipStream_t st);
 hipError_t launch_bwd_dkv_mfma(int dtype, const BwdArgs& a, hipStream_t st);
 hipError_t launch_bwd_dq_generic(int dtype, const BwdArgs& a, hipStream_t st);
 hipError_t launch_bwd_dkv_generic(int dtype, const BwdArgs& a, hipStream_t st);
+// fp32 inputs on the fp32 matrix cores (f32_mfma_head_dim, 16-byte aligned
+// rows and outputs); dq / dk / dv are written as fp32
+hipError_t launch_fwd_f32mfma(const FwdArgs& a, hipStream_t st);
+hipError_t launch_bwd_dq_f32mfma(const BwdArgs& a, hipStream_t st);
+hipError_t launch_bwd_dkv_f32mfma(const BwdArgs& a, hipStream_t st);
 // Rows of a [total_rows, row_bytes] tensor outside [cu[0], cu[num_seqs]).
 struct ZeroFill {
     void* ptr;
@@ -108,6 +113,9 @@ inline int64_t decode_workspace_rows(int64_t total_kv, int num_seqs, int hkv, in
 inline bool mfma_head_dim(int d) {
     return d == 64 || d == 80 || d == 88 || d == 96 || d == 128 || d == 160 || d == 256;
 }
+// head dims of the fp32 matrix-core kernels (columns padded to a multiple
+// of 32 with zeros)
+inline bool f32_mfma_head_dim(int d) { return d > 0 && d <= 128 && d % 4 == 0; }
 // head dims of the split-KV decode kernels
 inline bool decode_head_dim(int d) { return d == 64 || d == 128; }
 

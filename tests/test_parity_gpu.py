@@ -458,6 +458,53 @@ def test_bwd_fp32(mt):
     _bwd(mt, "bwd varlen GQA", [128, 300], [128, 300], 12, 4, 128, f, 1e-4, causal=True)
 
 
+def test_fp32_matrix_cores(mt, monkeypatch):
+    """fp32 inputs at head dims up to 128 that are a multiple of 4 run the
+    fp32 matrix-core kernels (v_mfma_f32_32x32x2_f32, columns padded to a
+    multiple of 32): ragged GQA causal with a one-token sequence, cross
+    lengths with a window, non-causal cross, per-head and broadcast bias,
+    lengths around the 128-row workgroup and 32-row tile edges, forward and
+    backward against the oracle; and both these kernels and the portable
+    ones (MTLATTN_NO_MFMA) against the fp64 oracle with the fp32 criterion of
+    tests/helpers.py (floor32 = the fp32 oracle's own error)."""
+    f = torch.float32
+    for D in (16, 36, 64, 100, 128):
+        _fwd(mt, f"fp32 D={D} GQA causal ragged", [300, 77, 513, 1], [300, 77, 513, 1], 8, 2, D, f, causal=True)
+        _bwd(mt, f"fp32 bwd D={D} GQA causal ragged", [200, 91, 333, 1], [200, 91, 333, 1], 8, 2, D, f, 1e-4,
+             causal=True)
+    _fwd(mt, "fp32 D=64 cross window", [64, 200], [333, 260], 8, 2, 64, f, causal=True, window=100)
+    _bwd(mt, "fp32 bwd D=96 cross window", [150, 40], [410, 30], 4, 4, 96, f, 1e-4, causal=True, window=90)
+    _bwd(mt, "fp32 bwd D=128 cross non-causal GQA", [100, 33], [250, 700], 8, 4, 128, f, 1e-4)
+    _bwd(mt, "fp32 bwd D=64 tile edges", [1, 31, 32, 33, 127, 128, 129], [1, 31, 32, 33, 127, 128, 129], 4, 2, 64,
+         f, 1e-4, causal=True)
+    _bwd(mt, "fp32 bwd D=64 per-head bias", [640], [640], 8, 4, 64, f, 1e-4, bias=_make_bias(640, 8, 640, False))
+    _bwd(mt, "fp32 bwd D=128 broadcast bias causal ragged", [300, 212], [300, 212], 8, 8, 128, f, 1e-4,
+         causal=True, bias=_make_bias(512, 8, 300, True))
+    _banner("fp32 matrix cores and portable kernels vs the fp64 oracle")
+    lens = [700, 129]
+    q, k, v = _inputs(lens, lens, 8, 2, 128, f, seed=4)
+    dout = randn((sum(lens), 8, 128), f, torch.Generator().manual_seed(5))
+    cu = cu_of(lens, "cuda")
+    res = []
+    for env in ("0", "1"):
+        monkeypatch.setenv("MTLATTN_NO_MFMA", env)
+        qm, km, vm = (t.cuda().requires_grad_() for t in (q, k, v))
+        out = mt.varlen_attention(qm, km, vm, cu, cu, max(lens), causal=True, window=300)
+        out.backward(dout.cuda())
+        torch.cuda.synchronize()
+        res.append([t.detach().cpu() for t in (out, qm.grad, km.grad, vm.grad)])
+    monkeypatch.delenv("MTLATTN_NO_MFMA")
+    args = (q, k, v, dout, cu_of(lens), cu_of(lens), None, True, 300, None)
+    r64 = oracle.varlen_forward_backward(*args, dtype=torch.float64)
+    r32 = oracle.varlen_forward_backward(*args, dtype=torch.float32)
+    for i, (nm, j) in enumerate((("out", 0), ("dQ", 2), ("dK", 3), ("dV", 4))):
+        floor32 = err_stats(r32[j], r64[j], f)["rel"]
+        for path, r in zip(("matrix cores", "portable"), res):
+            st = err_stats(r[i], r64[j], f, floor32)
+            print(f"  {nm} {path}: rel={st['rel']:.3e} floor32={floor32:.3e}", flush=True)
+            assert st["ok_elem"], f"{nm} {path}: {st}"
+
+
 def test_bwd_fp16(mt):
     h = torch.float16
     _bwd(mt, "bwd fp16 causal", [256], [256], 8, 8, 128, h, 5e-3, causal=True)
@@ -607,7 +654,9 @@ def test_empty_sequences(mt):
     cases = [
         ("bf16 D128 GQA non-causal", [0, 300, 5, 129, 0], [50, 300, 0, 129, 0], 8, 2, 128, torch.bfloat16, False),
         ("fp16 D64 causal", [0, 200, 7, 64], [40, 200, 0, 64], 4, 4, 64, torch.float16, True),
-        ("fp32 D64 non-causal (portable)", [0, 30, 5, 12], [50, 30, 0, 12], 4, 2, 64, torch.float32, False),
+        ("fp32 D64 non-causal (fp32 matrix cores)", [0, 30, 5, 12], [50, 30, 0, 12], 4, 2, 64, torch.float32,
+         False),
+        ("fp32 D66 causal (portable)", [0, 30, 5, 12], [50, 30, 0, 12], 4, 2, 66, torch.float32, True),
     ]
     for name, ql, kl, hq, hkv, d, dt, causal in cases:
         _banner(f"empty sequences: {name}")
@@ -792,7 +841,8 @@ def test_bias_per_sequence_rows(mt):
         ("bf16 D128 ragged causal", [300, 77, 513], [300, 77, 513], 8, 2, 128, torch.bfloat16, True, (3, 8), 513),
         ("fp16 D64 broadcast batch+head", [200, 650], [200, 650], 4, 4, 64, torch.float16, False, (1, 1), 650),
         ("bf16 rows past Nq clamp", [100, 260], [100, 260], 8, 8, 128, torch.bfloat16, True, (2, 1), 200),
-        ("fp32 portable kernels", [40, 90], [40, 90], 4, 2, 64, torch.float32, True, (2, 4), 90),
+        ("fp32 matrix-core kernels", [40, 90], [40, 90], 4, 2, 64, torch.float32, True, (2, 4), 90),
+        ("fp32 portable kernels", [40, 90], [40, 90], 4, 2, 66, torch.float32, True, (2, 4), 90),
         ("decode q_len 2", [2, 1], [3000, 2500], 8, 2, 128, torch.bfloat16, True, (2, 8), 2),
     ]
     for name, ql, kl, hq, hkv, d, dt, causal, (bb, bh), nq in cases:
