@@ -4,6 +4,7 @@
 // Metal-specific; it never allocates device memory and never syncs the host.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -378,9 +379,40 @@ int mtlattn_varlen_fwd_noalloc(const mtlattn_problem* p, const void* q, int64_t 
     return mtlattn_varlen_fwd(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, ws, need, stream);
 }
 
+namespace {
+
+size_t bwd_delta_bytes(const mtlattn_problem* p) { return (size_t)p->total_q * (size_t)p->num_heads_q * sizeof(float); }
+// offset of the fp32 dK/dV partials in the backward workspace
+size_t bwd_part_offset(const mtlattn_problem* p) { return (bwd_delta_bytes(p) + 255) / 256 * 256; }
+
+// Splits of the fp32 matrix-core dK/dV: its grid has one workgroup per 128
+// keys and kv head, which leaves CUs idle on small problems and few kv heads;
+// split each workgroup's (query head, query tile) iterations until there are
+// about two workgroups per CU, at most 8 splits and no more than the
+// iterations of the longest sequence.
+int f32_dkv_splits(const mtlattn_problem* p) {
+    if (p->dtype != MTLATTN_DTYPE_F32 || !f32_mfma_head_dim(p->head_dim) || force_generic() || p->total_q <= 0 ||
+        p->total_kv <= 0)
+        return 1;
+    const int64_t tiles = std::max<int64_t>((p->total_kv + 127) / 128, p->num_seqs);
+    const int64_t wgs = tiles * p->num_heads_kv, want = 2 * (int64_t)device_cus();
+    if (wgs >= want) return 1;
+    const int64_t iters = (int64_t)(p->num_heads_q / p->num_heads_kv) * ((std::max<int64_t>(p->max_seqlen_q, 1) + 31) / 32);
+    const int64_t ns = std::min<int64_t>(std::min<int64_t>((want + wgs - 1) / wgs, 8), iters);
+    return (int)std::max<int64_t>(ns, 1);
+}
+
+size_t bwd_part_bytes(const mtlattn_problem* p, int splits) {
+    return (size_t)f32_dkv_part_floats(splits, p->total_kv, p->num_heads_kv, p->head_dim) * sizeof(float);
+}
+
+}  // namespace
+
 size_t mtlattn_varlen_bwd_workspace_size(const mtlattn_problem* p) {
     if (check_problem(p) != MTLATTN_OK) return 0;
-    return (size_t)p->total_q * (size_t)p->num_heads_q * sizeof(float);
+    const int splits = f32_dkv_splits(p);
+    if (splits > 1) return bwd_part_offset(p) + bwd_part_bytes(p, splits);
+    return bwd_delta_bytes(p);
 }
 
 int mtlattn_bwd_preprocess(const mtlattn_problem* p, const void* out, int64_t out_row_stride, const void* dout,
@@ -450,10 +482,13 @@ int mtlattn_bwd_dq(const mtlattn_problem* p, const void* q, int64_t q_row_stride
     return launch_status(launch_bwd_dq_generic(p->dtype, a, st), "generic dQ");
 }
 
-int mtlattn_bwd_dkv(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
-                    int64_t k_row_stride, const void* v, int64_t v_row_stride, const void* dout,
-                    int64_t dout_row_stride, const float* lse, const float* delta, void* dk, void* dv,
-                    int32_t dkv_dtype, void* stream) {
+namespace {
+
+// mtlattn_bwd_dkv, with fp32 dK/dV partials for `splits` splits in `part`
+// (fp32 matrix-core path only; splits == 1: none)
+int bwd_dkv(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k, int64_t k_row_stride,
+            const void* v, int64_t v_row_stride, const void* dout, int64_t dout_row_stride, const float* lse,
+            const float* delta, void* dk, void* dv, int32_t dkv_dtype, void* stream, float* part, int splits) {
     int rc = check_problem(p);
     if (rc != MTLATTN_OK) return rc;
     if (dkv_dtype != MTLATTN_DTYPE_F32 && dkv_dtype != p->dtype)
@@ -470,9 +505,22 @@ int mtlattn_bwd_dkv(const mtlattn_problem* p, const void* q, int64_t q_row_strid
     if (bwd_mfma_ok(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride))
         return launch_status(launch_bwd_dkv_mfma(p->dtype, a, st), "dK/dV");
     if (bwd_f32_ok(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride) &&
-        ((uintptr_t)dk & 15u) == 0 && ((uintptr_t)dv & 15u) == 0)
+        ((uintptr_t)dk & 15u) == 0 && ((uintptr_t)dv & 15u) == 0) {
+        a.f32_part = part;
+        a.f32_splits = part != nullptr ? splits : 1;
         return launch_status(launch_bwd_dkv_f32mfma(a, st), "fp32 dK/dV");
+    }
     return launch_status(launch_bwd_dkv_generic(p->dtype, a, st), "generic dK/dV");
+}
+
+}  // namespace
+
+int mtlattn_bwd_dkv(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
+                    int64_t k_row_stride, const void* v, int64_t v_row_stride, const void* dout,
+                    int64_t dout_row_stride, const float* lse, const float* delta, void* dk, void* dv,
+                    int32_t dkv_dtype, void* stream) {
+    return bwd_dkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride, lse, delta, dk, dv,
+                   dkv_dtype, stream, nullptr, 1);
 }
 
 int mtlattn_varlen_bwd(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
@@ -481,11 +529,21 @@ int mtlattn_varlen_bwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
                        void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes, void* stream) {
     int rc = check_problem(p);
     if (rc != MTLATTN_OK) return rc;
-    const size_t need = mtlattn_varlen_bwd_workspace_size(p);
+    // delta is required; the fp32 dK/dV partials after it are used when the
+    // workspace holds them (mtlattn_varlen_bwd_workspace_size), else dK/dV
+    // runs unsplit
+    const size_t need = bwd_delta_bytes(p);
     if (workspace_bytes < need || (need > 0 && workspace == nullptr))
         return fail(MTLATTN_ERR_WORKSPACE, "mtlattn: backward workspace too small (%zu < %zu bytes)",
                     workspace_bytes, need);
     float* delta = (float*)workspace;
+    int splits = f32_dkv_splits(p);
+    float* part = nullptr;
+    if (splits > 1 && workspace != nullptr && ((uintptr_t)workspace & 15u) == 0 &&
+        workspace_bytes >= bwd_part_offset(p) + bwd_part_bytes(p, splits))
+        part = (float*)((char*)workspace + bwd_part_offset(p));
+    else
+        splits = 1;
     // Head dims 64 and 128 on the matrix-core path: the dQ kernel computes
     // delta from O and dO itself (bitwise equal to the preprocess) and leaves
     // it in the workspace for dK/dV, which saves the preprocess's pass over dO.
@@ -511,8 +569,8 @@ int mtlattn_varlen_bwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
                             delta, dq, p->dtype, stream);
         if (rc != MTLATTN_OK) return rc;
     }
-    rc = mtlattn_bwd_dkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride, lse, delta,
-                         dk, dv, p->dtype, stream);
+    rc = bwd_dkv(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride, lse, delta, dk, dv,
+                 p->dtype, stream, part, splits);
     if (rc != MTLATTN_OK) return rc;
     // Rows outside every sequence take no part in the forward: zero gradient.
     hipStream_t st = (hipStream_t)stream;

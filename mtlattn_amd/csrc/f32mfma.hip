@@ -54,6 +54,11 @@ struct F32Params {
     int num_seqs, hq, hkv, g, d;
     float scale;
     int causal, window;
+    // dK/dV split over its (query head, query tile) iterations: split z of
+    // nsplit writes unscaled fp32 partials to part + z * 2 * total_kv * hkv * d
+    // (dK, then dV); part == nullptr: one split writing dk / dv
+    float* part;
+    int nsplit;
 };
 
 __device__ inline f32x16_t mma(float a, float b, const f32x16_t& c) {
@@ -397,7 +402,10 @@ __global__ __launch_bounds__(256, 1) void f32_dq_kernel(F32Params p) {
 
 // ---------------------------------------------------------------------------
 // dV = P^T.dO, dK = scale * dS^T.Q, summed over the g query heads of the kv
-// head in a fixed order (no atomics).
+// head in a fixed order (no atomics). Grids with fewer workgroups than the
+// GPU holds split the (head, query tile) iterations of each workgroup over
+// blockIdx.z; f32_dkv_reduce_kernel then adds the splits in order z = 0, 1,
+// ... (deterministic for a given split count).
 // ---------------------------------------------------------------------------
 template <int DP>
 __global__ __launch_bounds__(256, 1) void f32_dkv_kernel(F32Params p) {
@@ -417,7 +425,8 @@ __global__ __launch_bounds__(256, 1) void f32_dkv_kernel(F32Params p) {
     const Band qz = query_band(jlast, coff, q_len, kv_len, p.causal, p.window);
     const int qlo = qa.lo & ~31, qhi = qz.lo + (int)qz.width;
     const int nq = qhi > qlo ? (qhi - qlo + 31) / 32 : 0;
-    const int n_it = nq * p.g;
+    const int z = (int)blockIdx.z;
+    const int it0 = (int)((int64_t)nq * p.g * z / p.nsplit), it1 = (int)((int64_t)nq * p.g * (z + 1) / p.nsplit);
 
     const int wj0 = j0 + 32 * w;
     const bool wave_on = wj0 < kv_len;
@@ -459,16 +468,16 @@ __global__ __launch_bounds__(256, 1) void f32_dkv_kernel(F32Params p) {
         if (t < 64) slot[2 * KSZ + 2 * TSZ + t] = lse_d;
     };
 
-    if (n_it > 0) {
-        load_tile(0);
+    if (it1 > it0) {
+        load_tile(it0);
         store_tile(lds);
     }
     __syncthreads();
-    for (int it = 0; it < n_it; ++it) {
+    for (int it = it0; it < it1; ++it) {
         const int hh = it / nq, qt = qlo + 32 * (it - hh * nq), head = hk * p.g + hh;
-        const bool more = it + 1 < n_it;
+        const bool more = it + 1 < it1;
         if (more) load_tile(it + 1);
-        const float* qs = lds + (it & 1) * SLOT;
+        const float* qs = lds + ((it - it0) & 1) * SLOT;
         if (wave_on && qt < whi && qt + 32 > wlo) {
             // P first and its dV product, then dP and dS (P is 0 wherever
             // the key is masked for the query, so dS is too)
@@ -508,13 +517,38 @@ __global__ __launch_bounds__(256, 1) void f32_dkv_kernel(F32Params p) {
             row_product<DP>(qs + 2 * KSZ, l32, h, ds,         // Q transposed
                             [&](int b, const f32x16_t& part) { dka[b] += part; });
         }
-        if (more) store_tile(lds + ((it + 1) & 1) * SLOT);
+        if (more) store_tile(lds + ((it + 1 - it0) & 1) * SLOT);
         __syncthreads();
     }
     if (wave_on && kvalid) {
-        store_row<DP>(p.dk + (krow * p.hkv + hk) * p.d, dka, h, p.d, p.scale);
-        store_row<DP>(p.dv + (krow * p.hkv + hk) * p.d, dva, h, p.d, 1.f);
+        const int64_t o = (krow * p.hkv + hk) * p.d;
+        if (p.part == nullptr) {
+            store_row<DP>(p.dk + o, dka, h, p.d, p.scale);
+            store_row<DP>(p.dv + o, dva, h, p.d, 1.f);
+        } else {
+            float* pk = p.part + (int64_t)z * 2 * p.total_kv * p.hkv * p.d;
+            store_row<DP>(pk + o, dka, h, p.d, 1.f);
+            store_row<DP>(pk + p.total_kv * p.hkv * p.d + o, dva, h, p.d, 1.f);
+        }
     }
+}
+
+// dk = scale * sum_z dK part z, dv = sum_z dV part z, in order z = 0, 1, ...;
+// n4 = total_kv * hkv * d / 4 float4 elements (d % 4 == 0)
+__global__ __launch_bounds__(256) void f32_dkv_reduce_kernel(const float* __restrict__ part, int nsplit, int64_t n4,
+                                                             float scale, float* __restrict__ dk,
+                                                             float* __restrict__ dv) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const int64_t stride = 2 * n4;   // float4 elements per split
+    const f32x4_t* src = reinterpret_cast<const f32x4_t*>(part);
+    f32x4_t a = src[i], b = src[n4 + i];
+    for (int z = 1; z < nsplit; ++z) {
+        a += src[z * stride + i];
+        b += src[z * stride + n4 + i];
+    }
+    reinterpret_cast<f32x4_t*>(dk)[i] = a * scale;
+    reinterpret_cast<f32x4_t*>(dv)[i] = b;
 }
 
 F32Params make_params(const Geometry& g) {
@@ -525,20 +559,22 @@ F32Params make_params(const Geometry& g) {
     p.total_q = g.total_q; p.total_kv = g.total_kv;
     p.num_seqs = g.num_seqs; p.hq = g.hq; p.hkv = g.hkv; p.g = g.g; p.d = g.d;
     p.scale = g.scale; p.causal = g.causal; p.window = g.window > 0 ? g.window : 0;
+    p.part = nullptr; p.nsplit = 1;
     return p;
 }
 
 using F32Kernel = void (*)(F32Params);
 
 hipError_t launch(const F32Params& p, int64_t total_rows, int heads, hipStream_t st, F32Kernel k32, F32Kernel k64,
-                  F32Kernel k96, F32Kernel k128) {
+                  F32Kernel k96, F32Kernel k128, int splits = 1) {
     if (total_rows <= 0 || heads <= 0) return hipSuccess;
-    if (!f32_mfma_head_dim(p.d) || p.num_seqs <= 0 || heads > 65535) return hipErrorInvalidValue;
-    const int64_t blocks = total_rows / kWgRows + p.num_seqs + 1;
+    if (!f32_mfma_head_dim(p.d) || p.num_seqs <= 0 || heads > 65535 || splits < 1 || splits > 64)
+        return hipErrorInvalidValue;
+    const int64_t blocks = f32_row_tiles(total_rows, p.num_seqs);
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     const int dp = (p.d + 31) / 32 * 32;
     const F32Kernel k = dp == 32 ? k32 : dp == 64 ? k64 : dp == 96 ? k96 : k128;
-    hipLaunchKernelGGL(k, dim3((unsigned)blocks, (unsigned)heads), dim3(256), 0, st, p);
+    hipLaunchKernelGGL(k, dim3((unsigned)blocks, (unsigned)heads, (unsigned)splits), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 
@@ -567,8 +603,16 @@ hipError_t launch_bwd_dkv_f32mfma(const BwdArgs& a, hipStream_t st) {
     p.q = (const float*)a.q; p.k = (const float*)a.k; p.v = (const float*)a.v; p.dout = (const float*)a.dout;
     p.q_rs = a.q_rs; p.k_rs = a.k_rs; p.v_rs = a.v_rs; p.do_rs = a.do_rs;
     p.lse_in = a.lse; p.delta = a.delta; p.dk = (float*)a.dk; p.dv = (float*)a.dv;
-    return launch(p, a.geo.total_kv, a.geo.hkv, st, f32_dkv_kernel<32>, f32_dkv_kernel<64>, f32_dkv_kernel<96>,
-                  f32_dkv_kernel<128>);
+    const int splits = a.f32_part != nullptr && a.f32_splits > 1 ? a.f32_splits : 1;
+    p.part = splits > 1 ? a.f32_part : nullptr;
+    p.nsplit = splits;
+    hipError_t e = launch(p, a.geo.total_kv, a.geo.hkv, st, f32_dkv_kernel<32>, f32_dkv_kernel<64>,
+                          f32_dkv_kernel<96>, f32_dkv_kernel<128>, splits);
+    if (e != hipSuccess || splits == 1 || a.geo.total_kv <= 0) return e;
+    const int64_t n4 = a.geo.total_kv * a.geo.hkv * a.geo.d / 4;
+    hipLaunchKernelGGL(f32_dkv_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, p.part, splits,
+                       n4, p.scale, p.dk, p.dv);
+    return hipGetLastError();
 }
 
 }  // namespace mtlattn

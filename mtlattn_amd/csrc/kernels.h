@@ -48,6 +48,11 @@ struct BwdArgs {
     // dK/dV kernel, in place of the separate preprocess (head dims 64 and 128)
     const void* o = nullptr; int64_t o_rs = 0;
     float* delta_out = nullptr;
+    // fp32 matrix-core dK/dV only: f32_splits > 1 splits each workgroup's
+    // work over that many workgroups, with fp32 partials in f32_part
+    // (f32_dkv_part_floats floats) summed in a fixed order afterwards
+    float* f32_part = nullptr;
+    int f32_splits = 1;
 };
 
 struct DecodeArgs {
@@ -116,6 +121,11 @@ inline bool mfma_head_dim(int d) {
 // head dims of the fp32 matrix-core kernels (columns padded to a multiple
 // of 32 with zeros)
 inline bool f32_mfma_head_dim(int d) { return d > 0 && d <= 128 && d % 4 == 0; }
+// grid x of the fp32 matrix-core kernels: 128-row tiles over every sequence
+inline int64_t f32_row_tiles(int64_t total_rows, int num_seqs) { return total_rows / 128 + num_seqs + 1; }
+inline int64_t f32_dkv_part_floats(int splits, int64_t total_kv, int hkv, int d) {
+    return splits > 1 ? (int64_t)splits * 2 * total_kv * hkv * d : 0;
+}
 // head dims of the split-KV decode kernels
 inline bool decode_head_dim(int d) { return d == 64 || d == 128; }
 

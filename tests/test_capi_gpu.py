@@ -165,6 +165,65 @@ def test_capi_fused_delta_matches_separate_kernels(D, dtype, causal, window, bia
                            ("dv", dv[:int(ck[-1])].cpu(), rv)], dtype)
 
 
+def test_capi_fp32_split_dkv():
+    """fp32 on the fp32 matrix-core kernels: when the dK/dV grid (one
+    workgroup per 128 keys and kv head) would leave CUs idle, the backward
+    workspace query adds room for fp32 partials and mtlattn_varlen_bwd splits
+    each workgroup's (query head, query tile) iterations, summing the splits
+    in a fixed order. Checked: the split path is taken (workspace larger than
+    delta), its gradients against the fp64 oracle, bitwise equal on a second
+    call, a NaN-filled workspace does not leak into owned rows, rows outside
+    every sequence are zero, and a delta-sized workspace (unsplit) gives
+    bitwise the separate mtlattn_bwd_dkv entry's dK / dV."""
+    print("\n[case] capi fp32 split dK/dV: ragged GQA causal window, empty sequence, trailing rows", flush=True)
+    q_lens, kv_lens, Hq, Hkv, D = [300, 0, 131, 1, 700], [300, 5, 200, 33, 700], 16, 2, 128
+    dtype = torch.float32
+    q, k, v, do, cq, ck = _case(q_lens, kv_lens, Hq, Hkv, D, dtype, seed=21)
+    g = torch.Generator().manual_seed(22)
+    q, do = (torch.cat([t, randn((3, Hq, D), dtype, g)]) for t in (q, do))
+    k, v = (torch.cat([t, randn((3, Hkv, D), dtype, g)]) for t in (k, v))
+    scale = 1.0 / math.sqrt(D)
+    qd, kd, vd, dod, cqd, ckd = (t.cuda() for t in (q, k, v, do, cq, ck))
+    p = capi.problem_for(qd, kd, cqd, ckd, max(q_lens), scale, causal=True, window=250)
+    out = torch.empty_like(qd)
+    lse = torch.empty(qd.shape[0], Hq, dtype=torch.float32, device="cuda")
+    s = _stream()
+    capi.call("mtlattn_varlen_fwd", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
+              out.data_ptr(), lse.data_ptr(), None, 0, s)
+    ws_n = capi.lib().mtlattn_varlen_bwd_workspace_size(p)
+    delta_n = qd.shape[0] * Hq * 4
+    assert ws_n > delta_n, "expected the split dK/dV workspace for this small grid"
+    runs = []
+    for n in (ws_n, ws_n, delta_n):
+        ws = torch.full((n // 4,), float("nan"), dtype=torch.float32, device="cuda")
+        dq, dk, dv = (torch.full_like(t, float("nan")) for t in (qd, kd, vd))
+        capi.call("mtlattn_varlen_bwd", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
+                  out.data_ptr(), Hq * D, dod.data_ptr(), Hq * D, lse.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                  dv.data_ptr(), ws.data_ptr(), n, s)
+        torch.cuda.synchronize()
+        runs.append([t.cpu() for t in (dq, dk, dv)])
+    delta = torch.empty((qd.shape[0], Hq), dtype=torch.float32, device="cuda")
+    capi.call("mtlattn_bwd_preprocess", p, out.data_ptr(), Hq * D, dod.data_ptr(), Hq * D, delta.data_ptr(), s)
+    dk2, dv2 = torch.empty_like(kd), torch.empty_like(vd)
+    capi.call("mtlattn_bwd_dkv", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
+              dod.data_ptr(), Hq * D, lse.data_ptr(), delta.data_ptr(), dk2.data_ptr(), dv2.data_ptr(),
+              capi.DTYPE_F32, s)
+    torch.cuda.synchronize()
+    nq, nk = int(cq[-1]), int(ck[-1])
+    for a, b in zip(runs[0], runs[1]):
+        assert torch.equal(a, b), "split dK/dV not bitwise repeatable"
+    assert torch.equal(runs[2][1][:nk], dk2[:nk].cpu()) and torch.equal(runs[2][2][:nk], dv2[:nk].cpu())
+    for r in runs:
+        assert not r[0][nq:].any() and not r[1][nk:].any() and not r[2][nk:].any()
+    args = (q[:nq], k[:nk], v[:nk], do[:nq], cq, ck, scale, True, 250)
+    r64 = oracle.varlen_forward_backward(*args, dtype=torch.float64)
+    r32 = oracle.varlen_forward_backward(*args, dtype=torch.float32)
+    floors = [err_stats(r32[i], r64[i], dtype)["rel"] for i in (2, 3, 4)]
+    for name, r in (("split", runs[0]), ("unsplit", runs[2])):
+        _check(f"fp32 {name}", [("dq", r[0][:nq], r64[2]), ("dk", r[1][:nk], r64[3]), ("dv", r[2][:nk], r64[4])],
+               dtype, floors)
+
+
 def test_capi_splitkv_and_workspace_errors():
     print("\n[case] capi split-KV decode bf16 + workspace check", flush=True)
     kv_lens, Hq, Hkv, D = [3000, 5000, 2048], 16, 2, 128
