@@ -147,10 +147,11 @@ int mtlattn_varlen_fwd_noalloc(const mtlattn_problem* p,
  * workspace (fp32 [total_q, Hq]) holds delta = rowsum(dO * O) of every row a
  * sequence owns when the call returns; at head dims 64 and 128 the dQ kernel
  * computes it (no separate preprocess launch), bitwise equal to
- * mtlattn_bwd_preprocess. For fp32 problems on the fp32 matrix-core kernels
- * whose dK/dV grid would leave CUs idle, the size query adds room (after
- * delta, 256-byte aligned) for fp32 dK/dV partials of 2-8 splits, summed in a
- * fixed order; a workspace of only the delta size runs dK/dV unsplit.
+ * mtlattn_bwd_preprocess. On the fp32 matrix-core kernels the dQ kernel
+ * computes delta too (equal to the preprocess up to fp32 rounding); for fp32
+ * problems whose dQ or dK/dV grid would leave CUs idle, the size query adds
+ * room (after delta, 256-byte aligned) for fp32 partials of 2-8 splits,
+ * summed in a fixed order; a workspace of only the delta size runs unsplit.
  */
 size_t mtlattn_varlen_bwd_workspace_size(const mtlattn_problem* p);
 int mtlattn_varlen_bwd(const mtlattn_problem* p,

@@ -402,16 +402,34 @@ int f32_dkv_splits(const mtlattn_problem* p) {
     return (int)std::max<int64_t>(ns, 1);
 }
 
-size_t bwd_part_bytes(const mtlattn_problem* p, int splits) {
-    return (size_t)f32_dkv_part_floats(splits, p->total_kv, p->num_heads_kv, p->head_dim) * sizeof(float);
+// Splits of the fp32 matrix-core dQ over its key tiles, by the same rule
+// (one workgroup per 128 query rows and head; the key tiles of a workgroup
+// bounded by total_kv).
+int f32_dq_splits(const mtlattn_problem* p) {
+    if (p->dtype != MTLATTN_DTYPE_F32 || !f32_mfma_head_dim(p->head_dim) || force_generic() || p->total_q <= 0 ||
+        p->total_kv <= 0)
+        return 1;
+    const int64_t tiles = std::max<int64_t>((p->total_q + 127) / 128, p->num_seqs);
+    const int64_t wgs = tiles * p->num_heads_q, want = 2 * (int64_t)device_cus();
+    if (wgs >= want) return 1;
+    const int64_t ns = std::min<int64_t>(std::min<int64_t>((want + wgs - 1) / wgs, 8), (p->total_kv + 31) / 32);
+    return (int)std::max<int64_t>(ns, 1);
+}
+
+// fp32 partial bytes after delta: dQ's, then (in the same space, after the
+// dQ splits are summed) dK/dV's
+size_t bwd_part_bytes(const mtlattn_problem* p) {
+    const int64_t fq = f32_dq_part_floats(f32_dq_splits(p), p->total_q, p->num_heads_q, p->head_dim);
+    const int64_t fk = f32_dkv_part_floats(f32_dkv_splits(p), p->total_kv, p->num_heads_kv, p->head_dim);
+    return (size_t)std::max<int64_t>(fq, fk) * sizeof(float);
 }
 
 }  // namespace
 
 size_t mtlattn_varlen_bwd_workspace_size(const mtlattn_problem* p) {
     if (check_problem(p) != MTLATTN_OK) return 0;
-    const int splits = f32_dkv_splits(p);
-    if (splits > 1) return bwd_part_offset(p) + bwd_part_bytes(p, splits);
+    const size_t part = bwd_part_bytes(p);
+    if (part > 0) return bwd_part_offset(p) + part;
     return bwd_delta_bytes(p);
 }
 
@@ -537,13 +555,14 @@ int mtlattn_varlen_bwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
         return fail(MTLATTN_ERR_WORKSPACE, "mtlattn: backward workspace too small (%zu < %zu bytes)",
                     workspace_bytes, need);
     float* delta = (float*)workspace;
-    int splits = f32_dkv_splits(p);
+    int splits = f32_dkv_splits(p), dq_splits = f32_dq_splits(p);
     float* part = nullptr;
-    if (splits > 1 && workspace != nullptr && ((uintptr_t)workspace & 15u) == 0 &&
-        workspace_bytes >= bwd_part_offset(p) + bwd_part_bytes(p, splits))
+    const size_t part_bytes = bwd_part_bytes(p);
+    if (part_bytes > 0 && workspace != nullptr && ((uintptr_t)workspace & 15u) == 0 &&
+        workspace_bytes >= bwd_part_offset(p) + part_bytes)
         part = (float*)((char*)workspace + bwd_part_offset(p));
     else
-        splits = 1;
+        splits = dq_splits = 1;
     // Head dims 64 and 128 on the matrix-core path: the dQ kernel computes
     // delta from O and dO itself (bitwise equal to the preprocess) and leaves
     // it in the workspace for dK/dV, which saves the preprocess's pass over dO.
@@ -551,6 +570,10 @@ int mtlattn_varlen_bwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
                             bwd_mfma_ok(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout,
                                         dout_row_stride) &&
                             ((uintptr_t)out & 15u) == 0 && out_row_stride % 8 == 0;
+    const bool fuse_delta_f32 = p->total_q > 0 && out != nullptr && dout != nullptr &&
+                                bwd_f32_ok(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout,
+                                           dout_row_stride) &&
+                                aligned16(out, out_row_stride, p->dtype) && ((uintptr_t)dq & 15u) == 0;
     if (fuse_delta) {
         if (q == nullptr || out == nullptr || dout == nullptr || lse == nullptr || dq == nullptr ||
             (p->total_kv > 0 && (k == nullptr || v == nullptr)))
@@ -561,6 +584,21 @@ int mtlattn_varlen_bwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
         a.o_rs = out_row_stride;
         a.delta_out = delta;
         rc = launch_status(launch_bwd_dq_mfma(p->dtype, a, (hipStream_t)stream), "dQ");
+        if (rc != MTLATTN_OK) return rc;
+    } else if (fuse_delta_f32) {
+        // fp32 matrix cores: the dQ kernel computes delta from O and dO (equal
+        // to the preprocess up to fp32 rounding) and leaves it in the workspace
+        if (q == nullptr || lse == nullptr || dq == nullptr || (p->total_kv > 0 && (k == nullptr || v == nullptr)))
+            return fail(MTLATTN_ERR_INVALID, "mtlattn: null pointer argument");
+        BwdArgs a = make_bwd(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, dout, dout_row_stride, lse, delta);
+        a.dq = dq;
+        a.out_f32 = 1;
+        a.o = out;
+        a.o_rs = out_row_stride;
+        a.delta_out = delta;
+        a.f32_part = part;
+        a.f32_splits = part != nullptr ? dq_splits : 1;
+        rc = launch_status(launch_bwd_dq_f32mfma(a, (hipStream_t)stream), "fp32 dQ");
         if (rc != MTLATTN_OK) return rc;
     } else if (p->total_q > 0) {
         rc = mtlattn_bwd_preprocess(p, out, out_row_stride, dout, dout_row_stride, delta, stream);

@@ -54,11 +54,16 @@ struct F32Params {
     int num_seqs, hq, hkv, g, d;
     float scale;
     int causal, window;
-    // dK/dV split over its (query head, query tile) iterations: split z of
-    // nsplit writes unscaled fp32 partials to part + z * 2 * total_kv * hkv * d
-    // (dK, then dV); part == nullptr: one split writing dk / dv
+    // dQ split over its key tiles, dK/dV over its (query head, query tile)
+    // iterations: split z of nsplit writes unscaled fp32 partials to
+    // part + z * total_q * hq * d (dQ) or part + z * 2 * total_kv * hkv * d
+    // (dK, then dV); part == nullptr: one split writing dq / dk / dv
     float* part;
     int nsplit;
+    // dQ only: o != nullptr computes delta = rowsum(dO * O) in the kernel
+    // (written to delta_out by split 0) instead of reading delta
+    const float* o_in; int64_t o_rs;
+    float* delta_out;
 };
 
 __device__ inline f32x16_t mma(float a, float b, const f32x16_t& c) {
@@ -308,7 +313,9 @@ __global__ __launch_bounds__(256, DP <= 96 ? 2 : 1) void f32_fwd_kernel(F32Param
 }
 
 // ---------------------------------------------------------------------------
-// dQ = scale * dS.K with dS = P * (dP - delta), dP = dO.V^T.
+// dQ = scale * dS.K with dS = P * (dP - delta), dP = dO.V^T. Grids with fewer
+// workgroups than the GPU holds split each workgroup's key tiles over
+// blockIdx.z; f32_split_sum_kernel adds the splits in order.
 // ---------------------------------------------------------------------------
 template <int DP>
 __global__ __launch_bounds__(256, 1) void f32_dq_kernel(F32Params p) {
@@ -326,6 +333,8 @@ __global__ __launch_bounds__(256, 1) void f32_dq_kernel(F32Params p) {
     const Band bz = key_band(qlast, coff, kv_len, p.causal, p.window);
     const int klo = ba.lo & ~31, khi = bz.lo + (int)bz.width;
     const int ntiles = khi > klo ? (khi - klo + 31) / 32 : 0;
+    const int z = (int)blockIdx.z;
+    const int it0 = (int)((int64_t)ntiles * z / p.nsplit), it1 = (int)((int64_t)ntiles * (z + 1) / p.nsplit);
 
     const int wq0 = q0 + 32 * w;
     const bool wave_on = wq0 < q_len;
@@ -339,13 +348,25 @@ __global__ __launch_bounds__(256, 1) void f32_dq_kernel(F32Params p) {
     const bool qvalid = qi < q_len;
     const int64_t grow = (int64_t)tl.start + qi;
     const float lse = qvalid ? p.lse_in[grow * p.hq + head] : kNegInf;
-    const float dlt = qvalid ? p.delta[grow * p.hq + head] : 0.f;
     // a row with no keys (LSE -inf) has P = 0 everywhere
     const Band qb = (qvalid && lse != kNegInf) ? key_band(qi, coff, kv_len, p.causal, p.window) : Band{0, 0u};
 
     float qreg[HD], doreg[HD];
     load_half_row<DP>(qreg, p.q + grow * p.q_rs + (int64_t)head * p.d, qvalid, h, p.d);
     load_half_row<DP>(doreg, p.dout + grow * p.do_rs + (int64_t)head * p.d, qvalid, h, p.d);
+    float dlt;
+    if (p.o_in != nullptr) {
+        // delta over the lane's half row of dO and O, then the two halves
+        float oreg[HD];
+        load_half_row<DP>(oreg, p.o_in + grow * p.o_rs + (int64_t)head * p.d, qvalid, h, p.d);
+        float part = 0.f;
+#pragma unroll
+        for (int j = 0; j < HD; ++j) part = fmaf(doreg[j], oreg[j], part);
+        dlt = pair_sum(part);
+        if (qvalid && wave_on && z == 0 && h == 0) p.delta_out[grow * p.hq + head] = dlt;
+    } else {
+        dlt = qvalid ? p.delta[grow * p.hq + head] : 0.f;
+    }
     const float* brow = (p.bias != nullptr && qvalid)
                             ? p.bias + bias_row_offset(grow, tl.s, tl.start, p.bias_qs, p.bias_ss, p.bias_rows) +
                                   (int64_t)head * p.bias_hs
@@ -358,21 +379,22 @@ __global__ __launch_bounds__(256, 1) void f32_dq_kernel(F32Params p) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = f32x16_t{};
 
-    if (ntiles > 0) {
-        tk.load(kbase + (int64_t)klo * p.k_rs, p.k_rs, kv_len - klo, p.d, t);
-        tv.load(vbase + (int64_t)klo * p.v_rs, p.v_rs, kv_len - klo, p.d, t);
+    if (it1 > it0) {
+        const int k0 = klo + 32 * it0;
+        tk.load(kbase + (int64_t)k0 * p.k_rs, p.k_rs, kv_len - k0, p.d, t);
+        tv.load(vbase + (int64_t)k0 * p.v_rs, p.v_rs, kv_len - k0, p.d, t);
         tk.template store<true, true>(lds, lds + 2 * KSZ, t);
         tv.template store<true, false>(lds + KSZ, nullptr, t);
     }
     __syncthreads();
-    for (int it = 0; it < ntiles; ++it) {
+    for (int it = it0; it < it1; ++it) {
         const int kt = klo + 32 * it;
-        const bool more = it + 1 < ntiles;
+        const bool more = it + 1 < it1;
         if (more) {
             tk.load(kbase + (int64_t)(kt + 32) * p.k_rs, p.k_rs, kv_len - kt - 32, p.d, t);
             tv.load(vbase + (int64_t)(kt + 32) * p.v_rs, p.v_rs, kv_len - kt - 32, p.d, t);
         }
-        const float* ks = lds + (it & 1) * SLOT;
+        const float* ks = lds + ((it - it0) & 1) * SLOT;
         if (wave_on && kt < whi && kt + 32 > wlo) {
             const f32x16_t sacc = head_product<DP>(ks + l32 * SR + h * HD, qreg);
             const f32x16_t pacc = head_product<DP>(ks + KSZ + l32 * SR + h * HD, doreg);
@@ -391,20 +413,24 @@ __global__ __launch_bounds__(256, 1) void f32_dq_kernel(F32Params p) {
             row_product<DP>(ks + 2 * KSZ, l32, h, ds, [&](int b, const f32x16_t& part) { acc[b] += part; });
         }
         if (more) {
-            float* nx = lds + ((it + 1) & 1) * SLOT;
+            float* nx = lds + ((it + 1 - it0) & 1) * SLOT;
             tk.template store<true, true>(nx, nx + 2 * KSZ, t);
             tv.template store<true, false>(nx + KSZ, nullptr, t);
         }
         __syncthreads();
     }
-    if (wave_on && qvalid) store_row<DP>(p.dq + (grow * p.hq + head) * p.d, acc, h, p.d, p.scale);
+    if (wave_on && qvalid) {
+        const int64_t o = (grow * p.hq + head) * p.d;
+        if (p.part == nullptr) store_row<DP>(p.dq + o, acc, h, p.d, p.scale);
+        else store_row<DP>(p.part + (int64_t)z * p.total_q * p.hq * p.d + o, acc, h, p.d, 1.f);
+    }
 }
 
 // ---------------------------------------------------------------------------
 // dV = P^T.dO, dK = scale * dS^T.Q, summed over the g query heads of the kv
 // head in a fixed order (no atomics). Grids with fewer workgroups than the
 // GPU holds split the (head, query tile) iterations of each workgroup over
-// blockIdx.z; f32_dkv_reduce_kernel then adds the splits in order z = 0, 1,
+// blockIdx.z; f32_split_sum_kernel then adds the splits in order z = 0, 1,
 // ... (deterministic for a given split count).
 // ---------------------------------------------------------------------------
 template <int DP>
@@ -533,22 +559,24 @@ __global__ __launch_bounds__(256, 1) void f32_dkv_kernel(F32Params p) {
     }
 }
 
-// dk = scale * sum_z dK part z, dv = sum_z dV part z, in order z = 0, 1, ...;
-// n4 = total_kv * hkv * d / 4 float4 elements (d % 4 == 0)
-__global__ __launch_bounds__(256) void f32_dkv_reduce_kernel(const float* __restrict__ part, int nsplit, int64_t n4,
-                                                             float scale, float* __restrict__ dk,
-                                                             float* __restrict__ dv) {
+// Sum of the splits' partials in order z = 0, 1, ...: out0 = scale0 * sum_z
+// part[z][0], and with out1, out1 = sum_z part[z][1]; a split holds nout
+// arrays of n4 float4 elements (d % 4 == 0).
+__global__ __launch_bounds__(256) void f32_split_sum_kernel(const float* __restrict__ part, int nsplit, int64_t n4,
+                                                            float scale0, float* __restrict__ out0,
+                                                            float* __restrict__ out1) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n4) return;
-    const int64_t stride = 2 * n4;   // float4 elements per split
+    const int64_t stride = (out1 != nullptr ? 2 : 1) * n4;   // float4 elements per split
     const f32x4_t* src = reinterpret_cast<const f32x4_t*>(part);
-    f32x4_t a = src[i], b = src[n4 + i];
-    for (int z = 1; z < nsplit; ++z) {
-        a += src[z * stride + i];
-        b += src[z * stride + n4 + i];
+    f32x4_t a = src[i];
+    for (int z = 1; z < nsplit; ++z) a += src[z * stride + i];
+    reinterpret_cast<f32x4_t*>(out0)[i] = a * scale0;
+    if (out1 != nullptr) {
+        f32x4_t b = src[n4 + i];
+        for (int z = 1; z < nsplit; ++z) b += src[z * stride + n4 + i];
+        reinterpret_cast<f32x4_t*>(out1)[i] = b;
     }
-    reinterpret_cast<f32x4_t*>(dk)[i] = a * scale;
-    reinterpret_cast<f32x4_t*>(dv)[i] = b;
 }
 
 F32Params make_params(const Geometry& g) {
@@ -560,6 +588,7 @@ F32Params make_params(const Geometry& g) {
     p.num_seqs = g.num_seqs; p.hq = g.hq; p.hkv = g.hkv; p.g = g.g; p.d = g.d;
     p.scale = g.scale; p.causal = g.causal; p.window = g.window > 0 ? g.window : 0;
     p.part = nullptr; p.nsplit = 1;
+    p.o_in = nullptr; p.o_rs = 0; p.delta_out = nullptr;
     return p;
 }
 
@@ -594,8 +623,19 @@ hipError_t launch_bwd_dq_f32mfma(const BwdArgs& a, hipStream_t st) {
     p.q = (const float*)a.q; p.k = (const float*)a.k; p.v = (const float*)a.v; p.dout = (const float*)a.dout;
     p.q_rs = a.q_rs; p.k_rs = a.k_rs; p.v_rs = a.v_rs; p.do_rs = a.do_rs;
     p.lse_in = a.lse; p.delta = a.delta; p.dq = (float*)a.dq;
-    return launch(p, a.geo.total_q, a.geo.hq, st, f32_dq_kernel<32>, f32_dq_kernel<64>, f32_dq_kernel<96>,
-                  f32_dq_kernel<128>);
+    if (a.o != nullptr && a.delta_out != nullptr) {
+        p.o_in = (const float*)a.o; p.o_rs = a.o_rs; p.delta_out = a.delta_out;
+    }
+    const int splits = a.f32_part != nullptr && a.f32_splits > 1 ? a.f32_splits : 1;
+    p.part = splits > 1 ? a.f32_part : nullptr;
+    p.nsplit = splits;
+    hipError_t e = launch(p, a.geo.total_q, a.geo.hq, st, f32_dq_kernel<32>, f32_dq_kernel<64>, f32_dq_kernel<96>,
+                          f32_dq_kernel<128>, splits);
+    if (e != hipSuccess || splits == 1 || a.geo.total_q <= 0) return e;
+    const int64_t n4 = a.geo.total_q * a.geo.hq * a.geo.d / 4;
+    hipLaunchKernelGGL(f32_split_sum_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, p.part, splits,
+                       n4, p.scale, p.dq, nullptr);
+    return hipGetLastError();
 }
 
 hipError_t launch_bwd_dkv_f32mfma(const BwdArgs& a, hipStream_t st) {
@@ -610,7 +650,7 @@ hipError_t launch_bwd_dkv_f32mfma(const BwdArgs& a, hipStream_t st) {
                           f32_dkv_kernel<96>, f32_dkv_kernel<128>, splits);
     if (e != hipSuccess || splits == 1 || a.geo.total_kv <= 0) return e;
     const int64_t n4 = a.geo.total_kv * a.geo.hkv * a.geo.d / 4;
-    hipLaunchKernelGGL(f32_dkv_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, p.part, splits,
+    hipLaunchKernelGGL(f32_split_sum_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, p.part, splits,
                        n4, p.scale, p.dk, p.dv);
     return hipGetLastError();
 }

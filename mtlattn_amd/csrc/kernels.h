@@ -48,9 +48,10 @@ struct BwdArgs {
     // dK/dV kernel, in place of the separate preprocess (head dims 64 and 128)
     const void* o = nullptr; int64_t o_rs = 0;
     float* delta_out = nullptr;
-    // fp32 matrix-core dK/dV only: f32_splits > 1 splits each workgroup's
-    // work over that many workgroups, with fp32 partials in f32_part
-    // (f32_dkv_part_floats floats) summed in a fixed order afterwards
+    // fp32 matrix-core dQ and dK/dV only: f32_splits > 1 splits each
+    // workgroup's work over that many workgroups, with fp32 partials in
+    // f32_part (f32_dq_part_floats / f32_dkv_part_floats floats) summed in a
+    // fixed order afterwards; dQ also takes o / delta_out (delta in-kernel)
     float* f32_part = nullptr;
     int f32_splits = 1;
 };
@@ -123,6 +124,9 @@ inline bool mfma_head_dim(int d) {
 inline bool f32_mfma_head_dim(int d) { return d > 0 && d <= 128 && d % 4 == 0; }
 // grid x of the fp32 matrix-core kernels: 128-row tiles over every sequence
 inline int64_t f32_row_tiles(int64_t total_rows, int num_seqs) { return total_rows / 128 + num_seqs + 1; }
+inline int64_t f32_dq_part_floats(int splits, int64_t total_q, int hq, int d) {
+    return splits > 1 ? (int64_t)splits * total_q * hq * d : 0;
+}
 inline int64_t f32_dkv_part_floats(int splits, int64_t total_kv, int hkv, int d) {
     return splits > 1 ? (int64_t)splits * 2 * total_kv * hkv * d : 0;
 }

@@ -166,15 +166,17 @@ def test_capi_fused_delta_matches_separate_kernels(D, dtype, causal, window, bia
 
 
 def test_capi_fp32_split_dkv():
-    """fp32 on the fp32 matrix-core kernels: when the dK/dV grid (one
-    workgroup per 128 keys and kv head) would leave CUs idle, the backward
+    """fp32 on the fp32 matrix-core kernels: when the dQ or dK/dV grid (one
+    workgroup per 128 rows and head) would leave CUs idle, the backward
     workspace query adds room for fp32 partials and mtlattn_varlen_bwd splits
-    each workgroup's (query head, query tile) iterations, summing the splits
-    in a fixed order. Checked: the split path is taken (workspace larger than
+    each workgroup's key tiles (dQ) or (query head, query tile) iterations
+    (dK/dV), summing the splits in a fixed order; its dQ kernel computes
+    delta itself. Checked: the split path is taken (workspace larger than
     delta), its gradients against the fp64 oracle, bitwise equal on a second
     call, a NaN-filled workspace does not leak into owned rows, rows outside
-    every sequence are zero, and a delta-sized workspace (unsplit) gives
-    bitwise the separate mtlattn_bwd_dkv entry's dK / dV."""
+    every sequence are zero, the in-kernel delta against the preprocess's,
+    and a delta-sized workspace (unsplit) gives bitwise the separate
+    mtlattn_bwd_dq / mtlattn_bwd_dkv entries' results on that delta."""
     print("\n[case] capi fp32 split dK/dV: ragged GQA causal window, empty sequence, trailing rows", flush=True)
     q_lens, kv_lens, Hq, Hkv, D = [300, 0, 131, 1, 700], [300, 5, 200, 33, 700], 16, 2, 128
     dtype = torch.float32
@@ -202,16 +204,24 @@ def test_capi_fp32_split_dkv():
                   dv.data_ptr(), ws.data_ptr(), n, s)
         torch.cuda.synchronize()
         runs.append([t.cpu() for t in (dq, dk, dv)])
+    nq, nk = int(cq[-1]), int(ck[-1])
+    wdelta = ws[:qd.shape[0] * Hq].clone()          # delta the last (unsplit) call left in its workspace
     delta = torch.empty((qd.shape[0], Hq), dtype=torch.float32, device="cuda")
     capi.call("mtlattn_bwd_preprocess", p, out.data_ptr(), Hq * D, dod.data_ptr(), Hq * D, delta.data_ptr(), s)
-    dk2, dv2 = torch.empty_like(kd), torch.empty_like(vd)
+    dq2, dk2, dv2 = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    capi.call("mtlattn_bwd_dq", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
+              dod.data_ptr(), Hq * D, lse.data_ptr(), wdelta.data_ptr(), dq2.data_ptr(), capi.DTYPE_F32, s)
     capi.call("mtlattn_bwd_dkv", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
-              dod.data_ptr(), Hq * D, lse.data_ptr(), delta.data_ptr(), dk2.data_ptr(), dv2.data_ptr(),
+              dod.data_ptr(), Hq * D, lse.data_ptr(), wdelta.data_ptr(), dk2.data_ptr(), dv2.data_ptr(),
               capi.DTYPE_F32, s)
     torch.cuda.synchronize()
-    nq, nk = int(cq[-1]), int(ck[-1])
+    dl_w, dl_p = wdelta.view(-1, Hq)[:nq].cpu(), delta[:nq].cpu()
+    derr = ((dl_w - dl_p).abs().max() / dl_p.pow(2).mean().sqrt()).item()
+    print(f"  in-kernel delta vs preprocess: max|diff| / RMS = {derr:.3e}", flush=True)
+    assert derr < 1e-5
     for a, b in zip(runs[0], runs[1]):
-        assert torch.equal(a, b), "split dK/dV not bitwise repeatable"
+        assert torch.equal(a, b), "split dQ / dK/dV not bitwise repeatable"
+    assert torch.equal(runs[2][0][:nq], dq2[:nq].cpu())
     assert torch.equal(runs[2][1][:nk], dk2[:nk].cpu()) and torch.equal(runs[2][2][:nk], dv2[:nk].cpu())
     for r in runs:
         assert not r[0][nq:].any() and not r[1][nk:].any() and not r[2][nk:].any()
