@@ -108,8 +108,9 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_fwd_kernel(GenParams p) {
         const float pj = x == kNegInf ? 0.f : __expf(x - mu);
         l = l * corr + wave_sum(pj);
         m = mn;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] *= corr;
+        // the chunk's P.V from zero, folded in with the rescale (one rounding
+        // of the running sum per 64 keys instead of one per key)
+        float part[4] = {0.f, 0.f, 0.f, 0.f};
         const int n = min(64, hi - kt);
         for (int jj = 0; jj < n; ++jj) {
             const float pw = __shfl(pj, jj);
@@ -118,9 +119,11 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_fwd_kernel(GenParams p) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const int dd = lane + 64 * c;
-                if (dd < p.d) acc[c] = fmaf(pw, ldf<T>(p.v, vo + dd), acc[c]);
+                if (dd < p.d) part[c] = fmaf(pw, ldf<T>(p.v, vo + dd), part[c]);
             }
         }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] = fmaf(acc[c], corr, part[c]);
     }
     const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
@@ -176,6 +179,7 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_dq_kernel(GenParams p) {
                 dsj = pj * (dp - dlt);
             }
             const int n = min(64, hi - kt);
+            float part[4] = {0.f, 0.f, 0.f, 0.f};   // this chunk's dS.K, added once per 64 keys
             for (int jj = 0; jj < n; ++jj) {
                 const float sw = __shfl(dsj, jj);
                 if (sw == 0.f) continue;
@@ -183,9 +187,11 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_dq_kernel(GenParams p) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const int dd = lane + 64 * c;
-                    if (dd < p.d) acc[c] = fmaf(sw, ldf<T>(p.k, ko + dd), acc[c]);
+                    if (dd < p.d) part[c] = fmaf(sw, ldf<T>(p.k, ko + dd), part[c]);
                 }
             }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] += part[c];
         }
     }
 #pragma unroll
@@ -243,6 +249,8 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_dkv_kernel(GenParams p) {
                 }
             }
             const int n = min(64, hi - qt);
+            // this chunk's P^T.dO and dS^T.Q, added once per 64 queries
+            float pk[4] = {0.f, 0.f, 0.f, 0.f}, pv[4] = {0.f, 0.f, 0.f, 0.f};
             for (int ii = 0; ii < n; ++ii) {
                 const float pw = __shfl(pi, ii), sw = __shfl(dsi, ii);
                 if (pw == 0.f && sw == 0.f) continue;
@@ -253,10 +261,15 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_dkv_kernel(GenParams p) {
                 for (int c = 0; c < 4; ++c) {
                     const int dd = lane + 64 * c;
                     if (dd < p.d) {
-                        dva[c] = fmaf(pw, ldf<T>(p.dout, oo + dd), dva[c]);
-                        dka[c] = fmaf(sw, ldf<T>(p.q, qo + dd), dka[c]);
+                        pv[c] = fmaf(pw, ldf<T>(p.dout, oo + dd), pv[c]);
+                        pk[c] = fmaf(sw, ldf<T>(p.q, qo + dd), pk[c]);
                     }
                 }
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                dva[c] += pv[c];
+                dka[c] += pk[c];
             }
         }
     }

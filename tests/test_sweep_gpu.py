@@ -1,0 +1,121 @@
+"""GPU parity sweep: a fixed, seeded list of mixed cases crossing what the
+targeted tests cover one feature at a time. It varies dtype (bf16, fp16,
+fp32), head dim (every matrix-core size, the fp32 matrix-core sizes, and
+sizes only the portable kernels take), GQA ratio, ragged and cross lengths
+(kv shorter and longer than q, one-token sequences), causal, window, bias
+(none, head-broadcast, per-head, 4-D per-sequence) and scale. Each case runs
+forward + backward through mtlattn.varlen_attention and is checked against
+the fp64 oracle. Every case prints its parameters first.
+
+Criteria:
+  * fp32: tests/helpers.py's, max|err| / RMS(ref) <= 1e-5 + 2 * floor32, with
+    floor32 the fp32 oracle's own deviation from fp64 on the same case;
+  * fp16 / bf16: RMS(err) / RMS(ref) <= RMS_BOUND (tests/helpers.py), and
+    max|err| <= 4 u max|ref| + 2e-2 RMS(ref) with u the unit roundoff
+    (2^-9 bf16, 2^-11 fp16). The 16-bit kernels round P (and dS) to the
+    input type before the second products (u), write the output in it (u),
+    and take the LSE from the sum of the rounded P, which can be off by 2u
+    when a few keys dominate a row; this sweep's random shapes include such
+    rows (one query against hundreds of keys), where the largest element
+    carries all three, so the bound is stated in u at the largest element
+    rather than in the rounding floor of tests/helpers.py;
+  * a tensor whose exact value is zero everywhere (every sequence one token
+    long: dQ = 0) is held to max|err| <= 1e-5 (fp32) or 1e-4 (16-bit)."""
+
+import math
+import random
+
+import pytest
+import torch
+
+import oracle
+from tests.helpers import RMS_BOUND, TOL_RMS, cu_of, err_stats, randn
+
+UNIT_ROUNDOFF = {torch.bfloat16: 2.0 ** -9, torch.float16: 2.0 ** -11}
+
+pytestmark = pytest.mark.gpu
+
+D16 = [64, 80, 88, 96, 128, 160, 256, 48]      # 48: portable kernels
+D32 = [16, 32, 64, 100, 128, 36, 66, 160]     # 66, 160: portable kernels
+
+
+def _cases(n=40, seed=1234):
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        dt = [torch.bfloat16, torch.float16, torch.float32][i % 3]
+        d = rng.choice(D32 if dt == torch.float32 else D16)
+        hkv = rng.choice([1, 2])
+        g = rng.choice([1, 2, 4, 8])
+        b = rng.randint(1, 4)
+        cap = 400 if d >= 160 else 700
+        ql = [rng.choice([1, rng.randint(1, cap)]) for _ in range(b)]
+        cross = rng.random() < 0.4
+        kl = [max(1, rng.randint(1, cap)) if cross else x for x in ql]
+        causal = rng.random() < 0.6
+        window = rng.choice([0, 0, rng.randint(1, 300)])
+        bias = rng.choice([None, "bcast", "head", "4d"])
+        scale = rng.choice([None, None, 0.2])
+        out.append((i, dt, d, g * hkv, hkv, ql, kl, causal, window, bias, scale))
+    return out
+
+
+def _bias(kind, ql, kl, hq, gen):
+    """(bias given to the kernels, the 3-D bias the oracle uses)."""
+    if kind is None:
+        return None, None
+    if kind == "4d":
+        nq = max(ql)
+        b4 = torch.randn((len(ql), 1, nq, max(kl)), generator=gen)
+        b4[..., ::5] -= 20.0
+        rows = [b4[s][:, :L, :].transpose(0, 1) for s, L in enumerate(ql)]
+        return b4, torch.cat(rows).contiguous()
+    b = torch.randn((sum(ql), 1 if kind == "bcast" else hq, max(kl)), generator=gen)
+    b[:, :, ::7] -= 30.0
+    return b, b
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: f"case{c[0]}")
+def test_sweep(case):
+    import mtlattn
+    i, dt, d, hq, hkv, ql, kl, causal, window, bias_kind, scale = case
+    print(f"\n[case] sweep {i}: {dt} D={d} Hq={hq} Hkv={hkv} q={ql} kv={kl} causal={causal} "
+          f"window={window} bias={bias_kind} scale={scale}", flush=True)
+    gen = torch.Generator().manual_seed(100 + i)
+    q = randn((sum(ql), hq, d), dt, gen)
+    k = randn((sum(kl), hkv, d), dt, gen)
+    v = randn((sum(kl), hkv, d), dt, gen)
+    dout = randn((sum(ql), hq, d), dt, gen)
+    bias_in, bias_ref = _bias(bias_kind, ql, kl, hq, gen)
+    cq, ck = cu_of(ql), cu_of(kl)
+    qm, km, vm = (t.cuda().requires_grad_() for t in (q, k, v))
+    out = mtlattn.varlen_attention(qm, km, vm, cq.cuda(), ck.cuda(), max(ql), scale=scale, causal=causal,
+                                   window=window, attn_bias=None if bias_in is None else bias_in.cuda())
+    out.backward(dout.cuda())
+    torch.cuda.synchronize()
+    sc = 1.0 / math.sqrt(d) if scale is None else scale
+    args = (q, k, v, dout, cq, ck, sc, causal, window, bias_ref)
+    r64 = oracle.varlen_forward_backward(*args, dtype=torch.float64)
+    r32 = oracle.varlen_forward_backward(*args, dtype=torch.float32) if dt == torch.float32 else None
+    for nm, a, j in (("out", out, 0), ("dQ", qm.grad, 2), ("dK", km.grad, 3), ("dV", vm.grad, 4)):
+        assert torch.isfinite(a.float()).all(), f"case {i}: non-finite {nm}"
+        ref = r64[j].float()
+        got = a.detach().float().cpu()
+        max_abs = (got - ref).abs().max().item() if ref.numel() else 0.0
+        if ref.numel() == 0 or ref.abs().max().item() == 0.0:
+            print(f"  {nm}: exact zero, max_abs={max_abs:.3e}", flush=True)
+            assert max_abs <= (1e-5 if dt == torch.float32 else 1e-4), f"case {i}: {nm} max_abs {max_abs}"
+            continue
+        if dt == torch.float32:
+            f32 = err_stats(r32[j], r64[j], dt)["rel"]
+            st = err_stats(a, ref, dt, f32)
+            print(f"  {nm}: rel={st['rel']:.3e} rms_rel={st['rms_rel']:.3e} floor32={f32:.3e}", flush=True)
+            assert st["ok_elem"], f"case {i}: {nm} {st}"
+        else:
+            st = err_stats(a, ref, dt)
+            rms = st["rms_ref"]
+            bound = 4 * UNIT_ROUNDOFF[dt] * ref.abs().max().item() + TOL_RMS[dt] * rms
+            print(f"  {nm}: rel={st['rel']:.3e} rms_rel={st['rms_rel']:.3e} floor={st['floor']:.3e} "
+                  f"max_abs={max_abs:.3e} bound={bound:.3e}", flush=True)
+            assert st["rms_rel"] <= RMS_BOUND[dt], f"case {i}: {nm} rms_rel {st['rms_rel']:.3e}"
+            assert max_abs <= bound, f"case {i}: {nm} max_abs {max_abs:.3e} > {bound:.3e}"
