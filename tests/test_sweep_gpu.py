@@ -3,7 +3,9 @@ targeted tests cover one feature at a time. It varies dtype (bf16, fp16,
 fp32), head dim (every matrix-core size, the fp32 matrix-core sizes, and
 sizes only the portable kernels take), GQA ratio, ragged and cross lengths
 (kv shorter and longer than q, one-token sequences), causal, window, bias
-(none, head-broadcast, per-head, 4-D per-sequence) and scale. Each case runs
+(none, head-broadcast, per-head, 4-D per-sequence) and scale; a second set
+has few queries against long KV, which the forward routes to split-KV
+decode. Each case runs
 forward + backward through mtlattn.varlen_attention and is checked against
 the fp64 oracle. Every case prints its parameters first.
 
@@ -60,6 +62,28 @@ def _cases(n=40, seed=1234):
     return out
 
 
+def _decode_cases(n=16, seed=4321):
+    """Few queries against long KV (average >= 2048 keys, q_len <= 16): the
+    forward routes to split-KV decode + combine (with window and bias too),
+    the backward runs the prefill kernels on the combine's LSE."""
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        dt = [torch.bfloat16, torch.float16][i % 2]
+        d = rng.choice([64, 128])
+        hkv = rng.choice([1, 2, 4])
+        g = rng.choice([1, 4, 8])
+        b = rng.randint(1, 5)
+        ql = [rng.randint(1, 16) for _ in range(b)]
+        kl = [rng.randint(2048, 9000) for _ in range(b)]
+        causal = rng.random() < 0.7
+        window = rng.choice([0, rng.randint(64, 5000)])
+        bias = rng.choice([None, "bcast", "head", "4d"])
+        scale = rng.choice([None, 0.2])
+        out.append((100 + i, dt, d, g * hkv, hkv, ql, kl, causal, window, bias, scale))
+    return out
+
+
 def _bias(kind, ql, kl, hq, gen):
     """(bias given to the kernels, the 3-D bias the oracle uses)."""
     if kind is None:
@@ -75,7 +99,7 @@ def _bias(kind, ql, kl, hq, gen):
     return b, b
 
 
-@pytest.mark.parametrize("case", _cases(), ids=lambda c: f"case{c[0]}")
+@pytest.mark.parametrize("case", _cases() + _decode_cases(), ids=lambda c: f"case{c[0]}")
 def test_sweep(case):
     import mtlattn
     i, dt, d, hq, hkv, ql, kl, causal, window, bias_kind, scale = case
