@@ -104,6 +104,10 @@ int mtlattn_gpu_core_count(int device);
  * forward.
  *   out : contiguous [total_q, Hq, D], same dtype as q
  *   lse : NULL or fp32 [total_q, Hq] (rows with no allowed key get -inf)
+ * Workspace: the split-KV partials of calls routed to decode; for fp32
+ * problems on the fp32 matrix-core kernels whose grid would leave CUs idle,
+ * fp32 partials of 2-8 key splits (a smaller workspace runs them unsplit);
+ * otherwise none.
  */
 size_t mtlattn_varlen_fwd_workspace_size(const mtlattn_problem* p);
 int mtlattn_varlen_fwd(const mtlattn_problem* p,
@@ -120,7 +124,8 @@ int mtlattn_varlen_fwd(const mtlattn_problem* p,
  * memory -- code under HIP graph capture, tight serving (decode) loops,
  * harnesses that forbid allocation. Same routing, kernels and results as
  * mtlattn_varlen_fwd (bitwise); the split-KV partials of calls routed to
- * decode live in a static device array of MTLATTN_NOALLOC_SCRATCH_BYTES per
+ * decode, and the fp32 key-split partials (sized to fit it), live in a
+ * static device array of MTLATTN_NOALLOC_SCRATCH_BYTES per
  * GPU, set up on the first call on each GPU (do that call outside capture)
  * and held until the process ends. Calls whose partials would exceed it
  * (mtlattn_varlen_fwd_workspace_size(p) > MTLATTN_NOALLOC_SCRATCH_BYTES)

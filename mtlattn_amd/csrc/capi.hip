@@ -326,9 +326,37 @@ int32_t mtlattn_decode_num_splits(const mtlattn_problem* p) {
     return slots > 0x7fffffff ? 0x7fffffff : (int32_t)slots;
 }
 
+namespace {
+
+// Splits of the fp32 matrix-core forward over its key tiles: when its grid
+// (one workgroup per 128 query rows and head) holds fewer than two
+// workgroups per CU, up to 8 splits, no more than the key tiles, and few
+// enough that the partials fit the no-allocation scratch, so that
+// mtlattn_varlen_fwd_noalloc splits alike and stays bitwise equal.
+int f32_fwd_splits(const mtlattn_problem* p) {
+    if (p->dtype != MTLATTN_DTYPE_F32 || !f32_mfma_head_dim(p->head_dim) || force_generic() || p->total_q <= 0 ||
+        p->total_kv <= 0)
+        return 1;
+    const int64_t tiles = std::max<int64_t>((p->total_q + 127) / 128, p->num_seqs);
+    const int64_t wgs = tiles * p->num_heads_q, want = 2 * (int64_t)device_cus();
+    if (wgs >= want) return 1;
+    int64_t ns = std::min<int64_t>(std::min<int64_t>((want + wgs - 1) / wgs, 8), (p->total_kv + 31) / 32);
+    const int64_t per_split = (int64_t)p->total_q * p->num_heads_q * (p->head_dim + 1) * (int64_t)sizeof(float);
+    ns = std::min<int64_t>(ns, (int64_t)MTLATTN_NOALLOC_SCRATCH_BYTES / std::max<int64_t>(per_split, 1));
+    return ns >= 2 ? (int)ns : 1;
+}
+
+size_t fwd_part_bytes(const mtlattn_problem* p, int splits) {
+    return (size_t)f32_fwd_part_floats(splits, p->total_q, p->num_heads_q, p->head_dim) * sizeof(float);
+}
+
+}  // namespace
+
 size_t mtlattn_varlen_fwd_workspace_size(const mtlattn_problem* p) {
     const DecodePlan plan = decode_plan(p);
-    return plan.routed() ? splitkv_bytes(p, plan.ns, plan.chunk) : 0;
+    if (plan.routed()) return splitkv_bytes(p, plan.ns, plan.chunk);
+    if (check_problem(p) != MTLATTN_OK) return 0;
+    return fwd_part_bytes(p, f32_fwd_splits(p));
 }
 
 int mtlattn_varlen_fwd(const mtlattn_problem* p, const void* q, int64_t q_row_stride, const void* k,
@@ -353,8 +381,17 @@ int mtlattn_varlen_fwd(const mtlattn_problem* p, const void* q, int64_t q_row_st
     if (is16(p->dtype) && mfma_head_dim(p->head_dim) && vec_ok && tile_stride_ok(k_row_stride) &&
         tile_stride_ok(v_row_stride) && !force_generic())
         return launch_status(launch_fwd_mfma(p->dtype, a, st), "flash forward");
-    if (p->dtype == MTLATTN_DTYPE_F32 && f32_mfma_head_dim(p->head_dim) && vec_ok && !force_generic())
+    if (p->dtype == MTLATTN_DTYPE_F32 && f32_mfma_head_dim(p->head_dim) && vec_ok && !force_generic()) {
+        // split partials in the workspace when it holds them (the size query
+        // counts them); a smaller workspace runs unsplit
+        const int splits = f32_fwd_splits(p);
+        if (splits > 1 && workspace != nullptr && ((uintptr_t)workspace & 15u) == 0 &&
+            workspace_bytes >= fwd_part_bytes(p, splits)) {
+            a.f32_part = (float*)workspace;
+            a.f32_splits = splits;
+        }
         return launch_status(launch_fwd_f32mfma(a, st), "fp32 flash forward");
+    }
     return launch_status(launch_fwd_generic(p->dtype, a, st), "generic forward");
 }
 

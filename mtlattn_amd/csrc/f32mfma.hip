@@ -54,10 +54,13 @@ struct F32Params {
     int num_seqs, hq, hkv, g, d;
     float scale;
     int causal, window;
-    // dQ split over its key tiles, dK/dV over its (query head, query tile)
-    // iterations: split z of nsplit writes unscaled fp32 partials to
-    // part + z * total_q * hq * d (dQ) or part + z * 2 * total_kv * hkv * d
-    // (dK, then dV); part == nullptr: one split writing dq / dk / dv
+    // The forward and dQ split over their key tiles, dK/dV over its (query
+    // head, query tile) iterations. Split z of nsplit writes fp32 partials:
+    // forward, normalised O to part + z * total_q * hq * d and its LSE to
+    // part + nsplit * total_q * hq * d + z * total_q * hq; dQ, unscaled, to
+    // part + z * total_q * hq * d; dK/dV, unscaled, to
+    // part + z * 2 * total_kv * hkv * d (dK, then dV). part == nullptr: one
+    // split writing o / dq / dk / dv
     float* part;
     int nsplit;
     // dQ only: o != nullptr computes delta = rowsum(dO * O) in the kernel
@@ -204,7 +207,9 @@ __device__ inline Tiling tiling(const int* cu, const int* cu_other, int num_seqs
 }
 
 // ---------------------------------------------------------------------------
-// Forward.
+// Forward. Grids with fewer workgroups than the GPU holds split each
+// workgroup's key tiles over blockIdx.z; f32_fwd_combine_kernel merges the
+// splits' normalised O and LSE.
 // ---------------------------------------------------------------------------
 template <int DP>
 __global__ __launch_bounds__(256, DP <= 96 ? 2 : 1) void f32_fwd_kernel(F32Params p) {
@@ -222,6 +227,8 @@ __global__ __launch_bounds__(256, DP <= 96 ? 2 : 1) void f32_fwd_kernel(F32Param
     const Band bz = key_band(qlast, coff, kv_len, p.causal, p.window);
     const int klo = ba.lo & ~31, khi = bz.lo + (int)bz.width;
     const int ntiles = khi > klo ? (khi - klo + 31) / 32 : 0;
+    const int z = (int)blockIdx.z;
+    const int it0 = (int)((int64_t)ntiles * z / p.nsplit), it1 = (int)((int64_t)ntiles * (z + 1) / p.nsplit);
 
     const int wq0 = q0 + 32 * w;
     const bool wave_on = wq0 < q_len;
@@ -251,21 +258,22 @@ __global__ __launch_bounds__(256, DP <= 96 ? 2 : 1) void f32_fwd_kernel(F32Param
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = f32x16_t{};
 
-    if (ntiles > 0) {
-        tk.load(kbase + (int64_t)klo * p.k_rs, p.k_rs, kv_len - klo, p.d, t);
-        tv.load(vbase + (int64_t)klo * p.v_rs, p.v_rs, kv_len - klo, p.d, t);
+    if (it1 > it0) {
+        const int k0 = klo + 32 * it0;
+        tk.load(kbase + (int64_t)k0 * p.k_rs, p.k_rs, kv_len - k0, p.d, t);
+        tv.load(vbase + (int64_t)k0 * p.v_rs, p.v_rs, kv_len - k0, p.d, t);
         tk.template store<true, false>(lds, nullptr, t);
         tv.template store<false, true>(nullptr, lds + KSZ, t);
     }
     __syncthreads();
-    for (int it = 0; it < ntiles; ++it) {
+    for (int it = it0; it < it1; ++it) {
         const int kt = klo + 32 * it;
-        const bool more = it + 1 < ntiles;
+        const bool more = it + 1 < it1;
         if (more) {
             tk.load(kbase + (int64_t)(kt + 32) * p.k_rs, p.k_rs, kv_len - kt - 32, p.d, t);
             tv.load(vbase + (int64_t)(kt + 32) * p.v_rs, p.v_rs, kv_len - kt - 32, p.d, t);
         }
-        const float* ks = lds + (it & 1) * SLOT;
+        const float* ks = lds + ((it - it0) & 1) * SLOT;
         if (wave_on && kt < whi && kt + 32 > wlo) {
             const f32x16_t sacc = head_product<DP>(ks + l32 * SR + h * HD, qreg);
             float x[16];
@@ -299,7 +307,7 @@ __global__ __launch_bounds__(256, DP <= 96 ? 2 : 1) void f32_fwd_kernel(F32Param
             });
         }
         if (more) {
-            float* nx = lds + ((it + 1) & 1) * SLOT;
+            float* nx = lds + ((it + 1 - it0) & 1) * SLOT;
             tk.template store<true, false>(nx, nullptr, t);
             tv.template store<false, true>(nullptr, nx + KSZ, t);
         }
@@ -307,9 +315,55 @@ __global__ __launch_bounds__(256, DP <= 96 ? 2 : 1) void f32_fwd_kernel(F32Param
     }
     if (wave_on && qvalid) {
         const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-        store_row<DP>(p.o + (grow * p.hq + head) * p.d, acc, h, p.d, inv);
-        if (h == 0 && p.lse != nullptr) p.lse[grow * p.hq + head] = lsum > 0.f ? m + logf(lsum) : kNegInf;
+        const float l_out = lsum > 0.f ? m + logf(lsum) : kNegInf;
+        const int64_t rh = grow * p.hq + head;
+        if (p.part == nullptr) {
+            store_row<DP>(p.o + rh * p.d, acc, h, p.d, inv);
+            if (h == 0 && p.lse != nullptr) p.lse[rh] = l_out;
+        } else {
+            const int64_t plane = p.total_q * p.hq;
+            store_row<DP>(p.part + (z * plane + rh) * p.d, acc, h, p.d, inv);
+            if (h == 0) p.part[(int64_t)p.nsplit * plane * p.d + z * plane + rh] = l_out;
+        }
     }
+}
+
+// o and lse of the rows in [cu_q[0], cu_q[num_seqs]) from the forward's
+// nsplit partials (normalised O_z, LSE_z): O = sum_z w_z O_z / sum_z w_z with
+// w_z = exp(LSE_z - max_z LSE_z), LSE = max + log(sum_z w_z); a row whose
+// splits are all empty gets O = 0, LSE = -inf. One thread per 4 columns.
+__global__ __launch_bounds__(256) void f32_fwd_combine_kernel(const float* __restrict__ part, int nsplit,
+                                                              const int* __restrict__ cu_q, int num_seqs,
+                                                              int64_t total_q, int hq, int d, float* __restrict__ o,
+                                                              float* __restrict__ lse) {
+    const int dq4 = d / 4;
+    const int64_t plane = total_q * hq;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= plane * dq4) return;
+    const int64_t rh = i / dq4;
+    const int c4 = (int)(i - rh * dq4);
+    const int64_t row = rh / hq;
+    int64_t r0 = cu_q[0], r1 = cu_q[num_seqs];
+    r0 = r0 < 0 ? 0 : (r0 > total_q ? total_q : r0);
+    r1 = r1 < r0 ? r0 : (r1 > total_q ? total_q : r1);
+    if (row < r0 || row >= r1) return;
+    const float* lp = part + (int64_t)nsplit * plane * d;
+    float mx = kNegInf;
+    for (int z = 0; z < nsplit; ++z) mx = fmaxf(mx, lp[z * plane + rh]);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    float sum = 0.f;
+    if (mx != kNegInf) {
+        for (int z = 0; z < nsplit; ++z) {
+            const float lz = lp[z * plane + rh];
+            if (lz == kNegInf) continue;
+            const float wz = __expf(lz - mx);
+            sum += wz;
+            acc += wz * ld4(part + (z * plane + rh) * d + 4 * c4);
+        }
+    }
+    const float inv = sum > 0.f ? 1.f / sum : 0.f;
+    *reinterpret_cast<f32x4_t*>(o + rh * d + 4 * c4) = acc * inv;
+    if (c4 == 0 && lse != nullptr) lse[rh] = sum > 0.f ? mx + logf(sum) : kNegInf;
 }
 
 // ---------------------------------------------------------------------------
@@ -614,8 +668,16 @@ hipError_t launch_fwd_f32mfma(const FwdArgs& a, hipStream_t st) {
     p.q = (const float*)a.q; p.k = (const float*)a.k; p.v = (const float*)a.v;
     p.q_rs = a.q_rs; p.k_rs = a.k_rs; p.v_rs = a.v_rs;
     p.o = (float*)a.o; p.lse = a.lse;
-    return launch(p, a.geo.total_q, a.geo.hq, st, f32_fwd_kernel<32>, f32_fwd_kernel<64>, f32_fwd_kernel<96>,
-                  f32_fwd_kernel<128>);
+    const int splits = a.f32_part != nullptr && a.f32_splits > 1 ? a.f32_splits : 1;
+    p.part = splits > 1 ? a.f32_part : nullptr;
+    p.nsplit = splits;
+    hipError_t e = launch(p, a.geo.total_q, a.geo.hq, st, f32_fwd_kernel<32>, f32_fwd_kernel<64>,
+                          f32_fwd_kernel<96>, f32_fwd_kernel<128>, splits);
+    if (e != hipSuccess || splits == 1 || a.geo.total_q <= 0) return e;
+    const int64_t n = a.geo.total_q * a.geo.hq * (a.geo.d / 4);
+    hipLaunchKernelGGL(f32_fwd_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p.part, splits,
+                       a.geo.cu_q, a.geo.num_seqs, a.geo.total_q, a.geo.hq, a.geo.d, p.o, p.lse);
+    return hipGetLastError();
 }
 
 hipError_t launch_bwd_dq_f32mfma(const BwdArgs& a, hipStream_t st) {

@@ -29,6 +29,11 @@ struct FwdArgs {
     const void* v; int64_t v_rs;
     void* o;                      // contiguous [total_q, hq, d]
     float* lse;                   // nullable [total_q, hq]
+    // fp32 matrix-core forward only: f32_splits > 1 splits each workgroup's
+    // key tiles over that many workgroups, with normalised fp32 partials and
+    // their LSEs in f32_part (f32_fwd_part_floats floats), then merged
+    float* f32_part = nullptr;
+    int f32_splits = 1;
 };
 
 struct BwdArgs {
@@ -124,6 +129,9 @@ inline bool mfma_head_dim(int d) {
 inline bool f32_mfma_head_dim(int d) { return d > 0 && d <= 128 && d % 4 == 0; }
 // grid x of the fp32 matrix-core kernels: 128-row tiles over every sequence
 inline int64_t f32_row_tiles(int64_t total_rows, int num_seqs) { return total_rows / 128 + num_seqs + 1; }
+inline int64_t f32_fwd_part_floats(int splits, int64_t total_q, int hq, int d) {
+    return splits > 1 ? (int64_t)splits * total_q * hq * (d + 1) : 0;
+}
 inline int64_t f32_dq_part_floats(int splits, int64_t total_q, int hq, int d) {
     return splits > 1 ? (int64_t)splits * total_q * hq * d : 0;
 }

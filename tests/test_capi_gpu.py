@@ -50,9 +50,12 @@ def test_capi_forward_backward(dtype):
     p = capi.problem_for(qd, kd, cqd, ckd, max(q_lens), scale, causal=True)
     out = torch.empty_like(qd)
     lse = torch.empty(qd.shape[0], Hq, dtype=torch.float32, device="cuda")
-    assert capi.lib().mtlattn_varlen_fwd_workspace_size(p) == 0
+    # prefill: no workspace, except fp32 on a small grid (key-split partials)
+    fws_n = capi.lib().mtlattn_varlen_fwd_workspace_size(p)
+    assert fws_n == 0 or dtype == torch.float32
+    fws = torch.empty(max(fws_n, 1), dtype=torch.uint8, device="cuda")
     capi.call("mtlattn_varlen_fwd", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
-              out.data_ptr(), lse.data_ptr(), None, 0, _stream())
+              out.data_ptr(), lse.data_ptr(), fws.data_ptr(), fws_n, _stream())
     ws_n = capi.lib().mtlattn_varlen_bwd_workspace_size(p)
     ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
     dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
@@ -192,6 +195,24 @@ def test_capi_fp32_split_dkv():
     s = _stream()
     capi.call("mtlattn_varlen_fwd", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
               out.data_ptr(), lse.data_ptr(), None, 0, s)
+    # the forward with its workspace splits its key tiles (merged by LSE):
+    # equal to the unsplit forward above up to fp32 rounding
+    fws_n = capi.lib().mtlattn_varlen_fwd_workspace_size(p)
+    assert fws_n > 0, "expected the split forward workspace for this small grid"
+    fws = torch.full((fws_n // 4,), float("nan"), dtype=torch.float32, device="cuda")
+    out_s = torch.full_like(qd, float("nan"))
+    lse_s = torch.full_like(lse, float("nan"))
+    capi.call("mtlattn_varlen_fwd", p, qd.data_ptr(), Hq * D, kd.data_ptr(), Hkv * D, vd.data_ptr(), Hkv * D,
+              out_s.data_ptr(), lse_s.data_ptr(), fws.data_ptr(), fws_n, s)
+    torch.cuda.synchronize()
+    nq0 = int(cq[-1])
+    rms_o = out[:nq0].pow(2).mean().sqrt().item()
+    oerr = (out_s[:nq0] - out[:nq0]).abs().max().item() / rms_o
+    fin = torch.isfinite(lse[:nq0])
+    assert torch.equal(fin, torch.isfinite(lse_s[:nq0]))
+    lerr = (lse_s[:nq0][fin] - lse[:nq0][fin]).abs().max().item()
+    print(f"  split vs unsplit forward: out max|diff| / RMS = {oerr:.3e}, lse max|diff| = {lerr:.3e}", flush=True)
+    assert oerr < 1e-5 and lerr < 2e-5
     ws_n = capi.lib().mtlattn_varlen_bwd_workspace_size(p)
     delta_n = qd.shape[0] * Hq * 4
     assert ws_n > delta_n, "expected the split dK/dV workspace for this small grid"

@@ -2,9 +2,9 @@
 that cannot allocate): through the C ABI, its outputs must equal
 mtlattn_varlen_fwd's with a caller workspace, bitwise (same routing, same
 kernels), on two calls in a row -- the second smaller, reusing the static
-scratch the first one filled -- plus a prefill call (no scratch needed) and
-a call whose partials would exceed the static scratch (refused before any
-launch)."""
+scratch the first one filled -- plus a prefill call (no scratch needed), an
+fp32 small-grid call (key-split partials in the scratch) and a call whose
+partials would exceed the static scratch (refused before any launch)."""
 
 import ctypes
 import math
@@ -76,6 +76,19 @@ def test_noalloc_forward_matches_workspace_entry():
     cu = cu_of(lens, "cuda")
     need, ((o_ws, l_ws), (o_na, l_na)) = _both(q, k, v, cu, cu, max(lens))
     assert need == 0
+    assert torch.equal(o_ws, o_na) and torch.equal(l_ws, l_na)
+    # fp32 on a small grid: the forward splits its key tiles, with the
+    # partials in the caller's workspace or in the static scratch
+    print("[case] noalloc forward: fp32 small grid (key splits in the scratch)", flush=True)
+    lens = [250, 129, 17]
+    q = torch.randn(sum(lens), 4, 64, generator=g).cuda()
+    k = torch.randn(sum(lens), 4, 64, generator=g).cuda()
+    v = torch.randn(sum(lens), 4, 64, generator=g).cuda()
+    cu = cu_of(lens, "cuda")
+    need, ((o_ws, l_ws), (o_na, l_na)) = _both(q, k, v, cu, cu, max(lens), causal=False)
+    print(f"  scratch bytes {need} of {limit}", flush=True)
+    assert 0 < need <= limit
+    assert torch.isfinite(o_ws).all() and torch.isfinite(l_ws).all()
     assert torch.equal(o_ws, o_na) and torch.equal(l_ws, l_na)
 
 
