@@ -142,6 +142,24 @@ template <> __device__ inline float dot2_ones<F16>(uint32_t w, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), one, acc, false);
 }
 
+// exp(a) in fp32 for the fp32 kernels. exp2(a * log2 e) with the product
+// rounded is off by up to |a log2 e| / 2 ulp (8 ulp at a = 10, which softmax
+// arguments reach); here the product's rounding error e (an FMA) and the
+// part of log2 e below fp32 are kept and applied to first order:
+// exp(a) = 2^t (1 + e ln 2), t = fl(a * L). With 2^t correctly rounded
+// this is within 1.9 ulp over [-100, 88] (mean 0.4; the rounded product
+// alone: 64 ulp), to which v_exp_f32 adds its own error. a is clamped at
+// -104 (exp(-104) is below the smallest fp32 denormal) so -inf gives 0
+// without a NaN.
+__device__ inline float exp_fp32(float a) {
+    constexpr float kL = 1.44269502162933349609375f;   // log2(e) rounded to fp32
+    constexpr float kLlo = 1.925963e-08f;              // log2(e) - kL
+    a = fmaxf(a, -104.f);
+    const float t = a * kL;
+    const float e = fmaf(a, kL, -t) + a * kLlo;
+    return __builtin_amdgcn_exp2f(t) * fmaf(e, kLn2, 1.f);
+}
+
 // max / sum of x over lanes l and l ^ 32 via v_permlane32_swap: swapping a
 // register with itself across the halves leaves every lane holding its own
 // value in one result and its partner's in the other.

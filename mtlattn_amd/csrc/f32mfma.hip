@@ -4,7 +4,8 @@
 // products, accumulation and softmax stay fp32 end to end (the reference runs
 // fp32 inputs on its simdgroup kernels in fp32, src/attention.metal:334, 863;
 // the mathematics is src/attention.metal:44-289 forward, 741-784 dQ,
-// 788-835 dK/dV). Other fp32 shapes take the portable kernels.
+// 788-835 dK/dV). Exponentials use exp_fp32 (common.h). Other fp32 shapes
+// take the portable kernels.
 //
 // v_mfma_f32_32x32x2_f32: C[32x32] += A[32x2] * B[2x32]
 //   A: lane l holds A[m = l%32][k = l/32]
@@ -292,11 +293,11 @@ __global__ __launch_bounds__(256, DP <= 96 ? 2 : 1) void f32_fwd_kernel(F32Param
             mt = pair_max(mt);
             const float mn = fmaxf(m, mt);
             const float mu = mn == kNegInf ? 0.f : mn;
-            const float corr = __expf(m - mu);
+            const float corr = exp_fp32(m - mu);
             float ps = 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                x[r] = x[r] == kNegInf ? 0.f : __expf(x[r] - mu);
+                x[r] = x[r] == kNegInf ? 0.f : exp_fp32(x[r] - mu);
                 ps += x[r];
             }
             lsum = lsum * corr + pair_sum(ps);
@@ -356,7 +357,7 @@ __global__ __launch_bounds__(256) void f32_fwd_combine_kernel(const float* __res
         for (int z = 0; z < nsplit; ++z) {
             const float lz = lp[z * plane + rh];
             if (lz == kNegInf) continue;
-            const float wz = __expf(lz - mx);
+            const float wz = exp_fp32(lz - mx);
             sum += wz;
             acc += wz * ld4(part + (z * plane + rh) * d + 4 * c4);
         }
@@ -460,7 +461,7 @@ __global__ __launch_bounds__(256, 1) void f32_dq_kernel(F32Params p) {
                 if (qb.has(kj)) {
                     float xv = sacc[r] * p.scale;
                     if (brow != nullptr && kj < p.bias_cols) xv += brow[kj];
-                    v = __expf(xv - lse) * (pacc[r] - dlt);
+                    v = exp_fp32(xv - lse) * (pacc[r] - dlt);
                 }
                 ds[r] = v;
             }
@@ -579,7 +580,7 @@ __global__ __launch_bounds__(256, 1) void f32_dkv_kernel(F32Params p) {
                                                          p.bias_rows) +
                                          (int64_t)head * p.bias_hs + kj];
                         }
-                        pv = __expf(xv - l4[e]);
+                        pv = exp_fp32(xv - l4[e]);
                     }
                     pr[r] = pv;
                 }

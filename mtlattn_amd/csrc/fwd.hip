@@ -206,13 +206,15 @@ __global__ __launch_bounds__(NW * 64, kWaves / NW) void fwd_mfma_kernel(FwdKPara
     // cmul > 0 (scale > 0, host-checked)
     constexpr bool raw_max = SM != 2;
     const float cmul = SM == 1 ? kLog2e : c2;
-    // Rescale O only when the running max grows by more than 2^32: the
-    // unnormalised weights then stay <= 2^32 (bf16/fp16 P keeps its relative
-    // precision at any scale; the fp32 row sum stays below 2^63 and O below
-    // 2^79 for 2^31 keys of fp16-range V), exact after the final division by
-    // the row sum. A bias that grows along the keys (ALiBi-like) raises the
-    // max every tile; a wide slack turns those into rare rescales.
-    constexpr float kRescale = 32.f;
+    // Rescale O only when the running max grows by more than kRescale (log2
+    // units): the unnormalised weights then stay <= 2^kRescale, exact after
+    // the final division by the row sum. bf16 P keeps its relative precision
+    // up to 2^127, so the slack is 32 (the fp32 row sum stays below 2^63 and O
+    // below 2^79 for 2^31 keys of fp16-range V); fp16 P must stay below its
+    // largest finite value, 65504 < 2^16, so the slack is 15. A bias that grows
+    // along the keys (ALiBi-like) raises the max every tile; a wide slack
+    // turns those into rare rescales.
+    constexpr float kRescale = std::is_same<T, F16>::value ? 15.f : 32.f;
     // For DK <= 64 the softmax VALU work is a larger share of a tile than the
     // MFMAs, so the tile max is skipped: weights are taken against the running
     // max and the max is recomputed only when a row's tile sum reaches

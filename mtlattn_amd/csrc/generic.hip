@@ -11,6 +11,8 @@
 //   dK / dV  : one wave per (key row, kv head), looping over the g query heads
 //              of the group and the query rows that can see the key
 //              (src/attention.metal:788-835), plus window bounds.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 #include "../../include/mtlattn_capi.h"
@@ -47,6 +49,14 @@ __device__ inline int seq_of_row(const int* __restrict__ cu, int num_seqs, int64
     }
     const SeqRange r = seq_range(cu, lo, total);
     return (row >= r.start && row < r.end) ? lo : -1;
+}
+
+// exp for the softmax: exp_fp32 for fp32 inputs (the accuracy of the fp32
+// path), the hardware exponential for 16-bit ones
+template <typename T>
+__device__ inline float sexp(float a) {
+    if constexpr (std::is_same<T, F32>::value) return exp_fp32(a);
+    else return __expf(a);
 }
 
 template <typename T>
@@ -104,8 +114,8 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_fwd_kernel(GenParams p) {
         const float mt = wave_max(x);
         const float mn = fmaxf(m, mt);
         const float mu = mn == kNegInf ? 0.f : mn;
-        const float corr = __expf(m - mu);
-        const float pj = x == kNegInf ? 0.f : __expf(x - mu);
+        const float corr = sexp<T>(m - mu);
+        const float pj = x == kNegInf ? 0.f : sexp<T>(x - mu);
         l = l * corr + wave_sum(pj);
         m = mn;
         // the chunk's P.V from zero, folded in with the rescale (one rounding
@@ -174,7 +184,7 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_dq_kernel(GenParams p) {
                 const int64_t vo = (int64_t)(kr.start + j) * p.v_rs + (int64_t)hk * p.d;
                 float x = dot_row<T>(qs[w], p.k, ko, p.d) * p.scale;
                 if (brow != nullptr && j < p.bias_cols) x += brow[j];
-                const float pj = __expf(x - lse);
+                const float pj = sexp<T>(x - lse);
                 const float dp = dot_row<T>(ds_[w], p.v, vo, p.d);
                 dsj = pj * (dp - dlt);
             }
@@ -243,7 +253,7 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_dkv_kernel(GenParams p) {
                     if (p.bias != nullptr && j < p.bias_cols)
                         x += p.bias[bias_row_offset(row, s, qr.start, p.bias_qs, p.bias_ss, p.bias_rows) +
                                     (int64_t)head * p.bias_hs + j];
-                    pi = __expf(x - lse);
+                    pi = sexp<T>(x - lse);
                     const float dp = dot_row<T>(vs_[w], p.dout, row * p.do_rs + (int64_t)head * p.d, p.d);
                     dsi = pi * (dp - p.delta[row * p.hq + head]);
                 }

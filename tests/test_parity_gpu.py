@@ -251,6 +251,26 @@ def test_mfma_d64_rising_scores(mt):
     _fwd(mt, "D=64 bias lifts the tail", [2048], [2048], 8, 8, 64, torch.float16, bias=bias)
 
 
+def test_rising_logits_between_tiles(mt):
+    """The forward rescales O only when a row's max grows by more than a
+    slack (32 log2 units for bf16, 15 for fp16, whose P must stay below 65504).
+    Logits that step up by 15 (natural units, 21.6 in log2) after the first
+    key tile and again later leave the slack without a rescale in bf16 and
+    force one in fp16: forward and backward stay finite and match the oracle
+    at the head dims of the non-deferred softmax (80, 128, 160, 256), with a
+    per-head and a head-broadcast (staged) bias."""
+    for dt in (torch.float16, torch.bfloat16):
+        for D, bc in ((80, False), (128, True), (160, True), (256, False)):
+            L, H = 300, 8
+            bias = torch.full((L, 1 if bc else H, L), -20.0)
+            bias[:, :, 64:] = -5.0
+            bias[:, :, 200:] = 10.0
+            name = f"rising logits {dt} D={D} {'broadcast' if bc else 'per-head'} bias"
+            _fwd(mt, name, [L], [L], H, 2 if bc else H, D, dt, bias=bias)
+            _bwd(mt, "bwd " + name, [L], [L], H, 2 if bc else H, D, dt, 6e-3 if dt == torch.float16 else 4e-2,
+                 bias=bias)
+
+
 def test_generic_head_dims(mt):
     _fwd(mt, "D=96 causal", [2048], [2048], 12, 12, 96, torch.float16, causal=True)
     _fwd(mt, "D=96 bf16", [1500], [1500], 8, 8, 96, torch.bfloat16)

@@ -11,7 +11,11 @@ the fp64 oracle. Every case prints its parameters first.
 
 Criteria:
   * fp32: tests/helpers.py's, max|err| / RMS(ref) <= 1e-5 + 2 * floor32, with
-    floor32 the fp32 oracle's own deviation from fp64 on the same case;
+    floor32 the fp32 oracle's own deviation from fp64 on the same case, plus
+    4 u32 max|ref| (u32 = 2^-24): on heavy-tailed cases (a few keys
+    dominating, so max|ref| is ~100x the RMS) one ulp of the largest element
+    alone exceeds 1e-5 RMS, and the fp32 oracle's own deviation there is
+    whatever its rounding happened to be;
   * fp16 / bf16: RMS(err) / RMS(ref) <= RMS_BOUND (tests/helpers.py), and
     max|err| <= 4 u max|ref| + 2e-2 RMS(ref) with u the unit roundoff
     (2^-9 bf16, 2^-11 fp16). The 16-bit kernels round P (and dS) to the
@@ -20,7 +24,12 @@ Criteria:
     when a few keys dominate a row; this sweep's random shapes include such
     rows (one query against hundreds of keys), where the largest element
     carries all three, so the bound is stated in u at the largest element
-    rather than in the rounding floor of tests/helpers.py;
+    rather than in the rounding floor of tests/helpers.py. For dQ and dK it
+    is 8 u max|ref|: dS = P (dP - delta) with delta = rowsum(dO * O) formed
+    from the stored (rounded) O, as in the reference, so dS carries delta's
+    rounding (u |dO . O|) however small dP - delta is; where the two nearly
+    cancel at a few dominant keys, that error rides on the largest dQ / dK
+    elements in addition to P's, dS's and the output's roundings;
   * a tensor whose exact value is zero everywhere (every sequence one token
     long: dQ = 0) is held to max|err| <= 1e-5 (fp32) or 1e-4 (16-bit)."""
 
@@ -133,12 +142,15 @@ def test_sweep(case):
         if dt == torch.float32:
             f32 = err_stats(r32[j], r64[j], dt)["rel"]
             st = err_stats(a, ref, dt, f32)
-            print(f"  {nm}: rel={st['rel']:.3e} rms_rel={st['rms_rel']:.3e} floor32={f32:.3e}", flush=True)
-            assert st["ok_elem"], f"case {i}: {nm} {st}"
+            bound = (TOL_RMS[dt] + 2 * f32) * st["rms_ref"] + 4 * 2.0 ** -24 * ref.abs().max().item()
+            print(f"  {nm}: rel={st['rel']:.3e} rms_rel={st['rms_rel']:.3e} floor32={f32:.3e} "
+                  f"max_abs={max_abs:.3e} bound={bound:.3e}", flush=True)
+            assert max_abs <= bound, f"case {i}: {nm} max_abs {max_abs:.3e} > {bound:.3e}"
         else:
             st = err_stats(a, ref, dt)
             rms = st["rms_ref"]
-            bound = 4 * UNIT_ROUNDOFF[dt] * ref.abs().max().item() + TOL_RMS[dt] * rms
+            ku = 8 if nm in ("dQ", "dK") else 4
+            bound = ku * UNIT_ROUNDOFF[dt] * ref.abs().max().item() + TOL_RMS[dt] * rms
             print(f"  {nm}: rel={st['rel']:.3e} rms_rel={st['rms_rel']:.3e} floor={st['floor']:.3e} "
                   f"max_abs={max_abs:.3e} bound={bound:.3e}", flush=True)
             assert st["rms_rel"] <= RMS_BOUND[dt], f"case {i}: {nm} rms_rel {st['rms_rel']:.3e}"
