@@ -5,7 +5,8 @@ sizes only the portable kernels take), GQA ratio, ragged and cross lengths
 (kv shorter and longer than q, one-token sequences), causal, window, bias
 (none, head-broadcast, per-head, 4-D per-sequence) and scale; a second set
 has few queries against long KV, which the forward routes to split-KV
-decode. Each case runs
+decode; a third has longer rows, GQA groups up to 16 and explicit scales
+(negative and zero among them). Each case runs
 forward + backward through mtlattn.varlen_attention and is checked against
 the fp64 oracle. Every case prints its parameters first.
 
@@ -93,6 +94,30 @@ def _decode_cases(n=16, seed=4321):
     return out
 
 
+def _wide_cases(n=16, seed=77):
+    """Longer rows (up to 2048 keys), GQA groups up to 16 heads, and
+    explicit scales including negative and zero (the explicitly scaled
+    softmax mode)."""
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        dt = [torch.bfloat16, torch.float16, torch.float32][i % 3]
+        d = rng.choice(D32 if dt == torch.float32 else D16)
+        hkv = rng.choice([1, 2])
+        g = rng.choice([1, 4, 16])
+        b = rng.randint(1, 3)
+        cap = 600 if d >= 160 else 2048
+        ql = [rng.choice([1, rng.randint(1, cap)]) for _ in range(b)]
+        cross = rng.random() < 0.3
+        kl = [max(1, rng.randint(1, cap)) if cross else x for x in ql]
+        causal = rng.random() < 0.6
+        window = rng.choice([0, 0, rng.randint(1, 600)])
+        bias = rng.choice([None, "bcast", "head", "4d"])
+        scale = rng.choice([None, 0.2, -0.1, 0.0, 0.05])
+        out.append((200 + i, dt, d, g * hkv, hkv, ql, kl, causal, window, bias, scale))
+    return out
+
+
 def _bias(kind, ql, kl, hq, gen):
     """(bias given to the kernels, the 3-D bias the oracle uses)."""
     if kind is None:
@@ -108,7 +133,7 @@ def _bias(kind, ql, kl, hq, gen):
     return b, b
 
 
-@pytest.mark.parametrize("case", _cases() + _decode_cases(), ids=lambda c: f"case{c[0]}")
+@pytest.mark.parametrize("case", _cases() + _decode_cases() + _wide_cases(), ids=lambda c: f"case{c[0]}")
 def test_sweep(case):
     import mtlattn
     i, dt, d, hq, hkv, ql, kl, causal, window, bias_kind, scale = case
