@@ -193,17 +193,21 @@ struct Tiling {
 
 // Workgroup blockIdx.x -> (sequence, first row) over 128-row tiles of `cu`
 // (tile numbering of common.h); r0 >= len means the workgroup has no rows.
+// Query tiles run last-first: under a causal mask the last tiles of a
+// sequence see the most keys, and dispatching the heaviest workgroups first
+// keeps them out of the final round (key tiles are heaviest first already).
 __device__ inline Tiling tiling(const int* cu, const int* cu_other, int num_seqs, int64_t total, int64_t total_other,
                                 bool rows_are_queries) {
     Tiling t;
-    t.s = find_seq_for_tile(cu, num_seqs, kWgRows, (int)blockIdx.x, total);
+    const int bx = rows_are_queries ? (int)(gridDim.x - 1 - blockIdx.x) : (int)blockIdx.x;
+    t.s = find_seq_for_tile(cu, num_seqs, kWgRows, bx, total);
     const int tb = tile_base(cu, t.s, kWgRows, total);
     const SeqRange a = seq_range(cu, t.s, total), b = seq_range(cu_other, t.s, total_other);
     t.start = a.start; t.len = a.end - a.start;
     t.other_start = b.start; t.other_len = b.end - b.start;
     t.coff = rows_are_queries ? t.other_len - t.len : t.len - t.other_len;   // kv_len - q_len
     // a block before its sequence's first tile (rows ahead of cu[0]) has no rows
-    t.r0 = (int)blockIdx.x < tb ? t.len : ((int)blockIdx.x - tb) * kWgRows;
+    t.r0 = bx < tb ? t.len : (bx - tb) * kWgRows;
     return t;
 }
 
