@@ -241,9 +241,11 @@ def _basic_ok(query, key, value, dropout_p, min_seqlen):
 def _try_padding_varlen(query, key, value, attn_mask, is_causal, scale):
     """Self-attention key-padding mask -> packed varlen call (reference:
     mtlattn/__init__.py:202-249). Applies when the mask depends only on
-    (batch, key) and keeps a contiguous key prefix per batch; returns the dense
-    [B, H, N, D] result with padded query rows zeroed, or None when the mask is
-    not of that form."""
+    (batch, key) and keeps a contiguous key prefix per batch, and a float mask
+    adds exactly 0 to the keys it keeps; returns the dense [B, H, N, D] result
+    with padded query rows zeroed, or None when the mask is not of that form.
+    (The reference takes any float mask without -inf entries as keep-all and
+    drops its values; here such a mask is left to the additive-bias path.)"""
     B, Hq, Nq, D = query.shape
     Hkv, Nkv = key.shape[1], key.shape[2]
     if Nq != Nkv:
@@ -261,6 +263,10 @@ def _try_padding_varlen(query, key, value, attn_mask, is_causal, scale):
     # the mask's own broadcast shape, not the expanded [B, H, N, N])
     ok = torch.logical_and((keep0 == kv_keep[:, None, None, :]).all(),
                            (kv_keep == (idx[None, :] < lens[:, None])).all())
+    if attn_mask.dtype != torch.bool:
+        # a float mask is a padding mask only if it adds nothing to the keys
+        # it keeps (else its values are an additive bias)
+        ok = torch.logical_and(ok, (attn_mask.masked_fill(~keep0, 0) == 0).all())
     if not bool(ok):
         return None
     # pack, attend, unpack on the device: no lengths on the host, no

@@ -852,6 +852,41 @@ def test_sdpa_mask(mt):
         assert err < 5e-3
 
 
+def test_replace_sdpa_float_masks(mt):
+    """Through replace_sdpa(), a float additive mask on equal query and key
+    lengths is an additive bias, not a key-padding mask: its values must reach
+    the kernels (the reference's padding shortcut takes any float mask without
+    -inf entries as keep-all and drops them). A float mask of 0 / -inf with a
+    kept key prefix per batch still takes the packed padding path (its padded
+    query rows come back zero). Against torch's SDPA in fp32 on the CPU."""
+    import torch.nn.functional as F
+    orig = F.scaled_dot_product_attention
+    mt.replace_sdpa(min_seqlen=1)
+    try:
+        g = torch.Generator().manual_seed(5)
+        B, H, N, D = 2, 4, 300, 64
+        q, k, v = (randn((B, H, N, D), torch.bfloat16, g) for _ in range(3))
+        lens = [300, 171]
+        pad = torch.full((B, 1, 1, N), float("-inf"))
+        for b, L in enumerate(lens):
+            pad[b, 0, 0, :L] = 0.0
+        for name, m in (("float [B,H,N,N]", torch.randn((B, H, N, N), generator=g)),
+                        ("float [1,1,N,N]", torch.randn((1, 1, N, N), generator=g)),
+                        ("float padding 0/-inf", pad)):
+            _banner(f"replace_sdpa {name}")
+            out = F.scaled_dot_product_attention(q.cuda(), k.cuda(), v.cuda(), attn_mask=m.cuda()).cpu().float()
+            ref = orig(q.float(), k.float(), v.float(), attn_mask=m)
+            if name.startswith("float padding"):
+                for b, L in enumerate(lens):
+                    assert not out[b, :, L:].any(), "padded query rows must be zero"
+                    ref[b, :, L:] = 0.0
+            err = (out - ref).abs().max().item()
+            print(f"  max_err={err:.3e}", flush=True)
+            assert err < REF_ATOL[torch.bfloat16], f"{name}: err {err}"
+    finally:
+        mt.restore_sdpa()
+
+
 def test_bias_per_sequence_rows(mt):
     """A 4-D bias [B or 1, H or 1, Nq, max_kv] is indexed by (sequence,
     sequence-local row) in place; rows past Nq read row Nq - 1. It must give
