@@ -135,6 +135,41 @@ def test_workspace_sizes(lib):
     assert lib.mtlattn_attn_splitkv_workspace_size(ctypes.byref(p), 0) == 0
 
 
+def test_fp32_split_workspace_sizes(lib):
+    """fp32 problems on the fp32 matrix-core kernels whose grids (one
+    workgroup per 128 rows and head) would leave CUs idle ask for split
+    partials (256 CUs assumed without a GPU, as on MI355X): the forward for
+    normalised O and LSE per split, the backward after delta (256-byte
+    aligned) for the larger of dQ's and dK/dV's partials. Large grids, 16-bit
+    inputs and head dims the fp32 matrix-core kernels do not take ask for
+    none; the forward's split count is capped so its partials fit the 64 MiB
+    no-allocation scratch."""
+    # C1: 460 rows, 4 + 4 heads, D = 64, 4 sequences: 16 workgroups -> 8 splits
+    p = problem(dtype=F32, num_seqs=4, total_q=460, total_kv=460, num_heads_q=4, num_heads_kv=4, head_dim=64,
+                max_seqlen_q=250)
+    assert lib.mtlattn_varlen_fwd_workspace_size(ctypes.byref(p)) == 8 * 460 * 4 * (64 + 1) * 4
+    delta = 460 * 4 * 4
+    dq_part = 8 * 460 * 4 * 64 * 4
+    dkv_part = 8 * 2 * 460 * 4 * 64 * 4
+    assert lib.mtlattn_varlen_bwd_workspace_size(ctypes.byref(p)) == (delta + 255) // 256 * 256 + max(dq_part, dkv_part)
+    # a grid that fills the GPU: no splits
+    p = problem(dtype=F32, num_seqs=8, total_q=8 * 4096, total_kv=8 * 4096, num_heads_q=32, num_heads_kv=8,
+                head_dim=128, max_seqlen_q=4096)
+    assert lib.mtlattn_varlen_fwd_workspace_size(ctypes.byref(p)) == 0
+    assert lib.mtlattn_varlen_bwd_workspace_size(ctypes.byref(p)) == 8 * 4096 * 32 * 4
+    # the same small shape in bf16, or at an fp32 head dim of the portable kernels: none
+    for kw in ({"dtype": BF16, "head_dim": 64}, {"dtype": F32, "head_dim": 160}, {"dtype": F32, "head_dim": 66}):
+        p = problem(num_seqs=4, total_q=460, total_kv=460, num_heads_q=4, num_heads_kv=4, max_seqlen_q=250, **kw)
+        assert lib.mtlattn_varlen_fwd_workspace_size(ctypes.byref(p)) == 0, kw
+        assert lib.mtlattn_varlen_bwd_workspace_size(ctypes.byref(p)) == 460 * 4 * 4, kw
+    # 511 workgroups would split 2 ways, but 2 x 33.75 MB of forward partials
+    # exceed the 64 MiB scratch: the forward stays unsplit
+    p = problem(dtype=F32, num_seqs=1, total_q=73 * 128, total_kv=73 * 128, num_heads_q=7, num_heads_kv=7,
+                head_dim=128, max_seqlen_q=73 * 128)
+    assert 2 * 73 * 128 * 7 * 129 * 4 > 64 << 20
+    assert lib.mtlattn_varlen_fwd_workspace_size(ctypes.byref(p)) == 0
+
+
 def test_backward_workspace_checked(lib):
     p = problem()
     rc = lib.mtlattn_varlen_bwd(ctypes.byref(p), FAKE, 0, FAKE, 0, FAKE, 0, FAKE, 0, FAKE, 0, FAKE, FAKE, FAKE, FAKE,
