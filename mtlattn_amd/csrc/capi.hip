@@ -402,7 +402,9 @@ int mtlattn_varlen_fwd_noalloc(const mtlattn_problem* p, const void* q, int64_t 
     if (rc != MTLATTN_OK) return rc;
     if (p->total_q == 0) return ok();
     // the workspace mtlattn_varlen_fwd would need: split-KV partials when the
-    // call is routed to decode, nothing for the flash forward
+    // call is routed to decode, the key-split partials of an fp32 forward on a
+    // small grid (f32_fwd_splits caps their count so that they fit the static
+    // scratch), nothing for the 16-bit flash forward
     const size_t need = mtlattn_varlen_fwd_workspace_size(p);
     if (need == 0)
         return mtlattn_varlen_fwd(p, q, q_row_stride, k, k_row_stride, v, v_row_stride, out, lse, nullptr, 0, stream);

@@ -150,11 +150,13 @@ template <> __device__ inline float dot2_ones<F16>(uint32_t w, float acc) {
 // this is within 1.9 ulp over [-100, 88] (mean 0.4; the rounded product
 // alone: 64 ulp), to which v_exp_f32 adds its own error. a is clamped at
 // -104 (exp(-104) is below the smallest fp32 denormal) so -inf gives 0
-// without a NaN.
+// without a NaN. The clamp is a compare, not fmaxf: fmaxf(NaN, -104) is
+// -104, which would turn a NaN logit into a weight of 0; a NaN compares
+// false and passes through.
 __device__ inline float exp_fp32(float a) {
     constexpr float kL = 1.44269502162933349609375f;   // log2(e) rounded to fp32
     constexpr float kLlo = 1.925963e-08f;              // log2(e) - kL
-    a = fmaxf(a, -104.f);
+    a = a < -104.f ? -104.f : a;
     const float t = a * kL;
     const float e = fmaf(a, kL, -t) + a * kLlo;
     return __builtin_amdgcn_exp2f(t) * fmaf(e, kLn2, 1.f);

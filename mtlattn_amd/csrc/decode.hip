@@ -327,7 +327,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
     float lt = l_run + __shfl_xor(l_run, 16);
     lt += __shfl_xor(lt, 32);
     if (row_ok) {
-        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        const float inv = !(lt <= 0.f) ? 1.f / lt : 0.f;
         const int64_t prow = ((int64_t)(hk * p.n_hg + hgi) * p.n_slots + slot) * 16 + n16;
         float* op = p.o_part + prow * D;
 #pragma unroll
@@ -335,7 +335,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void decode_split_kernel(DecKParams
             const int d = 16 * db + 4 * lg;
             *reinterpret_cast<f32x4_t*>(op + d) = oacc[db] * inv;
         }
-        if (lg == 0) p.lse_part[prow] = lt > 0.f ? m_run * kLn2 + logf(lt) : kNegInf;
+        if (lg == 0) p.lse_part[prow] = !(lt <= 0.f) ? m_run * kLn2 + logf(lt) : kNegInf;
     }
 }
 
@@ -411,13 +411,13 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecKParams p, typen
             }
         }
     }
-    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+    const float inv = !(wsum <= 0.f) ? 1.f / wsum : 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int dd = lane + 64 * j;
         if (dd < d) out[rh * d + dd] = T::from_float(acc[j] * inv);
     }
-    if (lse_out != nullptr && lane == 0) lse_out[rh] = wsum > 0.f ? m + logf(wsum) : kNegInf;
+    if (lse_out != nullptr && lane == 0) lse_out[rh] = !(wsum <= 0.f) ? m + logf(wsum) : kNegInf;
 }
 
 template <typename T, int D>

@@ -319,8 +319,8 @@ __global__ __launch_bounds__(256, DP <= 96 ? 2 : 1) void f32_fwd_kernel(F32Param
         __syncthreads();
     }
     if (wave_on && qvalid) {
-        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-        const float l_out = lsum > 0.f ? m + logf(lsum) : kNegInf;
+        const float inv = !(lsum <= 0.f) ? 1.f / lsum : 0.f;
+        const float l_out = !(lsum <= 0.f) ? m + logf(lsum) : kNegInf;
         const int64_t rh = grow * p.hq + head;
         if (p.part == nullptr) {
             store_row<DP>(p.o + rh * p.d, acc, h, p.d, inv);
@@ -366,9 +366,9 @@ __global__ __launch_bounds__(256) void f32_fwd_combine_kernel(const float* __res
             acc += wz * ld4(part + (z * plane + rh) * d + 4 * c4);
         }
     }
-    const float inv = sum > 0.f ? 1.f / sum : 0.f;
+    const float inv = !(sum <= 0.f) ? 1.f / sum : 0.f;
     *reinterpret_cast<f32x4_t*>(o + rh * d + 4 * c4) = acc * inv;
-    if (c4 == 0 && lse != nullptr) lse[rh] = sum > 0.f ? mx + logf(sum) : kNegInf;
+    if (c4 == 0 && lse != nullptr) lse[rh] = !(sum <= 0.f) ? mx + logf(sum) : kNegInf;
 }
 
 // ---------------------------------------------------------------------------

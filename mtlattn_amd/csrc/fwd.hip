@@ -450,7 +450,7 @@ __global__ __launch_bounds__(NW * 64, kWaves / NW) void fwd_mfma_kernel(FwdKPara
     // Epilogue: lanes l and l^32 hold the two halves of one query's row sum.
     const float lt = pair_sum(l_run);
     if (wave_active && qrow < q_len) {
-        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        const float inv = !(lt <= 0.f) ? 1.f / lt : 0.f;
         uint16_t* op = p.o + (int64_t)(qr.start + qrow) * ((int64_t)p.hq * DV) + (int64_t)head * DV + p.col0;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(NW * 64, kWaves / NW) void fwd_mfma_kernel(FwdKPara
             }
         }
         if (p.lse != nullptr && hi == 0)
-            p.lse[(int64_t)(qr.start + qrow) * p.hq + head] = lt > 0.f ? m_run * kLn2 + logf(lt) : kNegInf;
+            p.lse[(int64_t)(qr.start + qrow) * p.hq + head] = !(lt <= 0.f) ? m_run * kLn2 + logf(lt) : kNegInf;
     }
 }
 

@@ -135,13 +135,13 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_fwd_kernel(GenParams p) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[c] = fmaf(acc[c], corr, part[c]);
     }
-    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const float inv = !(l <= 0.f) ? 1.f / l : 0.f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const int dd = lane + 64 * c;
         if (dd < p.d) stf<T>(p.o, (row * p.hq + head) * p.d + dd, acc[c] * inv);
     }
-    if (p.lse != nullptr && lane == 0) p.lse[row * p.hq + head] = l > 0.f ? m + logf(l) : kNegInf;
+    if (p.lse != nullptr && lane == 0) p.lse[row * p.hq + head] = !(l <= 0.f) ? m + logf(l) : kNegInf;
 }
 
 template <typename T>

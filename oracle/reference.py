@@ -94,10 +94,11 @@ def _bias_block(bias, qo, ql, kl, Hq):
 
 def _masked_softmax(a, mask):
     """Softmax over the last dim restricted to `mask`; rows with no allowed key
-    give P = 0 and LSE = -inf (differentiable, NaN-free)."""
+    give P = 0 and LSE = -inf (differentiable). Only those rows are special:
+    a row with a NaN logit keeps the NaN a plain softmax gives it."""
     a = a.masked_fill(~mask, float("-inf"))
     lse = torch.logsumexp(a, dim=-1)
-    valid = torch.isfinite(lse)
+    valid = lse != float("-inf")
     a_safe = torch.where(valid[..., None], a, torch.zeros_like(a))
     p = torch.softmax(a_safe, dim=-1) * valid[..., None].to(a.dtype)
     return p, lse
@@ -240,7 +241,7 @@ def varlen_forward_backward_blocked(q, k, v, dout, cu_q, cu_kv, scale=None, caus
             m = allowed_mask(ql, kl, causal, window, q_rows=(b0, b1), k_cols=(lo, hi))
             a = a.masked_fill(~m, float("-inf"))
             l_b = torch.logsumexp(a, dim=-1)                                    # [nh, g, nq]
-            valid = torch.isfinite(l_b)
+            valid = l_b != float("-inf")      # rows with no allowed key (NaN rows stay NaN)
             p = torch.exp(a - torch.where(valid, l_b, torch.zeros_like(l_b))[..., None])
             p = p * valid[..., None].to(dtype)
             o_b = torch.matmul(p, vb.unsqueeze(1))                              # [nh, g, nq, D]

@@ -75,7 +75,7 @@ def test_c2_ragged_noncausal_bf16():
 
 
 def test_c3_causal_gqa_bf16():
-    print("\n[case] C3 bf16 8x4096 Hq=32 Hkv=8 D=128 causal fwd+bwd (seqs 0,7 x kv heads 0,7 checked)",
+    print("\n[case] C3 bf16 8x4096 Hq=32 Hkv=8 D=128 causal fwd+bwd (seqs 0,3,7 x kv heads 0,3,7 checked)",
           flush=True)
     B, L, Hq, Hkv, D = 8, 4096, 32, 8, 128
     g = torch.Generator().manual_seed(0)
@@ -86,7 +86,7 @@ def test_c3_causal_gqa_bf16():
     do = _gen((M, Hq, D), g, torch.bfloat16)
     cu = cu_of([L] * B)
     o, dq, dk, dv = _run_gpu(q, k, v, do, cu, cu, L, True)
-    seqs, heads = [0, 7], [0, 7]
+    seqs, heads = [0, 3, 7], [0, 3, 7]   # first, a middle and the last sequence and kv head
     ro, _, rq, rk, rv = oracle.varlen_forward_backward_blocked(q, k, v, do, cu, cu, 1 / math.sqrt(D), True,
                                                                seqs=seqs, heads=heads)
     rows = torch.cat([torch.arange(s * L, (s + 1) * L) for s in seqs])

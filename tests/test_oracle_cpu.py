@@ -128,6 +128,27 @@ def test_empty_rows_zero_and_neg_inf():
     assert torch.isfinite(lse[4:]).all()
 
 
+def test_nan_logit_rows_stay_nan():
+    """Only rows with no allowed key are special-cased to O = 0 and
+    LSE = -inf; a NaN logit gives NaN in its row, as a plain softmax does,
+    in the graph form and the blocked form alike (a planted check: treating
+    every non-finite LSE as empty turns these rows into zeros)."""
+    q, k, v = _rand([5, 6], [5, 6], 2, 1, 4)
+    q[7, 1, 0] = float("nan")          # sequence 1, head 1, one query row
+    k[2, 0, 3] = float("nan")          # sequence 0: every row of both heads
+    dout = torch.ones_like(q)
+    cq = cu_of([5, 6])
+    out, lse = oracle.varlen_forward(q, k, v, cq, cq, None, False, 0, dtype=torch.float64)
+    ob, lb = oracle.varlen_forward_backward_blocked(q, k, v, dout, cq, cq, None, False, 0, backward=False,
+                                                    dtype=torch.float64)[:2]
+    expect = torch.zeros(11, 2, dtype=torch.bool)
+    expect[0:5] = True
+    expect[7, 1] = True
+    for o, l in ((out, lse), (ob, lb)):
+        assert torch.equal(l.isnan(), expect)
+        assert torch.equal(o.isnan().all(-1), expect) and torch.equal(o.isnan().any(-1), expect)
+
+
 def test_gqa_equals_expanded_mha():
     lens = [7, 5]
     q, k, v = _rand(lens, lens, 6, 2, 8, seed=2)

@@ -1198,3 +1198,36 @@ def test_mfma_matches_generic(mt, D):
     err = (outs[0] - outs[1]).abs().max().item()
     print(f"  mfma_vs_generic={err:.3e}", flush=True)
     assert err < 5e-3
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float32, 64), (torch.float32, 128), (torch.float32, 66),
+                                     (torch.bfloat16, 64), (torch.bfloat16, 128), (torch.float16, 80)])
+def test_nan_inputs_propagate(mt, dtype, D):
+    """A NaN in q or k gives NaN outputs and LSEs in exactly the rows that
+    see it, as a softmax over a NaN logit does in the oracle; every other
+    row stays finite. (A clamp through fmaxf once turned NaN logits into
+    weights of 0 in the fp32 kernels, so a NaN row looked fully masked:
+    O = 0, LSE = -inf.) fp32 at 64 / 128 runs on the fp32 matrix cores, at 66
+    on the portable kernels; 16-bit on the flash forward."""
+    _banner(f"NaN inputs {dtype} D={D}")
+    lens = [40, 50]
+    Hq, Hkv = 4, 2
+    q, k, v = _inputs(lens, lens, Hq, Hkv, D, dtype, seed=11)
+    q[45, 3, 3] = float("nan")   # sequence 1, query head 3 (kv head 1), one row
+    k[20, 0, 5] = float("nan")   # sequence 0, kv head 0: query heads 0 and 1, every row
+    cu = cu_of(lens, "cuda")
+    lse = torch.empty(sum(lens), Hq, dtype=torch.float32, device="cuda")
+    out = mt._C.varlen_attention(q.cuda(), k.cuda(), v.cuda(), cu, cu, max(lens), 1 / math.sqrt(D), False, 0, lse)
+    torch.cuda.synchronize()
+    expect = torch.zeros(sum(lens), Hq, dtype=torch.bool)
+    expect[0:40, 0:2] = True
+    expect[45, 3] = True
+    ref, ref_lse = oracle.varlen_forward(q, k, v, cu.cpu(), cu.cpu(), 1 / math.sqrt(D), False, 0, None)
+    assert torch.equal(ref_lse.isnan(), expect), "the oracle's NaN pattern"
+    o_nan = out.float().cpu().isnan()
+    l_nan = lse.cpu().isnan()
+    print(f"  out rows NaN: {int(o_nan.all(-1).sum())} (expect {int(expect.sum())}); "
+          f"LSE NaN: {int(l_nan.sum())}", flush=True)
+    assert torch.equal(o_nan.all(-1), expect) and torch.equal(o_nan.any(-1), expect)
+    assert torch.equal(l_nan, expect)
+    assert torch.isfinite(out.float().cpu()[~expect]).all() and torch.isfinite(lse.cpu()[~expect]).all()

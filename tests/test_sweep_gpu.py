@@ -19,7 +19,7 @@ Criteria:
     whatever its rounding happened to be;
   * fp16 / bf16: RMS(err) / RMS(ref) <= RMS_BOUND (tests/helpers.py), and
     max|err| <= 4 u max|ref| + 2e-2 RMS(ref) with u the unit roundoff
-    (2^-9 bf16, 2^-11 fp16). The 16-bit kernels round P (and dS) to the
+    (2^-8 bf16, 2^-11 fp16: 8 and 11 significand bits, as tests/helpers.py). The 16-bit kernels round P (and dS) to the
     input type before the second products (u), write the output in it (u),
     and take the LSE from the sum of the rounded P, which can be off by 2u
     when a few keys dominate a row; this sweep's random shapes include such
@@ -34,9 +34,14 @@ Criteria:
   * the backward takes P = exp(x - LSE) with the forward's fp32 LSE, so
     each bound also allows 4 u32 |LSE|max max|ref| (the LSE's own rounding,
     relative to P; the oracle takes its softmax directly);
-  * a tensor whose exact value is zero, or below 1e-6, everywhere (every
-    sequence one token long, or one key dominating each row: dQ ~ 0) is
-    held to max|err| <= 1e-5 (fp32) or 1e-4 (16-bit)."""
+  * a tensor whose exact value is below 1e-6 everywhere (every sequence one
+    token long, or one key dominating each row: dQ ~ 0) is the difference
+    of terms that cancel, and its error is the fp32 rounding of those terms,
+    not a fraction of its own size. It is held to
+    max|err| <= 1e-2 max|ref| + 64 u32 C, with C the size of the cancelling
+    terms: for dQ, |scale| max|delta| max|K| (dS = P (dP - delta) times K);
+    for dK, |scale| max|delta| max|Q| Lq (up to Lq query rows add to a
+    key); for out and dV, max|V| and max|dO| Lq."""
 
 import math
 import random
@@ -47,7 +52,7 @@ import torch
 import oracle
 from tests.helpers import RMS_BOUND, TOL_RMS, cu_of, err_stats, randn
 
-UNIT_ROUNDOFF = {torch.bfloat16: 2.0 ** -9, torch.float16: 2.0 ** -11}
+UNIT_ROUNDOFF = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}
 
 pytestmark = pytest.mark.gpu
 
@@ -161,14 +166,24 @@ def test_sweep(case):
     r32 = oracle.varlen_forward_backward(*args, dtype=torch.float32) if dt == torch.float32 else None
     lse_ref = r64[1][torch.isfinite(r64[1])]
     lse_term = 4 * 2.0 ** -24 * (lse_ref.abs().max().item() if lse_ref.numel() else 0.0)
+    # size of the terms that cancel in a tensor whose exact value is ~0
+    delta = (dout.double() * r64[0].double()).sum(-1).abs().max().item() if dout.numel() else 0.0
+    amax = lambda t: t.double().abs().max().item() if t.numel() else 0.0
+    lq = max(ql)
+    cancel = {"out": amax(v), "dV": amax(dout) * lq, "dQ": abs(sc) * delta * amax(k),
+              "dK": abs(sc) * delta * amax(q) * lq}
     for nm, a, j in (("out", out, 0), ("dQ", qm.grad, 2), ("dK", km.grad, 3), ("dV", vm.grad, 4)):
         assert torch.isfinite(a.float()).all(), f"case {i}: non-finite {nm}"
         ref = r64[j].float()
         got = a.detach().float().cpu()
         max_abs = (got - ref).abs().max().item() if ref.numel() else 0.0
-        if ref.numel() == 0 or ref.abs().max().item() <= 1e-6:
-            print(f"  {nm}: exact zero, max_abs={max_abs:.3e}", flush=True)
-            assert max_abs <= (1e-5 if dt == torch.float32 else 1e-4), f"case {i}: {nm} max_abs {max_abs}"
+        if ref.numel() == 0:
+            continue
+        if ref.abs().max().item() <= 1e-6:
+            bound = 1e-2 * ref.abs().max().item() + 64 * 2.0 ** -24 * cancel[nm]
+            print(f"  {nm}: near zero, max|ref|={ref.abs().max().item():.3e} max_abs={max_abs:.3e} "
+                  f"bound={bound:.3e}", flush=True)
+            assert max_abs <= bound, f"case {i}: {nm} max_abs {max_abs:.3e} > {bound:.3e}"
             continue
         if dt == torch.float32:
             f32 = err_stats(r32[j], r64[j], dt)["rel"]

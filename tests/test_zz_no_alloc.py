@@ -94,20 +94,26 @@ def test_noalloc_forward_matches_workspace_entry():
 
 def test_noalloc_forward_refuses_oversized_scratch():
     """A decode call whose partials exceed the static scratch is refused
-    with MTLATTN_ERR_WORKSPACE before anything is launched (the problem is
-    sized on the host only; the tensors are small stand-ins that no kernel
-    reads)."""
+    with MTLATTN_ERR_WORKSPACE before anything is launched. The tensors are
+    the full size the problem describes (768 sequences of one query against
+    2048 keys, 8 kv heads: 2 x 3.2 GB of K and V), so that a regression in
+    the host-side refusal would run an in-bounds forward, not read past an
+    allocation."""
     print("\n[case] noalloc forward: oversized split-KV request refused", flush=True)
     L = capi.lib()
-    q = torch.zeros(64, 64, 128, dtype=torch.bfloat16, device="cuda")
-    k = torch.zeros(16, 8, 128, dtype=torch.bfloat16, device="cuda")
-    cq = cu_of([1] * 64, "cuda")
-    p = capi.problem_for(q, k, cq, cq, 1, 0.1, causal=True)
-    p.total_kv = 200_000_000     # routed to decode; partials far above 64 MiB
+    nseq, kv_len, hq, hkv, d = 768, 2048, 64, 8, 128
+    q = torch.zeros(nseq, hq, d, dtype=torch.bfloat16, device="cuda")
+    k = torch.zeros(nseq * kv_len, hkv, d, dtype=torch.bfloat16, device="cuda")
+    v = torch.zeros_like(k)
+    o = torch.empty_like(q)
+    cq = cu_of([1] * nseq, "cuda")
+    ck = cu_of([kv_len] * nseq, "cuda")
+    p = capi.problem_for(q, k, cq, ck, 1, 0.1, causal=True)
     need = L.mtlattn_varlen_fwd_workspace_size(ctypes.byref(p))
+    print(f"  split-KV scratch needed {need} bytes", flush=True)
     assert need > (64 << 20)
     sh = torch.cuda.current_stream().cuda_stream
     rc = L.mtlattn_varlen_fwd_noalloc(ctypes.byref(p), q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0),
-                                      k.data_ptr(), k.stride(0), q.data_ptr(), None, sh)
+                                      v.data_ptr(), v.stride(0), o.data_ptr(), None, sh)
     assert rc == capi.ERR_WORKSPACE
     assert b"static" in L.mtlattn_last_error()
