@@ -162,6 +162,10 @@ __device__ inline float exp_fp32(float a) {
     return __builtin_amdgcn_exp2f(t) * fmaf(e, kLn2, 1.f);
 }
 
+// max(a, b) that returns NaN when either is NaN (fmaxf returns the other
+// operand): used where a NaN must survive a max, e.g. a split's LSE.
+__device__ inline float nan_max(float a, float b) { return (a > b || a != a) ? a : b; }
+
 // max / sum of x over lanes l and l ^ 32 via v_permlane32_swap: swapping a
 // register with itself across the halves leaves every lane holding its own
 // value in one result and its partner's in the other.

@@ -377,9 +377,11 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecKParams p, typen
     const int64_t base = (int64_t)(hk * p.n_hg + hgi) * p.n_slots;
     // max LSE: lanes over items, then across the wave
     float m = kNegInf;
-    for (int i = lane; i < count; i += 64) m = fmaxf(m, p.lse_part[(base + first + i) * 16 + n]);
+    // (NaN-preserving: a NaN logit makes its item's LSE NaN, and a row whose
+    // items are all NaN must not look empty)
+    for (int i = lane; i < count; i += 64) m = nan_max(p.lse_part[(base + first + i) * 16 + n], m);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    for (int off = 32; off > 0; off >>= 1) m = nan_max(m, __shfl_xor(m, off));
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     float wsum = 0.f;
     if (m != kNegInf) {

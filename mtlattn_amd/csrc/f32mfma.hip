@@ -353,8 +353,14 @@ __global__ __launch_bounds__(256) void f32_fwd_combine_kernel(const float* __res
     r1 = r1 < r0 ? r0 : (r1 > total_q ? total_q : r1);
     if (row < r0 || row >= r1) return;
     const float* lp = part + (int64_t)nsplit * plane * d;
+    // max over the splits that keeps a NaN LSE (a NaN logit in the split):
+    // fmaxf would drop it and the row would look empty
     float mx = kNegInf;
-    for (int z = 0; z < nsplit; ++z) mx = fmaxf(mx, lp[z * plane + rh]);
+    for (int z = 0; z < nsplit; ++z) {
+        const float lz = lp[z * plane + rh];
+        mx = nan_max(lz, mx);
+        if (mx != mx) break;
+    }
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
     float sum = 0.f;
     if (mx != kNegInf) {

@@ -1231,3 +1231,28 @@ def test_nan_inputs_propagate(mt, dtype, D):
     assert torch.equal(o_nan.all(-1), expect) and torch.equal(o_nan.any(-1), expect)
     assert torch.equal(l_nan, expect)
     assert torch.isfinite(out.float().cpu()[~expect]).all() and torch.isfinite(lse.cpu()[~expect]).all()
+
+
+@pytest.mark.gpu
+def test_nan_inputs_propagate_split_kv(mt):
+    """The split-KV decode path keeps NaN rows NaN: a NaN in a query row makes
+    every split's LSE of that row NaN, and the combine's max over the splits
+    must not drop them (an fmaxf max would, and the row would come out as an
+    empty one: O = 0). A NaN in one key makes only the split that holds it
+    NaN; the combine's weights carry that into the row."""
+    _banner("NaN inputs, split-KV decode")
+    q_lens, kv_lens = [1, 1, 1], [5000, 2100, 9001]
+    Hq, Hkv = 8, 2
+    q, k, v = _inputs(q_lens, kv_lens, Hq, Hkv, 128, torch.bfloat16, seed=5)
+    q[1, 5, 7] = float("nan")        # sequence 1, query head 5 only
+    k[5000 + 2100 + 300, 0, 9] = float("nan")   # sequence 2, kv head 0: query heads 0-3
+    cq, ck = cu_of(q_lens, "cuda"), cu_of(kv_lens, "cuda")
+    expect = torch.zeros(3, Hq, dtype=torch.bool)
+    expect[1, 5] = True
+    expect[2, 0:4] = True
+    for ns in (1, 4, 16):
+        o = mt._C.attn_splitkv(q.cuda(), k.cuda(), v.cuda(), cq, ck, 1, 1 / math.sqrt(128), True, ns).cpu()
+        nan_rows = o.float().isnan().all(-1)
+        print(f"  ns={ns} NaN rows {int(nan_rows.sum())} (expect {int(expect.sum())})", flush=True)
+        assert torch.equal(nan_rows, expect) and torch.equal(o.float().isnan().any(-1), expect)
+        assert torch.isfinite(o.float()[~expect]).all()
