@@ -378,15 +378,19 @@ def issue_rates():
     names = {0: "idle", 1: "v_exp_f32", 2: "v_fmac_f32", 3: "mfma32x32x16 (VGPR acc)", 4: "mfma32x32x16 (AGPR acc)",
              5: "ds_read_b128", 6: "mfma + 2 v_exp + 2 v_fmac (one wave)", 7: "mfma + 4 v_exp (one wave)",
              8: "mfma (LDS operand) + 2 v_exp + 2 v_fmac (one wave)",
-             9: "mfma + softmax chain: 2 fma->exp, cvt, dot2 (one wave)"}
-    iters = {1: 2000, 2: 4000, 3: 1000, 4: 1000, 5: 1000, 6: 1000, 7: 1000, 8: 1000, 9: 1000}
+             9: "mfma + softmax chain: 2 fma->exp, cvt, dot2 (one wave)",
+             10: "global_load_lds_dwordx4 (1 KB, L2-resident)",
+             11: "mfma + 1 direct load per 4 MFMAs (one wave)",
+             12: "mfma (LDS operand shared by 2 MFMAs) + 2 v_exp + 2 v_fmac (one wave)"}
+    iters = {1: 2000, 2: 4000, 3: 1000, 4: 1000, 5: 1000, 6: 1000, 7: 1000, 8: 1000, 9: 1000, 10: 1000, 11: 1000,
+             12: 1000}
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     sink = torch.empty(cus * 512, dtype=torch.float32, device="cuda")
     cyc = torch.zeros(cus * 16, dtype=torch.int64, device="cuda")
     stream = torch.cuda.current_stream()
     pairs = [(1, 0), (1, 1), (2, 0), (2, 2), (3, 0), (4, 0), (3, 3), (4, 4), (3, 1), (4, 1), (3, 2), (4, 2),
              (5, 0), (5, 5), (3, 5), (6, 0), (7, 0), (6, 6), (7, 7), (6, 3),
-             (8, 0), (8, 8), (9, 0), (9, 9)]
+             (8, 0), (8, 8), (9, 0), (9, 9), (10, 0), (10, 10), (3, 10), (11, 0), (11, 11), (12, 0), (12, 12)]
     out = []
     for ra, rb in pairs:
         n = max(iters.get(ra, 1), iters.get(rb, 1))

@@ -26,7 +26,11 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmtlattn_hip.so")
 EXT = os.path.join(HERE, "_C" + sysconfig.get_config_var("EXT_SUFFIX"))
 CALIB = os.path.join(HERE, "libmtlattn_calib.so")
-HIP_SOURCES = ["fwd.hip", "bwd.hip", "decode.hip", "generic.hip", "f32mfma.hip", "pad.hip", "capi.hip"]
+HIP_SOURCES = ["fwd.hip", "bwd.hip", "bwd_wide.hip", "decode.hip", "generic.hip", "f32mfma.hip", "pad.hip", "capi.hip"]
+# Per-source flags. bwd_wide.hip pins its accumulators to the AGPRs by inline
+# asm and needs the compiler's own MFMA results in VGPRs, where the VALU reads
+# them.
+SOURCE_FLAGS = {"bwd_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = os.environ.get("MTLATTN_ARCH", "gfx950")
@@ -52,7 +56,7 @@ def build_lib(verbose=False, jobs=None):
 
     def compile_one(src):
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-        _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj], verbose)
+        _run([HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj], verbose)
         return obj
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:

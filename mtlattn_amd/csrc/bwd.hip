@@ -30,6 +30,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "bwd_common.h"
 #include "../../include/mtlattn_capi.h"
 
 namespace mtlattn {
@@ -39,52 +40,6 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kKW = 32;   // dK/dV: keys per wave
-
-struct BwdKParams {
-    const uint16_t* q; const uint16_t* k; const uint16_t* v; const uint16_t* dout;
-    const float* lse; const float* delta;
-    void* dq; void* dk; void* dv;
-    const int* cu_q; const int* cu_kv;
-    const float* bias;
-    int64_t q_rs, k_rs, v_rs, do_rs;
-    int64_t bias_qs, bias_hs, bias_cols, bias_ss, bias_rows;
-    int64_t total_q, total_kv;
-    int num_seqs, hq, hkv, g, hpw, n_tiles, n_hg;
-    float scale, scale_log2;
-    int causal, window;
-    int bias_v4;      // bias rows 16-byte aligned (pointer and strides)
-    int bias_b32;     // 64 bias rows plus a row's columns span < 2^32 bytes (32-bit buffer offsets)
-    const uint16_t* o; int64_t o_rs;   // forward output (dQ with delta_w)
-    float* delta_w;   // non-null: the dQ kernel computes delta and writes it here
-};
-
-// Sum of the 8 products of one 16-byte chunk of O and dO. The preprocess and
-// the dQ kernel's fused delta both use it and combine chunks in the same tree,
-// so the two give bitwise equal deltas.
-template <typename T>
-__device__ inline float dot8(const u32x4_t a, const u32x4_t b) {
-    float acc = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc += lo16<T>(a[e]) * lo16<T>(b[e]) + hi16<T>(a[e]) * hi16<T>(b[e]);
-    return acc;
-}
-
-template <typename T, bool OUT_F32>
-__device__ inline void store4(void* base, int64_t off, float a, float b, float c, float d) {
-    if (OUT_F32) {
-        *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(base) + off) = f32x4_t{a, b, c, d};
-    } else {
-        st8(reinterpret_cast<uint16_t*>(base) + off, u32x2_t{T::pack2(a, b), T::pack2(c, d)});
-    }
-}
-
-// Staged lse / delta columns as the dK/dV products use them: lse (which = 0)
-// becomes -lse log2(e), with rows of no allowed key (lse = -inf) giving -inf
-// so that every P of theirs is exp2(-inf) = 0; delta (which = 1) becomes -delta.
-__device__ inline void neg_col(float* x, int which) {
-    const float v = *x;
-    *x = which ? -v : (v == kNegInf ? kNegInf : -v * kLog2e);
-}
 
 // ---------------------------------------------------------------------------
 // dQ.  8 waves (2 per SIMD), 32 query rows x 1 head per wave, the heads of a
@@ -1162,30 +1117,7 @@ __global__ __launch_bounds__(256) void zero_outside_kernel(ZeroJobs jobs) {
 
 int gcd_int(int a, int b) { while (b) { const int t = a % b; a = b; b = t; } return a; }
 
-BwdKParams make_params(const BwdArgs& a) {
-    const Geometry& g = a.geo;
-    BwdKParams p;
-    p.q = (const uint16_t*)a.q; p.k = (const uint16_t*)a.k; p.v = (const uint16_t*)a.v;
-    p.dout = (const uint16_t*)a.dout;
-    p.lse = a.lse; p.delta = a.delta;
-    p.dq = a.dq; p.dk = a.dk; p.dv = a.dv;
-    p.cu_q = g.cu_q; p.cu_kv = g.cu_kv; p.bias = g.bias;
-    p.q_rs = a.q_rs; p.k_rs = a.k_rs; p.v_rs = a.v_rs; p.do_rs = a.do_rs;
-    p.bias_qs = g.bias_qs; p.bias_hs = g.bias_hs; p.bias_cols = g.bias_cols;
-    p.bias_ss = g.bias_ss; p.bias_rows = g.bias_rows;
-    p.total_q = g.total_q; p.total_kv = g.total_kv;
-    p.num_seqs = g.num_seqs; p.hq = g.hq; p.hkv = g.hkv; p.g = g.g;
-    p.hpw = 1;
-    p.n_tiles = 0; p.n_hg = 0;
-    p.scale = g.scale; p.scale_log2 = g.scale * kLog2e;
-    p.causal = g.causal; p.window = g.window > 0 ? g.window : 0;
-    p.bias_b32 = g.bias != nullptr && (64 * g.bias_qs + g.bias_cols) * 4 < ((int64_t)1 << 32);
-    p.bias_v4 = g.bias != nullptr && ((uintptr_t)g.bias % 16 == 0) && g.bias_qs % 4 == 0 && g.bias_hs % 4 == 0 &&
-                (g.bias_ss < 0 || g.bias_ss % 4 == 0);
-    p.o = (const uint16_t*)a.o; p.o_rs = a.o_rs;
-    p.delta_w = a.delta_out;
-    return p;
-}
+
 
 template <typename T, int D, int DV, int DO, int C0, int KB, bool OUT_F32, int NW = kWaves, int OCC = 1, int NB = 3>
 hipError_t launch_dq_typed(const BwdArgs& a, hipStream_t st) {
@@ -1254,6 +1186,7 @@ hipError_t launch_dkv_sym(const BwdArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((bwd_dkv_sym_kernel<T, D, DV, OUT_F32, NW>), dim3((unsigned)blocks), dim3(NW * 64), 0, st, p);
     return hipGetLastError();
 }
+
 
 }  // namespace
 
@@ -1356,6 +1289,11 @@ struct DkvLaunch {
             if (a.geo.bias == nullptr) return launch_dkv_sym<T, D, DV, F, 4>(a, st);
             return launch_dkv_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else if constexpr (D <= 128) {
+            // without a bias: one wave per SIMD, 64 keys per wave
+            if (a.geo.bias == nullptr) {
+                const hipError_t e = launch_bwd_dkv_wide(T::code, a, st);
+                if (e != hipErrorNotSupported) return e;
+            }
             return launch_dkv_typed<T, D, DV, DV, 0, 2, F>(a, st);
         } else {
             // 256-wide tiles: 32-query stages. D = 160 computes the whole

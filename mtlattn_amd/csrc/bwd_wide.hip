@@ -1,0 +1,537 @@
+// dK/dV for fp16/bf16 on gfx950 at the 128-wide tiles (head dims 80 to 128)
+// without a bias: one wave per SIMD, 64 keys per wave (counterpart of the
+// reference's bwd_dkv_mpp, src/attn_mpp.metal:546-647; the arithmetic is
+// that of bwd.hip's dK/dV kernels). Built with the compiler's MFMA results
+// kept in VGPRs (-mllvm -amdgpu-mfma-vgpr-form, build.py): the dK / dV
+// accumulators are pinned to the AGPRs by inline asm (mfma32_acc), and the S
+// and dP products' results, which the VALU reads, stay in VGPRs.
+#include <cstdlib>
+#include <type_traits>
+
+#include "common.h"
+#include "kernels.h"
+#include "bwd_common.h"
+#include "../../include/mtlattn_capi.h"
+
+namespace mtlattn {
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// dK/dV on the 128-wide tiles without a bias: workgroups of 4 waves, one per
+// SIMD (512 registers each), every wave computing all four products for its
+// own 64 keys -- two 32-key blocks -- in stages of 32 queries x 1 head.
+//  * Each Q or dO operand read from LDS feeds the MFMAs of both key blocks
+//    (0.5 KB of LDS per MFMA; the wave-pair kernel of bwd.hip reads 1 KB).
+//  * The K^T and V^T operands of the wave's keys stay in VGPRs; the 256
+//    dK / dV accumulators are pinned to the AGPRs (mfma32_acc, inline asm),
+//    which is why this file is built with the compiler's own MFMA results
+//    in VGPRs (build.py).
+//  * Iteration j is a software pipeline over two stages: S, P, dP and dV of
+//    stage j and dS and dK of stage j - 1, in four phases of 16 MFMAs, each
+//    written in issue order (one MFMA, its share of another product's VALU
+//    work, an LDS read ahead; groups kept in order by scheduling barriers):
+//      A. S(j)        beside dS(j - 1) of key block 1
+//      B. dK(j - 1)   beside P(j) of key block 0
+//      C. dP(j)       beside P(j) of key block 1
+//      D. dV(j)       beside dS(j) of key block 0 and stage j + 1's lse and
+//                     delta columns turned into -lse log2 e and -delta
+//  * Stages visit the query tiles top-down with the GQA group's heads inner,
+//    as the other dK/dV kernels do, on a 5-slot LDS ring (Q, dO, and each
+//    wave's own lse and delta columns): the loads of stage j + 3 go out
+//    between the products of iteration j, and every wave waits for its own
+//    loads of stage j + 1 in phase D, then one barrier per iteration.
+//  * A workgroup takes key blocks b and nb - 1 - b of a sequence (nb
+//    blocks): under causal masking every such pair is the same amount of
+//    work, which keeps the in-order dispatch balanced.
+// The arithmetic is that of the other dK/dV kernels: P and dS rounded to T,
+// dS from the rounded P, masks as -inf logits (scale > 0, host-checked).
+// ---------------------------------------------------------------------------
+template <typename T, int D, int DV, bool OUT_F32>
+__global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
+    static_assert(D == 128, "128-wide tiles");
+    constexpr int NW = 4, NKB = 2, KPW = 32 * NKB;     // waves, key blocks per wave, keys per wave
+    constexpr int DC = (DV + 15) / 16, DB = (DV + 31) / 32;
+    constexpr int QTL = 32;                             // queries per stage
+    constexpr int KB = NW * KPW;                        // keys per workgroup
+    constexpr int TILE = QTL * D * 2;                   // 8 KB
+    constexpr int LCOL = 64 * 4;                        // one lse / delta column (64 rows loaded)
+    constexpr int SLOT = 2 * TILE + NW * 2 * LCOL;      // Q, dO, each wave's own lse and delta columns
+    constexpr int NBUF = 5, AHEAD = 3;                 // slots; stages loading ahead
+    __shared__ __attribute__((aligned(1024))) char smem[NBUF * SLOT];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int L = xcd_remap(blockIdx.x, p.n_tiles * p.hkv);
+    const int hk = L / p.n_tiles;
+    const int t = L - hk * p.n_tiles;                  // early key blocks (heavier when causal) first
+    // Tiles are pairs of key blocks, block pi and block nb - 1 - pi of a
+    // sequence (nb blocks): with causal masking a pair's work is the same
+    // for every pair, so the in-order dispatch of workgroups keeps the CUs
+    // evenly loaded (single blocks, heaviest first per sequence, left each
+    // XCD's last sequence's heavy blocks running alone at the end).
+    const int s = find_seq_for_tile(p.cu_kv, p.num_seqs, 2 * KB, t, p.total_kv);
+    const int tb = tile_base(p.cu_kv, s, 2 * KB, p.total_kv);
+    if (t < tb) return;
+    const SeqRange qr = seq_range(p.cu_q, s, p.total_q);
+    const SeqRange kr = seq_range(p.cu_kv, s, p.total_kv);
+    const int q_len = qr.end - qr.start, kv_len = kr.end - kr.start;
+    const int pi = t - tb;
+    const int nb = (kv_len + KB - 1) / KB;
+    if (pi >= (nb + 1) / 2) return;
+    const int coff = kv_len - q_len;
+    for (int bi = 0; bi < 2; ++bi) {
+        const int blk = bi == 0 ? pi : nb - 1 - pi;
+        if (bi == 1 && blk == pi) break;
+        // the second block reloads the ring's slots: every wave is done with them
+        if (bi == 1) __syncthreads();
+        const int k0 = blk * KB;
+
+        const int kw = k0 + KPW * w;                 // first key of this wave (seq-local)
+        const bool wave_active = kw < kv_len;
+        const int wk_last = min(kv_len, kw + KPW) - 1;
+
+        // B operands of the S and dP products: K^T and V^T of both key blocks,
+        // lane = key kw + 32 kb + l32, d = 16 kc + 8 hi + j (keys past the end
+        // read the last key: masked; columns past DV are zero)
+        u32x4_t kf[NKB][DC], vf[NKB][DC];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            const int64_t grow = kr.start + min(kw + 32 * kb + l32, kv_len - 1);
+            const uint16_t* kp = p.k + grow * p.k_rs + (int64_t)hk * DV + 8 * hi;
+            const uint16_t* vp = p.v + grow * p.v_rs + (int64_t)hk * DV + 8 * hi;
+#pragma unroll
+            for (int kc = 0; kc < DC; ++kc) {
+                const bool in = DV % 16 == 0 || 16 * kc + 8 * hi < DV;
+                kf[kb][kc] = in ? ld16(kp + 16 * kc) : u32x4_t{};
+                vf[kb][kc] = in ? ld16(vp + 16 * kc) : u32x4_t{};
+            }
+        }
+        // settle the fragments here: the stage loop's own waits count only its
+        // direct loads
+        wait_vmcnt<0>();
+
+        const int k_last_wg = min(kv_len, k0 + KB) - 1;
+        const int q_lo = p.causal ? max(0, k0 - coff) / QTL * QTL : 0;
+        const int q_hi = p.window > 0 ? min(q_len, k_last_wg - coff + p.window) : q_len;
+        const int n_q_tiles = q_hi > q_lo ? (q_hi - q_lo + QTL - 1) / QTL : 0;
+        const int n_stages = n_q_tiles * p.g;
+        const int qt_first = q_lo + (n_q_tiles - 1) * QTL;
+
+        // Direct loads of a stage: the Q and dO tiles by all four waves (two
+        // 1 KB loads of each per wave), and every wave's own copy of the lse and
+        // delta columns (one row per lane; rows past the stage are loaded but
+        // never read), which the wave itself turns into -lse log2 e and -delta
+        // once they land, with no barrier in between. Every stage issues the same
+        // loads: past the last stage the loader cursor stays on it and reloads
+        // it into the free slot, so the wait counts below are constants.
+        TileStager<D, QTL, NW, DV> qst, dost;
+        qst.init(p.q_rs, w, lane);
+        dost.init(p.do_rs, w, lane);
+        constexpr int LQ = decltype(qst)::N;                 // loads per wave per tile
+        static_assert(decltype(qst)::PER % NW == 0, "whole tile loads per wave");
+        constexpr int NL = 2 * LQ + 2;                       // loads per wave per stage
+        static_assert(NL == 6, "the phases issue loads 0-5");
+        int ld_st = 0, ld_hl = 0, ld_qt = qt_first, ld_slot = 0;
+        const uint16_t* ld_q = p.q + (int64_t)(qr.start + qt_first) * p.q_rs + (int64_t)hk * p.g * DV;
+        const uint16_t* ld_do = p.dout + (int64_t)(qr.start + qt_first) * p.do_rs + (int64_t)hk * p.g * DV;
+        const int64_t l0 = (int64_t)(qr.start + qt_first) * p.hq + hk * p.g;
+        const float* ld_l = p.lse + l0;
+        const float* ld_d = p.delta + l0;
+        const int wcol = 2 * TILE + w * 2 * LCOL;            // this wave's lse column in a slot (delta: + LCOL)
+        const int64_t q_wrap = -(int64_t)(p.g - 1) * DV - (int64_t)QTL * p.q_rs;
+        const int64_t do_wrap = -(int64_t)(p.g - 1) * DV - (int64_t)QTL * p.do_rs;
+        const int64_t l_wrap = -(int64_t)(p.g - 1) - (int64_t)QTL * p.hq;
+        // per-lane source offsets of the cursor's stage (rows past the sequence
+        // end read its last row) and its LDS slot
+        uint32_t qo[LQ], dso[LQ], lvo = 0;
+        char* lbuf = smem;
+        auto prep = [&]() {
+            lbuf = smem + ld_slot * SLOT;
+            const int avail = q_len - ld_qt;                    // >= 1
+            if (avail >= QTL) {
+#pragma unroll
+                for (int j = 0; j < LQ; ++j) { qo[j] = qst.off[j]; dso[j] = dost.off[j]; }
+            } else {
+                const int rmax = max(avail - 1, 0);
+#pragma unroll
+                for (int j = 0; j < LQ; ++j) {
+                    const int i = w + j * NW;
+                    const int r = min(decltype(qst)::row_of(i, lane), rmax);
+                    qo[j] = decltype(qst)::lane_off(i, lane, r, (uint32_t)(2 * p.q_rs));
+                    dso[j] = decltype(dost)::lane_off(i, lane, r, (uint32_t)(2 * p.do_rs));
+                }
+            }
+            lvo = (uint32_t)min(lane, avail - 1) * (uint32_t)p.hq * 4u;
+        };
+        // load j of the cursor's stage: 0 .. LQ - 1 Q, LQ .. 2 LQ - 1 dO, then
+        // this wave's lse and delta columns
+        auto load = [&](int j) {
+            if (j < LQ) {
+                lds_dma16s(ld_q, qo[j], lbuf + (w + j * NW) * 1024);
+            } else if (j < 2 * LQ) {
+                lds_dma16s(ld_do, dso[j - LQ], lbuf + TILE + (w + (j - LQ) * NW) * 1024);
+            } else if (j == 2 * LQ) {
+                lds_dma4s(ld_l, lvo, lbuf + wcol);
+            } else {
+                lds_dma4s(ld_d, lvo, lbuf + wcol + LCOL);
+            }
+        };
+        // next slot; the source moves on only while stages remain
+        auto advance = [&]() {
+            ld_slot = ld_slot == NBUF - 1 ? 0 : ld_slot + 1;
+            if (ld_st + 1 >= n_stages) return;
+            ++ld_st;
+            if (++ld_hl == p.g) {
+                ld_hl = 0;
+                ld_qt -= QTL;
+                ld_q += q_wrap;
+                ld_do += do_wrap;
+                ld_l += l_wrap;
+                ld_d += l_wrap;
+            } else {
+                ld_q += DV;
+                ld_do += DV;
+                ld_l += 1;
+                ld_d += 1;
+            }
+        };
+        static_assert((AHEAD - 1) * NL <= 15, "vmcnt range");
+        // this wave's lse and delta columns of stage slot `slot` become -lse
+        // log2 e and -delta (lane = row; the wave's own loads, landed)
+        auto fix_cols = [&](int slot) {
+            float* c = reinterpret_cast<float*>(smem + slot * SLOT + wcol) + lane;
+            neg_col(c, 0);
+            neg_col(c + 64, 1);
+        };
+
+        const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
+        const float c2 = p.scale_log2;
+        f32x16_t accv[NKB][DB], acck[NKB][DB];       // dV^T, dK^T of both key blocks
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) accv[kb][db] = acck[kb][db] = f32x16_t{};
+
+        Band band[NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) band[kb] = query_band(kw + 32 * kb + l32, coff, q_len, kv_len, p.causal, p.window);
+
+        // Compute cursor: stage j (its slot and first query) and the slot of
+        // stage j - 1. Iteration j computes S, P, dP and dV of stage j and dS
+        // and dK of stage j - 1, in four phases of one MFMA stream each with
+        // the VALU work of another product beside it:
+        //   A. S(j)        beside dS(j - 1) = P (dP - delta), rounded to T
+        //   B. dK(j - 1)   beside half of P(j) = exp2(S c - lse'), rounded to T
+        //   C. dP(j)       beside the other half of P(j)
+        //   D. dV(j)       beside -lse log2 e, -delta of stage j + 1
+        // P(j) (packed) and dP(j) - delta stay in registers into iteration
+        // j + 1. The loads of stage j + 3 go out between the S products.
+        int c_hl = 0, c_qt = qt_first, c_slot = 0, p_slot = 0;
+        u32x4_t pk[NKB][2];                      // P of the stage in flight, rounded to T (B operands of dV)
+        f32x16_t pacc[NKB];                      // its dP - delta
+        f32x16_t sacc[NKB];
+        u32x4_t dsk[NKB][2];                     // dS of the previous stage, rounded to T (B operands of dK)
+        constexpr int NS = NKB * DC;             // S or dP products per stage
+        constexpr int NP = 2 * DB * NKB;         // dV or dK products per stage
+        constexpr int TPF = 4;                   // transposed operands read ahead
+        // Does any (query, key) of stage j fall outside the band? (the per-block
+        // tests of the other kernels over this wave's 64 keys)
+        auto stage_needs_mask = [&]() {
+            return (kw + KPW > kv_len) | (c_qt + QTL > q_len) | ((p.causal != 0) & (wk_last > c_qt + coff)) |
+                   ((p.window > 0) & (kw < min(q_len, c_qt + QTL) + coff - p.window));
+        };
+        // pair pr = 0..15 of a stage's 32 elements per lane: key block pr / 8,
+        // rows 2 (pr % 8) and 2 (pr % 8) + 1
+        auto exp_pair = [&](int pr, const f32x16_t& nl) {
+            const int kb = pr >> 3, r0 = 2 * (pr & 7);
+            const float x0 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r0], c2, nl[r0]));
+            const float x1 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r0 + 1], c2, nl[r0 + 1]));
+            pk[kb][r0 >> 3][(r0 & 7) >> 1] = T::pack2(x0, x1);
+        };
+        auto ds_pair = [&](int pr) {
+            const int kb = pr >> 3, r0 = 2 * (pr & 7);
+            const uint32_t wv = pk[kb][r0 >> 3][(r0 & 7) >> 1];
+            dsk[kb][r0 >> 3][(r0 & 7) >> 1] = T::pack2(lo16<T>(wv) * pacc[kb][r0], hi16<T>(wv) * pacc[kb][r0 + 1]);
+        };
+        auto read_col = [&](const char* slot, int which) {   // 16 rows of this wave's column, C layout
+            const float* c = reinterpret_cast<const float*>(slot + wcol + which * LCOL);
+            f32x16_t x;
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(c + 8 * rg + 4 * hi);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[4 * rg + e] = v4[e];
+            }
+            return x;
+        };
+
+        auto iter = [&](auto first_t, auto last_t, bool masked, int n_slot) {
+            constexpr bool FIRST = decltype(first_t)::value, LAST = decltype(last_t)::value;
+            const char* Qc = smem + c_slot * SLOT;   // stage j
+            const char* Qp = smem + p_slot * SLOT;   // stage j - 1
+            // A. S(j) beside dS(j - 1); the loads of stage j + 3 spread over the
+            //    S products
+            if constexpr (!LAST) {
+                const char* qrb = opaque(Qc + rbase);
+                u32x4_t qa[DC];
+#pragma unroll
+                for (int i = 0; i < 2 && i < DC; ++i) qa[i] = row_operand<D>(qrb, i, 0);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int kc = 0; kc < DC; ++kc) {
+#pragma unroll
+                    for (int kb = 0; kb < NKB; ++kb) {
+                        const int i = NKB * kc + kb;
+                        sacc[kb] = mfma32<T>(qa[kc], kf[kb][kc], kc == 0 ? f32x16_t{} : sacc[kb]);
+                        if (kb == NKB - 1 && kc + 2 < DC) qa[kc + 2] = row_operand<D>(qrb, kc + 2, 0);
+                        if (i == 1) load(0);
+                        if (i == NS / 2 + 1) load(1);
+                        if constexpr (!FIRST) {   // dS(j - 1) of key block 1
+#pragma unroll
+                            for (int pr = 8; pr < 16; ++pr)
+                                if ((pr - 8) * NS / 8 == i) ds_pair(pr);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+                // out-of-band logits -> -inf (P = exp2(-inf) = 0; scale > 0 is
+                // host-checked); a real branch, taken by the stages on a band edge
+                if (masked) {
+                    asm volatile("");
+                    const int qb0 = c_qt + 4 * hi;
+#pragma unroll
+                    for (int kb = 0; kb < NKB; ++kb) {
+                        const int d0 = qb0 - band[kb].lo;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            sacc[kb][r] = (uint32_t)(d0 + 8 * (r >> 2) + (r & 3)) < band[kb].width ? sacc[kb][r] : kNegInf;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int pr = 8; pr < 16; ++pr) ds_pair(pr);
+            }
+            // B. dK(j - 1) beside P(j) of key block 0 (the dK and dV products
+            //    are inline asm with their own hazard wait, mfma32_acc)
+            __builtin_amdgcn_sched_barrier(0);
+            f32x16_t nl;                             // -lse log2(e) of stage j's rows
+            if constexpr (!LAST) nl = read_col(Qc, 0);
+            if constexpr (!FIRST) {
+                const char* qtb = opaque(Qp + tbase);
+                u32x4_t ta[2 * DB];
+#pragma unroll
+                for (int i = 0; i < TPF && i < 2 * DB; ++i) ta[i] = tr_operand<D>(qtb, i / DB, i % DB);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i2 = 0; i2 < 2 * DB; ++i2) {
+                    const int qc = i2 / DB, db = i2 % DB;
+#pragma unroll
+                    for (int kb = 0; kb < NKB; ++kb) {
+                        const int i = NKB * i2 + kb;
+                        mfma32_acc<T>(acck[kb][db], ta[i2], dsk[kb][qc]);
+                        if (kb == NKB - 1 && i2 + TPF < 2 * DB)
+                            ta[i2 + TPF] = tr_operand<D>(qtb, (i2 + TPF) / DB, (i2 + TPF) % DB);
+                        if (!LAST && i == 1) load(2);
+                        if (!LAST && i == NP / 2 + 1) load(3);
+                        if constexpr (!LAST) {
+#pragma unroll
+                            for (int pr = 0; pr < 8; ++pr)
+                                if (pr * NP / 8 == i) exp_pair(pr, nl);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+            } else {
+                load(2);
+                load(3);
+#pragma unroll
+                for (int pr = 0; pr < 8; ++pr) exp_pair(pr, nl);
+            }
+            if constexpr (!LAST) {
+                // C. dP(j) onto -delta beside P(j) of key block 1
+                {
+                    const char* drb = opaque(Qc + TILE + rbase);
+                    const f32x16_t dinit = read_col(Qc, 1);
+                    u32x4_t da[DC];
+#pragma unroll
+                    for (int i = 0; i < 2 && i < DC; ++i) da[i] = row_operand<D>(drb, i, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int kc = 0; kc < DC; ++kc) {
+#pragma unroll
+                        for (int kb = 0; kb < NKB; ++kb) {
+                            const int i = NKB * kc + kb;
+                            pacc[kb] = mfma32<T>(da[kc], vf[kb][kc], kc == 0 ? dinit : pacc[kb]);
+                            if (kb == NKB - 1 && kc + 2 < DC) da[kc + 2] = row_operand<D>(drb, kc + 2, 0);
+                            if (i == 1) load(4);
+                            if (i == NS / 2 + 1) load(5);
+#pragma unroll
+                            for (int pr = 8; pr < 16; ++pr)
+                                if ((pr - 8) * NS / 8 == i) exp_pair(pr, nl);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
+                }
+                // D. dV(j) beside the columns of stage j + 1: this wave's own
+                //    loads of that stage have landed once at most the two later
+                //    stages' loads are in flight
+                __builtin_amdgcn_sched_barrier(0);
+                wait_vmcnt<(AHEAD - 1) * NL>();
+                fix_cols(n_slot);
+                {
+                    const char* dtb = opaque(Qc + TILE + tbase);
+                    u32x4_t ta[2 * DB];
+#pragma unroll
+                    for (int i = 0; i < TPF && i < 2 * DB; ++i) ta[i] = tr_operand<D>(dtb, i / DB, i % DB);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i2 = 0; i2 < 2 * DB; ++i2) {
+                        const int qc = i2 / DB, db = i2 % DB;
+#pragma unroll
+                        for (int kb = 0; kb < NKB; ++kb) {
+                            const int i = NKB * i2 + kb;
+                            mfma32_acc<T>(accv[kb][db], ta[i2], pk[kb][qc]);
+                            if (kb == NKB - 1 && i2 + TPF < 2 * DB)
+                                ta[i2 + TPF] = tr_operand<D>(dtb, (i2 + TPF) / DB, (i2 + TPF) % DB);
+                            // dS(j) of key block 0 (block 1 follows in the next
+                            // iteration's phase A)
+#pragma unroll
+                            for (int pr = 0; pr < 8; ++pr)
+                                if (pr * NP / 8 == i) ds_pair(pr);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
+                }
+            }
+        };
+        // next compute stage: slots and first query
+        auto step = [&](int n_slot) {
+            p_slot = c_slot;
+            c_slot = n_slot;
+            if (++c_hl == p.g) {
+                c_hl = 0;
+                c_qt -= QTL;
+            }
+        };
+
+        if (n_stages > 0) {
+#pragma unroll
+            for (int i = 0; i < AHEAD; ++i) {
+                prep();
+#pragma unroll
+                for (int l = 0; l < NL; ++l) load(l);
+                advance();
+            }
+            wait_vmcnt<(AHEAD - 1) * NL>();   // the K tile and stage 0
+            fix_cols(0);
+            __syncthreads();
+            // every wave's loads of stage j + 1 have landed by the end of
+            // iteration j (each waited for its own in phase D): the barrier
+            // after it publishes them
+            int n_slot = c_slot == NBUF - 1 ? 0 : c_slot + 1;
+            prep();
+            iter(std::true_type{}, std::false_type{}, stage_needs_mask(), n_slot);
+            advance();
+            __syncthreads();
+            step(n_slot);
+            for (int j = 1; j < n_stages; ++j) {
+                n_slot = c_slot == NBUF - 1 ? 0 : c_slot + 1;
+                prep();
+                iter(std::false_type{}, std::false_type{}, stage_needs_mask(), n_slot);
+                advance();
+                __syncthreads();
+                step(n_slot);
+            }
+            iter(std::false_type{}, std::true_type{}, false, 0);
+            // The last accumulating MFMAs' results settle before anything reads
+            // the accumulators (the compiler does not track the inline-asm
+            // MFMAs, and may copy accumulators out at the end of this block):
+            // these asm statements take every accumulator as an operand, the
+            // first one after 32 wait states, so no read can come earlier.
+            asm volatile("s_nop 15\n\ts_nop 15" : "+a"(acck[0][0]), "+a"(acck[1][0]));
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                if (db > 0) asm volatile("" : "+a"(acck[0][db]), "+a"(acck[1][db]));
+                asm volatile("" : "+a"(accv[0][db]), "+a"(accv[1][db]));
+            }
+        }
+        // the reloads issued past the last stage land before the wave ends
+        wait_vmcnt<0>();
+
+        if (wave_active) {
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                const int key = kw + 32 * kb + l32;
+                if (key >= kv_len) continue;
+                const int64_t off = (int64_t)(kr.start + key) * ((int64_t)p.hkv * DV) + (int64_t)hk * DV;
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                    for (int rg = 0; rg < 4; ++rg) {
+                        const int d = 32 * db + 8 * rg + 4 * hi;
+                        if (DV % 32 != 0 && d >= DV) continue;
+                        store4<T, OUT_F32>(p.dv, off + d, accv[kb][db][4 * rg], accv[kb][db][4 * rg + 1],
+                                           accv[kb][db][4 * rg + 2], accv[kb][db][4 * rg + 3]);
+                        store4<T, OUT_F32>(p.dk, off + d, acck[kb][db][4 * rg] * p.scale,
+                                           acck[kb][db][4 * rg + 1] * p.scale, acck[kb][db][4 * rg + 2] * p.scale,
+                                           acck[kb][db][4 * rg + 3] * p.scale);
+                    }
+                }
+            }
+        }
+    }
+}
+
+
+template <typename T, int DV, bool OUT_F32>
+hipError_t launch_wide(const BwdArgs& a, hipStream_t st) {
+    BwdKParams p = make_params(a);
+    p.n_tiles = (int)(a.geo.total_kv / 512) + a.geo.num_seqs + 1;   // pairs of 256-key blocks
+    const int64_t blocks = (int64_t)p.n_tiles * a.geo.hkv;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((bwd_dkv_wide_kernel<T, 128, DV, OUT_F32>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_wide_dims(const BwdArgs& a, hipStream_t st) {
+    const bool f = a.out_f32 != 0;
+    switch (a.geo.d) {
+        case 80: return f ? launch_wide<T, 80, true>(a, st) : launch_wide<T, 80, false>(a, st);
+        case 88: return f ? launch_wide<T, 88, true>(a, st) : launch_wide<T, 88, false>(a, st);
+        case 96: return f ? launch_wide<T, 96, true>(a, st) : launch_wide<T, 96, false>(a, st);
+        case 128: return f ? launch_wide<T, 128, true>(a, st) : launch_wide<T, 128, false>(a, st);
+        default: return hipErrorNotSupported;
+    }
+}
+
+// MTLATTN_DKV_WIDE=0 turns this kernel off (the wave-pair kernel of bwd.hip
+// then runs these head dims): for A/B measurements.
+bool wide_enabled() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("MTLATTN_DKV_WIDE");
+        v = (e == nullptr || e[0] != '0') ? 1 : 0;
+    }
+    return v != 0;
+}
+
+}  // namespace
+
+// hipErrorNotSupported: not this kernel's problem (a bias, another head dim,
+// row strides whose 256-row K tile offsets would pass 32 bits); the caller
+// runs another kernel.
+hipError_t launch_bwd_dkv_wide(int type_code, const BwdArgs& a, hipStream_t st) {
+    // (scale > 0: the masks enter as -inf initial S accumulators, which a
+    // negative scale would turn into +inf logits)
+    if (a.geo.bias != nullptr || !(a.geo.scale > 0.f) || !wide_enabled()) return hipErrorNotSupported;
+    if (a.k_rs <= 0 || a.k_rs >= ((int64_t)1 << 23) || a.q_rs >= ((int64_t)1 << 25) || a.do_rs >= ((int64_t)1 << 25))
+        return hipErrorNotSupported;
+    if (type_code == BF16::code) return launch_wide_dims<BF16>(a, st);
+    if (type_code == F16::code) return launch_wide_dims<F16>(a, st);
+    return hipErrorNotSupported;
+}
+
+}  // namespace mtlattn

@@ -98,12 +98,18 @@ __global__ __launch_bounds__(256) void calib_read_kernel(const u32x4_t* __restri
 //   9 role 6 with the attention softmax's dependences: per MFMA two
 //     v_fma_f32 -> v_exp_f32 pairs, one v_cvt_pk_bf16_f32 of the previous
 //     pair and one v_dot2c_f32_bf16 row-sum step on the pair before that
+//  10 global_load_lds_dwordx4 (1 KB direct-to-LDS loads of an L2-resident
+//     1 KB source): 8 per iteration, at most 16 in flight
+//  11 role 3's 8 MFMAs per iteration in one wave with 2 of role 10's loads
+//     between them (after MFMAs 1 and 5), at most 8 loads in flight
+//  12 role 8 with each LDS operand shared by two MFMAs (one ds_read_b128
+//     per two MFMAs, four reads ahead): 0.5 KB of LDS per MFMA
 // The instructions are inline asm so that their number and order are
 // exactly these. Each wave records its s_memtime cycles (shader clock) and
 // s_memrealtime ticks (100 MHz).
-constexpr int kRateOps[10] = {0, 16, 16, 8, 8, 16, 8, 8, 8, 8};   // roles 6-9: MFMAs
+constexpr int kRateOps[13] = {0, 16, 16, 8, 8, 16, 8, 8, 8, 8, 8, 8, 8};   // roles 6-9, 11, 12: MFMAs
 
-__device__ float rate_role(int role, int iters, int lane, const char* lds) {
+__device__ float rate_role(int role, int iters, int lane, const char* lds, const float* src) {
     float x[18];
 #pragma unroll
     for (int j = 0; j < 18; ++j) x[j] = 0.3f + 0.01f * j + 1e-4f * lane;
@@ -210,6 +216,59 @@ __device__ float rate_role(int role, int iters, int lane, const char* lds) {
                 asm volatile("v_dot2c_f32_bf16 %0, %1, %2" : "+v"(sum) : "v"(ones), "v"(pk[(g + 7) & 7]));
             }
         x[0] += sum;
+    } else if (role == 10 || role == 11) {
+        // source: 1 KB of this block's sink (lane chunk lane * 16); LDS
+        // destination rotates over 8 KB of the buffer
+        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
+        const uint32_t voff = (uint32_t)lane * 16u;
+        auto dma = [&](int slot) {
+            asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(src),
+                         "{m0}"(base + (uint32_t)(slot & 7) * 1024u) : "memory");
+        };
+        if (role == 10) {
+            for (int i = 0; i < iters; ++i) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dma(j);
+                asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+            }
+        } else {
+            for (int i = 0; i < iters; ++i) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c0) : "v"(a), "v"(b));
+                    dma(2 * u);
+                    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c1) : "v"(a), "v"(b));
+                    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c2) : "v"(a), "v"(b));
+                    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c3) : "v"(a), "v"(b));
+                }
+                asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else if (role == 12) {
+        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
+        auto rd = [&](int g) { return base + (uint32_t)(((g & 7) * 1024 + lane * 16) & 8191); };
+#pragma unroll
+        for (int g = 0; g < 4; ++g) asm volatile("ds_read_b128 %0, %1" : "=v"(r[g]) : "v"(rd(g)) : "memory");
+        for (int i = 0; i < iters; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                // operand r[g] feeds two MFMAs (two independent chains each)
+                asm volatile("s_waitcnt lgkmcnt(3)" ::: "memory");
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(g & 1 ? c2 : c0) : "v"(r[g]), "v"(b));
+                asm volatile("ds_read_b128 %0, %1" : "=v"(r[(g + 4) & 7]) : "v"(rd(g + 4)) : "memory");
+                const int j = 4 * g;
+                asm volatile("v_exp_f32 %0, %0" : "+v"(x[j]));
+                asm volatile("v_exp_f32 %0, %0" : "+v"(x[j + 1]));
+                asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(x[(j + 8) & 15]) : "v"(x[16]), "v"(x[17]));
+                asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(x[(j + 9) & 15]) : "v"(x[16]), "v"(x[17]));
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(g & 1 ? c3 : c1) : "v"(r[g]), "v"(a));
+                asm volatile("v_exp_f32 %0, %0" : "+v"(x[j + 2]));
+                asm volatile("v_exp_f32 %0, %0" : "+v"(x[j + 3]));
+                asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(x[(j + 10) & 15]) : "v"(x[16]), "v"(x[17]));
+                asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(x[(j + 11) & 15]) : "v"(x[16]), "v"(x[17]));
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     } else if (role == 5) {
         const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
         for (int i = 0; i < iters; ++i) {
@@ -240,7 +299,7 @@ __global__ __launch_bounds__(512, 1) void calib_rates_kernel(int ra, int rb, int
     __syncthreads();
     const int role = __builtin_amdgcn_readfirstlane(w < 4 ? ra : rb);   // wave-uniform
     const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
-    const float s = role ? rate_role(role, iters, lane, lds) : 0.f;
+    const float s = role ? rate_role(role, iters, lane, lds, sink + blockIdx.x * 512) : 0.f;
     const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
     if (s == 1.2345f) sink[blockIdx.x * 512 + threadIdx.x] = s;   // keeps the streams live
     if (lane == 0) {
@@ -276,10 +335,10 @@ int mtlattn_calib_read(const void* src, int64_t bytes, int blocks, uint32_t* sin
 // sink: blocks * 512 floats; cyc: blocks * 8 * 2 u64 (per wave: shader
 // cycles, 100 MHz ticks). Operations per iteration of role r: ops_per_iter.
 int mtlattn_calib_rates(int ra, int rb, int iters, int blocks, float* sink, unsigned long long* cyc, void* stream) {
-    if (ra < 0 || ra > 9 || rb < 0 || rb > 9 || iters < 1 || blocks < 1) return (int)hipErrorInvalidValue;
+    if (ra < 0 || ra > 12 || rb < 0 || rb > 12 || iters < 1 || blocks < 1) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(calib_rates_kernel, dim3(blocks), dim3(512), 0, (hipStream_t)stream, ra, rb, iters, sink, cyc);
     return (int)hipGetLastError();
 }
-int mtlattn_calib_rate_ops(int role) { return role >= 0 && role <= 9 ? kRateOps[role] : 0; }
+int mtlattn_calib_rate_ops(int role) { return role >= 0 && role <= 12 ? kRateOps[role] : 0; }
 
 }  // extern "C"

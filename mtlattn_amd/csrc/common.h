@@ -96,6 +96,24 @@ __device__ inline f32x16_t mfma32<F16>(const u32x4_t& a, const u32x4_t& b, const
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
+// c += a * b with the accumulator pinned to the accumulation registers
+// (AGPRs), as inline asm: for kernels whose accumulators fill the AGPRs while
+// the VGPRs hold everything else. The compiler's hazard tracking does not
+// see these, so each carries its own s_nop 1: the two wait states an MFMA
+// needs after a VALU instruction wrote its a or b (the compiler may copy an
+// operand into place right before the asm). Readers of c keep their own
+// distance from the last of these.
+template <typename T>
+__device__ inline void mfma32_acc(f32x16_t& c, const u32x4_t& a, const u32x4_t& b);
+template <>
+__device__ inline void mfma32_acc<BF16>(f32x16_t& c, const u32x4_t& a, const u32x4_t& b) {
+    asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+template <>
+__device__ inline void mfma32_acc<F16>(f32x16_t& c, const u32x4_t& a, const u32x4_t& b) {
+    asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
 template <typename T>
 __device__ inline f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c);
 template <>

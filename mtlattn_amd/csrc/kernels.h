@@ -89,6 +89,9 @@ hipError_t launch_bwd_preprocess(int dtype, const Geometry& geo, const void* o, 
                                  const void* dout, int64_t do_rs, float* delta, hipStream_t st);
 hipError_t launch_bwd_dq_mfma(int dtype, const BwdArgs& a, hipStream_t st);
 hipError_t launch_bwd_dkv_mfma(int dtype, const BwdArgs& a, hipStream_t st);
+// dK/dV without a bias at head dims 80-128, one wave per SIMD (bwd_wide.hip);
+// hipErrorNotSupported when the problem is not for it. type_code: BF16::code / F16::code.
+hipError_t launch_bwd_dkv_wide(int type_code, const BwdArgs& a, hipStream_t st);
 hipError_t launch_bwd_dq_generic(int dtype, const BwdArgs& a, hipStream_t st);
 hipError_t launch_bwd_dkv_generic(int dtype, const BwdArgs& a, hipStream_t st);
 // fp32 inputs on the fp32 matrix cores (f32_mfma_head_dim, 16-byte aligned
