@@ -126,11 +126,9 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
         // once they land, with no barrier in between. Every stage issues the same
         // loads: past the last stage the loader cursor stays on it and reloads
         // it into the free slot, so the wait counts below are constants.
-        TileStager<D, QTL, NW, DV> qst, dost;
-        qst.init(p.q_rs, w, lane);
-        dost.init(p.do_rs, w, lane);
-        constexpr int LQ = decltype(qst)::N;                 // loads per wave per tile
-        static_assert(decltype(qst)::PER % NW == 0, "whole tile loads per wave");
+        using Stager = TileStager<D, QTL, NW, DV>;           // the tiles' load layout
+        constexpr int LQ = Stager::N;                        // loads per wave per tile
+        static_assert(Stager::PER % NW == 0, "whole tile loads per wave");
         constexpr int NL = 2 * LQ + 2;                       // loads per wave per stage
         static_assert(NL == 6, "the phases issue loads 0-5");
         int ld_st = 0, ld_hl = 0, ld_qt = qt_first, ld_slot = 0;
@@ -147,23 +145,23 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
         // end read its last row) and its LDS slot
         uint32_t qo[LQ], dso[LQ], lvo = 0;
         char* lbuf = smem;
+        // (recomputed from the lane index at every stage, behind an empty asm:
+        // a few VALU operations, where offsets kept from the start would be
+        // loop-invariant registers that the allocator spills)
         auto prep = [&]() {
             lbuf = smem + ld_slot * SLOT;
             const int avail = q_len - ld_qt;                    // >= 1
-            if (avail >= QTL) {
+            const int rmax = min(avail, QTL) - 1;
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
 #pragma unroll
-                for (int j = 0; j < LQ; ++j) { qo[j] = qst.off[j]; dso[j] = dost.off[j]; }
-            } else {
-                const int rmax = max(avail - 1, 0);
-#pragma unroll
-                for (int j = 0; j < LQ; ++j) {
-                    const int i = w + j * NW;
-                    const int r = min(decltype(qst)::row_of(i, lane), rmax);
-                    qo[j] = decltype(qst)::lane_off(i, lane, r, (uint32_t)(2 * p.q_rs));
-                    dso[j] = decltype(dost)::lane_off(i, lane, r, (uint32_t)(2 * p.do_rs));
-                }
+            for (int j = 0; j < LQ; ++j) {
+                const int i = w + j * NW;
+                const int r = min(Stager::row_of(i, ln), rmax);
+                qo[j] = Stager::lane_off(i, ln, r, (uint32_t)(2 * p.q_rs));
+                dso[j] = Stager::lane_off(i, ln, r, (uint32_t)(2 * p.do_rs));
             }
-            lvo = (uint32_t)min(lane, avail - 1) * (uint32_t)p.hq * 4u;
+            lvo = (uint32_t)min(ln, avail - 1) * (uint32_t)p.hq * 4u;
         };
         // load j of the cursor's stage: 0 .. LQ - 1 Q, LQ .. 2 LQ - 1 dO, then
         // this wave's lse and delta columns
@@ -250,10 +248,15 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
             const float x1 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r0 + 1], c2, nl[r0 + 1]));
             pk[kb][r0 >> 3][(r0 & 7) >> 1] = T::pack2(x0, x1);
         };
+        // (the empty asm keeps each pair in the phase it is written in: left
+        // alone, the compiler moves the pairs next to their use, the dK
+        // products, where they run serially)
         auto ds_pair = [&](int pr) {
             const int kb = pr >> 3, r0 = 2 * (pr & 7);
             const uint32_t wv = pk[kb][r0 >> 3][(r0 & 7) >> 1];
-            dsk[kb][r0 >> 3][(r0 & 7) >> 1] = T::pack2(lo16<T>(wv) * pacc[kb][r0], hi16<T>(wv) * pacc[kb][r0 + 1]);
+            uint32_t d = T::pack2(lo16<T>(wv) * pacc[kb][r0], hi16<T>(wv) * pacc[kb][r0 + 1]);
+            asm volatile("" : "+v"(d));
+            dsk[kb][r0 >> 3][(r0 & 7) >> 1] = d;
         };
         auto read_col = [&](const char* slot, int which) {   // 16 rows of this wave's column, C layout
             const float* c = reinterpret_cast<const float*>(slot + wcol + which * LCOL);
