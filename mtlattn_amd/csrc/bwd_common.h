@@ -49,9 +49,10 @@ __device__ inline void store4(void* base, int64_t off, float a, float b, float c
 // Staged lse / delta columns as the dK/dV products use them: lse (which = 0)
 // becomes -lse log2(e), with rows of no allowed key (lse = -inf) giving -inf
 // so that every P of theirs is exp2(-inf) = 0; delta (which = 1) becomes -delta.
+__device__ inline float neg_lse2(float v) { return v == kNegInf ? kNegInf : -v * kLog2e; }
 __device__ inline void neg_col(float* x, int which) {
     const float v = *x;
-    *x = which ? -v : (v == kNegInf ? kNegInf : -v * kLog2e);
+    *x = which ? -v : neg_lse2(v);
 }
 
 BwdKParams make_params(const BwdArgs& a) {

@@ -141,39 +141,37 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
         const int64_t q_wrap = -(int64_t)(p.g - 1) * DV - (int64_t)QTL * p.q_rs;
         const int64_t do_wrap = -(int64_t)(p.g - 1) * DV - (int64_t)QTL * p.do_rs;
         const int64_t l_wrap = -(int64_t)(p.g - 1) - (int64_t)QTL * p.hq;
-        // per-lane source offsets of the cursor's stage (rows past the sequence
-        // end read its last row) and its LDS slot
-        uint32_t qo[LQ], dso[LQ], lvo = 0;
+        // The cursor's stage: its LDS slot, the last row that exists (rows
+        // past the sequence end read it) and a per-stage copy of the lane
+        // index. Each load computes its own per-lane offset from that copy
+        // right before it is issued: a few VALU operations between the
+        // products, where offsets kept from the start would be loop-invariant
+        // registers that the allocator spills (the empty asm keeps the
+        // compiler from hoisting them out of the loop).
         char* lbuf = smem;
-        // (recomputed from the lane index at every stage, behind an empty asm:
-        // a few VALU operations, where offsets kept from the start would be
-        // loop-invariant registers that the allocator spills)
+        int ld_rmax = 0, ln = lane;
         auto prep = [&]() {
             lbuf = smem + ld_slot * SLOT;
-            const int avail = q_len - ld_qt;                    // >= 1
-            const int rmax = min(avail, QTL) - 1;
-            int ln = lane;
+            ld_rmax = min(q_len - ld_qt, QTL) - 1;           // >= 0
+            ln = lane;
             asm volatile("" : "+v"(ln));
-#pragma unroll
-            for (int j = 0; j < LQ; ++j) {
-                const int i = w + j * NW;
-                const int r = min(Stager::row_of(i, ln), rmax);
-                qo[j] = Stager::lane_off(i, ln, r, (uint32_t)(2 * p.q_rs));
-                dso[j] = Stager::lane_off(i, ln, r, (uint32_t)(2 * p.do_rs));
-            }
-            lvo = (uint32_t)min(ln, avail - 1) * (uint32_t)p.hq * 4u;
         };
         // load j of the cursor's stage: 0 .. LQ - 1 Q, LQ .. 2 LQ - 1 dO, then
         // this wave's lse and delta columns
         auto load = [&](int j) {
-            if (j < LQ) {
-                lds_dma16s(ld_q, qo[j], lbuf + (w + j * NW) * 1024);
-            } else if (j < 2 * LQ) {
-                lds_dma16s(ld_do, dso[j - LQ], lbuf + TILE + (w + (j - LQ) * NW) * 1024);
-            } else if (j == 2 * LQ) {
-                lds_dma4s(ld_l, lvo, lbuf + wcol);
+            if (j < 2 * LQ) {
+                const int i = w + (j % LQ) * NW;
+                const int r = min(Stager::row_of(i, ln), ld_rmax);
+                if (j < LQ)
+                    lds_dma16s(ld_q, Stager::lane_off(i, ln, r, (uint32_t)(2 * p.q_rs)), lbuf + i * 1024);
+                else
+                    lds_dma16s(ld_do, Stager::lane_off(i, ln, r, (uint32_t)(2 * p.do_rs)), lbuf + TILE + i * 1024);
             } else {
-                lds_dma4s(ld_d, lvo, lbuf + wcol + LCOL);
+                const uint32_t lvo = (uint32_t)min(ln, ld_rmax) * (uint32_t)p.hq * 4u;
+                if (j == 2 * LQ)
+                    lds_dma4s(ld_l, lvo, lbuf + wcol);
+                else
+                    lds_dma4s(ld_d, lvo, lbuf + wcol + LCOL);
             }
         };
         // next slot; the source moves on only while stages remain
@@ -197,11 +195,22 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
         };
         static_assert((AHEAD - 1) * NL <= 15, "vmcnt range");
         // this wave's lse and delta columns of stage slot `slot` become -lse
-        // log2 e and -delta (lane = row; the wave's own loads, landed)
+        // log2 e and -delta (lane = row; the wave's own loads, landed): read
+        // in one phase, written back in the next
         auto fix_cols = [&](int slot) {
             float* c = reinterpret_cast<float*>(smem + slot * SLOT + wcol) + lane;
             neg_col(c, 0);
             neg_col(c + 64, 1);
+        };
+        auto fix_read = [&](int slot, float& lv, float& dv) {
+            const float* c = reinterpret_cast<const float*>(smem + slot * SLOT + wcol) + lane;
+            lv = c[0];
+            dv = c[64];
+        };
+        auto fix_write = [&](int slot, float lv, float dv) {
+            float* c = reinterpret_cast<float*>(smem + slot * SLOT + wcol) + lane;
+            c[0] = neg_lse2(lv);
+            c[64] = -dv;
         };
 
         const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
@@ -234,6 +243,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
         constexpr int NS = NKB * DC;             // S or dP products per stage
         constexpr int NP = 2 * DB * NKB;         // dV or dK products per stage
         constexpr int TPF = 4;                   // transposed operands read ahead
+        static_assert(TPF == 4 && 2 * DB >= TPF, "phases A and C read B's and D's first four");
         // Does any (query, key) of stage j fall outside the band? (the per-block
         // tests of the other kernels over this wave's 64 keys)
         auto stage_needs_mask = [&]() {
@@ -258,24 +268,37 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
             asm volatile("" : "+v"(d));
             dsk[kb][r0 >> 3][(r0 & 7) >> 1] = d;
         };
+        // (the lane half from the per-stage lane copy: see prep)
         auto read_col = [&](const char* slot, int which) {   // 16 rows of this wave's column, C layout
             const float* c = reinterpret_cast<const float*>(slot + wcol + which * LCOL);
             f32x16_t x;
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
-                const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(c + 8 * rg + 4 * hi);
+                const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(c + 8 * rg + 4 * (ln >> 5));
 #pragma unroll
                 for (int e = 0; e < 4; ++e) x[4 * rg + e] = v4[e];
             }
             return x;
         };
 
+        // Each phase's first operands are read during the previous phase's
+        // last products, so no phase starts by waiting for the LDS (phase A's
+        // Q rows excepted: the barrier before it publishes them).
         auto iter = [&](auto first_t, auto last_t, bool masked, int n_slot) {
             constexpr bool FIRST = decltype(first_t)::value, LAST = decltype(last_t)::value;
             const char* Qc = smem + c_slot * SLOT;   // stage j
             const char* Qp = smem + p_slot * SLOT;   // stage j - 1
-            // A. S(j) beside dS(j - 1); the loads of stage j + 3 spread over the
-            //    S products
+            const char* qtb = opaque(Qp + tbase);    // B: Q^T of stage j - 1
+            const char* drb = opaque(Qc + TILE + rbase);   // C: dO rows of stage j
+            const char* dtb = opaque(Qc + TILE + tbase);   // D: dO^T of stage j
+            f32x16_t nl;                             // -lse log2(e) of stage j's rows
+            f32x16_t dinit;                          // -delta of stage j's rows
+            u32x4_t tq[2 * DB], da[DC], td[2 * DB];  // operands of B, C, D
+            float fl = 0.f, fd = 0.f;                // stage j + 1's lse and delta (this wave's rows)
+            auto read_tq = [&](int i) { tq[i] = tr_operand<D>(qtb, i / DB, i % DB); };
+            auto read_td = [&](int i) { td[i] = tr_operand<D>(dtb, i / DB, i % DB); };
+            // A. S(j) beside dS(j - 1) of key block 1; the loads of stage j + 3
+            //    start; B's first operands are read at the end
             if constexpr (!LAST) {
                 const char* qrb = opaque(Qc + rbase);
                 u32x4_t qa[DC];
@@ -291,11 +314,14 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                         if (kb == NKB - 1 && kc + 2 < DC) qa[kc + 2] = row_operand<D>(qrb, kc + 2, 0);
                         if (i == 1) load(0);
                         if (i == NS / 2 + 1) load(1);
-                        if constexpr (!FIRST) {   // dS(j - 1) of key block 1
+                        if constexpr (!FIRST) {
 #pragma unroll
                             for (int pr = 8; pr < 16; ++pr)
                                 if ((pr - 8) * NS / 8 == i) ds_pair(pr);
+                            if (i == NS - 2) { read_tq(0); read_tq(1); }
+                            if (i == NS - 1) { read_tq(2); read_tq(3); }
                         }
+                        if (i == NS - 3) nl = read_col(Qc, 0);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
@@ -303,7 +329,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                 // host-checked); a real branch, taken by the stages on a band edge
                 if (masked) {
                     asm volatile("");
-                    const int qb0 = c_qt + 4 * hi;
+                    const int qb0 = c_qt + 4 * (ln >> 5);
 #pragma unroll
                     for (int kb = 0; kb < NKB; ++kb) {
                         const int d0 = qb0 - band[kb].lo;
@@ -315,33 +341,31 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
             } else {
 #pragma unroll
                 for (int pr = 8; pr < 16; ++pr) ds_pair(pr);
+#pragma unroll
+                for (int i = 0; i < TPF; ++i) read_tq(i);
             }
             // B. dK(j - 1) beside P(j) of key block 0 (the dK and dV products
-            //    are inline asm with their own hazard wait, mfma32_acc)
+            //    are inline asm with their own hazard wait, mfma32_acc); C's
+            //    first operands are read at the end
             __builtin_amdgcn_sched_barrier(0);
-            f32x16_t nl;                             // -lse log2(e) of stage j's rows
-            if constexpr (!LAST) nl = read_col(Qc, 0);
             if constexpr (!FIRST) {
-                const char* qtb = opaque(Qp + tbase);
-                u32x4_t ta[2 * DB];
-#pragma unroll
-                for (int i = 0; i < TPF && i < 2 * DB; ++i) ta[i] = tr_operand<D>(qtb, i / DB, i % DB);
-                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i2 = 0; i2 < 2 * DB; ++i2) {
                     const int qc = i2 / DB, db = i2 % DB;
 #pragma unroll
                     for (int kb = 0; kb < NKB; ++kb) {
                         const int i = NKB * i2 + kb;
-                        mfma32_acc<T>(acck[kb][db], ta[i2], dsk[kb][qc]);
-                        if (kb == NKB - 1 && i2 + TPF < 2 * DB)
-                            ta[i2 + TPF] = tr_operand<D>(qtb, (i2 + TPF) / DB, (i2 + TPF) % DB);
-                        if (!LAST && i == 1) load(2);
-                        if (!LAST && i == NP / 2 + 1) load(3);
+                        mfma32_acc<T>(acck[kb][db], tq[i2], dsk[kb][qc]);
+                        if (kb == NKB - 1 && i2 + TPF < 2 * DB) read_tq(i2 + TPF);
                         if constexpr (!LAST) {
+                            if (i == 1) load(2);
+                            if (i == NP / 2 + 1) load(3);
 #pragma unroll
                             for (int pr = 0; pr < 8; ++pr)
                                 if (pr * NP / 8 == i) exp_pair(pr, nl);
+                            if (i == NP - 4) dinit = read_col(Qc, 1);
+                            if (i == NP - 2) da[0] = row_operand<D>(drb, 0, 0);
+                            if (i == NP - 1) da[1] = row_operand<D>(drb, 1, 0);
                         }
                         __builtin_amdgcn_sched_barrier(0);
                     }
@@ -351,60 +375,53 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                 load(3);
 #pragma unroll
                 for (int pr = 0; pr < 8; ++pr) exp_pair(pr, nl);
+                dinit = read_col(Qc, 1);
+                da[0] = row_operand<D>(drb, 0, 0);
+                da[1] = row_operand<D>(drb, 1, 0);
             }
             if constexpr (!LAST) {
-                // C. dP(j) onto -delta beside P(j) of key block 1
-                {
-                    const char* drb = opaque(Qc + TILE + rbase);
-                    const f32x16_t dinit = read_col(Qc, 1);
-                    u32x4_t da[DC];
+                // C. dP(j) onto -delta beside P(j) of key block 1; at the end,
+                //    D's first operands and the columns of stage j + 1 (this
+                //    wave's own loads of that stage have landed once at most
+                //    the two later stages' loads are in flight)
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int i = 0; i < 2 && i < DC; ++i) da[i] = row_operand<D>(drb, i, 0);
-                    __builtin_amdgcn_sched_barrier(0);
+                for (int kc = 0; kc < DC; ++kc) {
 #pragma unroll
-                    for (int kc = 0; kc < DC; ++kc) {
+                    for (int kb = 0; kb < NKB; ++kb) {
+                        const int i = NKB * kc + kb;
+                        pacc[kb] = mfma32<T>(da[kc], vf[kb][kc], kc == 0 ? dinit : pacc[kb]);
+                        if (kb == NKB - 1 && kc + 2 < DC) da[kc + 2] = row_operand<D>(drb, kc + 2, 0);
+                        if (i == 1) load(4);
+                        if (i == NS / 2 + 1) load(5);
 #pragma unroll
-                        for (int kb = 0; kb < NKB; ++kb) {
-                            const int i = NKB * kc + kb;
-                            pacc[kb] = mfma32<T>(da[kc], vf[kb][kc], kc == 0 ? dinit : pacc[kb]);
-                            if (kb == NKB - 1 && kc + 2 < DC) da[kc + 2] = row_operand<D>(drb, kc + 2, 0);
-                            if (i == 1) load(4);
-                            if (i == NS / 2 + 1) load(5);
-#pragma unroll
-                            for (int pr = 8; pr < 16; ++pr)
-                                if ((pr - 8) * NS / 8 == i) exp_pair(pr, nl);
-                            __builtin_amdgcn_sched_barrier(0);
+                        for (int pr = 8; pr < 16; ++pr)
+                            if ((pr - 8) * NS / 8 == i) exp_pair(pr, nl);
+                        if (i == NS - 3) {
+                            wait_vmcnt<(AHEAD - 1) * NL>();
+                            fix_read(n_slot, fl, fd);
                         }
+                        if (i == NS - 2) { read_td(0); read_td(1); }
+                        if (i == NS - 1) { read_td(2); read_td(3); }
+                        __builtin_amdgcn_sched_barrier(0);
                     }
                 }
-                // D. dV(j) beside the columns of stage j + 1: this wave's own
-                //    loads of that stage have landed once at most the two later
-                //    stages' loads are in flight
+                // D. dV(j) beside dS(j) of key block 0 (block 1 follows in the
+                //    next iteration's phase A); stage j + 1's columns written
                 __builtin_amdgcn_sched_barrier(0);
-                wait_vmcnt<(AHEAD - 1) * NL>();
-                fix_cols(n_slot);
-                {
-                    const char* dtb = opaque(Qc + TILE + tbase);
-                    u32x4_t ta[2 * DB];
 #pragma unroll
-                    for (int i = 0; i < TPF && i < 2 * DB; ++i) ta[i] = tr_operand<D>(dtb, i / DB, i % DB);
-                    __builtin_amdgcn_sched_barrier(0);
+                for (int i2 = 0; i2 < 2 * DB; ++i2) {
+                    const int qc = i2 / DB, db = i2 % DB;
 #pragma unroll
-                    for (int i2 = 0; i2 < 2 * DB; ++i2) {
-                        const int qc = i2 / DB, db = i2 % DB;
+                    for (int kb = 0; kb < NKB; ++kb) {
+                        const int i = NKB * i2 + kb;
+                        mfma32_acc<T>(accv[kb][db], td[i2], pk[kb][qc]);
+                        if (kb == NKB - 1 && i2 + TPF < 2 * DB) read_td(i2 + TPF);
+                        if (i == 2) fix_write(n_slot, fl, fd);
 #pragma unroll
-                        for (int kb = 0; kb < NKB; ++kb) {
-                            const int i = NKB * i2 + kb;
-                            mfma32_acc<T>(accv[kb][db], ta[i2], pk[kb][qc]);
-                            if (kb == NKB - 1 && i2 + TPF < 2 * DB)
-                                ta[i2 + TPF] = tr_operand<D>(dtb, (i2 + TPF) / DB, (i2 + TPF) % DB);
-                            // dS(j) of key block 0 (block 1 follows in the next
-                            // iteration's phase A)
-#pragma unroll
-                            for (int pr = 0; pr < 8; ++pr)
-                                if (pr * NP / 8 == i) ds_pair(pr);
-                            __builtin_amdgcn_sched_barrier(0);
-                        }
+                        for (int pr = 0; pr < 8; ++pr)
+                            if (pr * NP / 8 == i) ds_pair(pr);
+                        __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             }
