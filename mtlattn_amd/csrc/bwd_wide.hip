@@ -1,10 +1,13 @@
-// dK/dV for fp16/bf16 on gfx950 at the 128-wide tiles (head dims 80 to 128)
-// without a bias: one wave per SIMD, 64 keys per wave (counterpart of the
-// reference's bwd_dkv_mpp, src/attn_mpp.metal:546-647; the arithmetic is
-// that of bwd.hip's dK/dV kernels). Built with the compiler's MFMA results
-// kept in VGPRs (-mllvm -amdgpu-mfma-vgpr-form, build.py): the dK / dV
-// accumulators are pinned to the AGPRs by inline asm (mfma32_acc), and the S
-// and dP products' results, which the VALU reads, stay in VGPRs.
+// dK/dV for fp16/bf16 on gfx950 without a bias: one wave per SIMD, 64 keys
+// per wave at the 128-wide tiles (head dims 80 to 128) and 32 at the 256-wide
+// ones (head dim 256: one pass over all output columns; at 160 the wave-pair
+// kernel, which holds all 160 columns, measured faster) -- counterpart of the
+// reference's bwd_dkv_mpp, src/attn_mpp.metal:546-647 (instances 668-679);
+// the arithmetic is that of bwd.hip's dK/dV kernels. Built with the
+// compiler's MFMA results kept in VGPRs (-mllvm -amdgpu-mfma-vgpr-form,
+// build.py): the dK / dV accumulators are pinned to the AGPRs by inline asm
+// (mfma32_acc), and the S and dP products' results, which the VALU reads,
+// stay in VGPRs.
 #include <cstdlib>
 #include <type_traits>
 
@@ -18,46 +21,56 @@ namespace mtlattn {
 namespace {
 
 // ---------------------------------------------------------------------------
-// dK/dV on the 128-wide tiles without a bias: workgroups of 4 waves, one per
-// SIMD (512 registers each), every wave computing all four products for its
-// own 64 keys -- two 32-key blocks -- in stages of 32 queries x 1 head.
-//  * Each Q or dO operand read from LDS feeds the MFMAs of both key blocks
-//    (0.5 KB of LDS per MFMA; the wave-pair kernel of bwd.hip reads 1 KB).
-//  * The K^T and V^T operands of the wave's keys stay in VGPRs; the 256
-//    dK / dV accumulators are pinned to the AGPRs (mfma32_acc, inline asm),
-//    which is why this file is built with the compiler's own MFMA results
-//    in VGPRs (build.py).
+// dK/dV without a bias: workgroups of 4 waves, one per SIMD (512 registers
+// each), every wave computing all four products for its own NKB 32-key
+// blocks (two at the 128-wide tiles, one at the 256-wide ones) in stages of
+// 32 queries x 1 head.
+//  * At 64 keys per wave each Q or dO operand read from LDS feeds the MFMAs
+//    of both key blocks (0.5 KB of LDS per MFMA; the wave-pair kernel of
+//    bwd.hip reads 1 KB). At 32 keys per wave and 256 columns the K^T and V^T
+//    operands and the accumulators of all columns fill the registers, so S
+//    and dP are computed once for all output columns (the wave-pair kernel
+//    computes the 256 columns as two 128-column slices, each recomputing S
+//    and dP).
+//  * The K^T and V^T operands of the wave's keys stay in VGPRs; the dK / dV
+//    accumulators (256 at D = 128 and D = 256) are pinned to the AGPRs
+//    (mfma32_acc, inline asm), which is why this file is built with the
+//    compiler's own MFMA results in VGPRs (build.py).
 //  * Iteration j is a software pipeline over two stages: S, P, dP and dV of
-//    stage j and dS and dK of stage j - 1, in four phases of 16 MFMAs, each
-//    written in issue order (one MFMA, its share of another product's VALU
-//    work, an LDS read ahead; groups kept in order by scheduling barriers):
-//      A. S(j)        beside dS(j - 1) of key block 1
-//      B. dK(j - 1)   beside P(j) of key block 0
-//      C. dP(j)       beside P(j) of key block 1
-//      D. dV(j)       beside dS(j) of key block 0 and stage j + 1's lse and
-//                     delta columns turned into -lse log2 e and -delta
+//    stage j and dS and dK of stage j - 1, in four phases of 16 MFMAs (at
+//    DV = 128 or 256), each written in issue order (one MFMA, its share of
+//    another product's VALU work, an LDS read ahead; groups kept in order by
+//    scheduling barriers), each phase's first operands read during the
+//    previous phase's last products:
+//      A. S(j)        beside the second half of dS(j - 1)
+//      B. dK(j - 1)   beside the first half of P(j)
+//      C. dP(j)       beside the second half of P(j)
+//      D. dV(j)       beside the first half of dS(j) and stage j + 1's lse
+//                     and delta columns turned into -lse log2 e and -delta
 //  * Stages visit the query tiles top-down with the GQA group's heads inner,
-//    as the other dK/dV kernels do, on a 5-slot LDS ring (Q, dO, and each
-//    wave's own lse and delta columns): the loads of stage j + 3 go out
-//    between the products of iteration j, and every wave waits for its own
-//    loads of stage j + 1 in phase D, then one barrier per iteration.
+//    as the other dK/dV kernels do, on an LDS ring (Q, dO, and each wave's
+//    own lse and delta columns; 5 slots of 18 KB or 4 of 34 KB): the loads
+//    of stage j + NBUF - 2 go out between the products of iteration j, and
+//    every wave waits for its own loads of stage j + 1 in phase C, then one
+//    barrier per iteration.
 //  * A workgroup takes key blocks b and nb - 1 - b of a sequence (nb
 //    blocks): under causal masking every such pair is the same amount of
 //    work, which keeps the in-order dispatch balanced.
 // The arithmetic is that of the other dK/dV kernels: P and dS rounded to T,
 // dS from the rounded P, masks as -inf logits (scale > 0, host-checked).
 // ---------------------------------------------------------------------------
-template <typename T, int D, int DV, bool OUT_F32>
+template <typename T, int D, int DV, int NKB, bool OUT_F32>
 __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
-    static_assert(D == 128, "128-wide tiles");
-    constexpr int NW = 4, NKB = 2, KPW = 32 * NKB;     // waves, key blocks per wave, keys per wave
+    static_assert((D == 128 && NKB == 2) || (D == 256 && NKB == 1), "128-wide tiles: 64 keys per wave; 256-wide: 32");
+    constexpr int NW = 4, KPW = 32 * NKB;               // waves, keys per wave
     constexpr int DC = (DV + 15) / 16, DB = (DV + 31) / 32;
     constexpr int QTL = 32;                             // queries per stage
     constexpr int KB = NW * KPW;                        // keys per workgroup
-    constexpr int TILE = QTL * D * 2;                   // 8 KB
+    constexpr int TILE = QTL * D * 2;                   // 8 or 16 KB
     constexpr int LCOL = 64 * 4;                        // one lse / delta column (64 rows loaded)
     constexpr int SLOT = 2 * TILE + NW * 2 * LCOL;      // Q, dO, each wave's own lse and delta columns
-    constexpr int NBUF = 5, AHEAD = 3;                 // slots; stages loading ahead
+    constexpr int NBUF = D == 128 ? 5 : 4;              // slots (90 or 136 KB)
+    constexpr int AHEAD = NBUF - 2;                     // stages loading ahead
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * SLOT];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -130,7 +143,6 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
         constexpr int LQ = Stager::N;                        // loads per wave per tile
         static_assert(Stager::PER % NW == 0, "whole tile loads per wave");
         constexpr int NL = 2 * LQ + 2;                       // loads per wave per stage
-        static_assert(NL == 6, "the phases issue loads 0-5");
         int ld_st = 0, ld_hl = 0, ld_qt = qt_first, ld_slot = 0;
         const uint16_t* ld_q = p.q + (int64_t)(qr.start + qt_first) * p.q_rs + (int64_t)hk * p.g * DV;
         const uint16_t* ld_do = p.dout + (int64_t)(qr.start + qt_first) * p.do_rs + (int64_t)hk * p.g * DV;
@@ -193,7 +205,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                 ld_d += 1;
             }
         };
-        static_assert((AHEAD - 1) * NL <= 15, "vmcnt range");
+        static_assert((AHEAD - 1) * NL < 64, "vmcnt range");
         // this wave's lse and delta columns of stage slot `slot` become -lse
         // log2 e and -delta (lane = row; the wave's own loads, landed): read
         // in one phase, written back in the next
@@ -215,7 +227,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
 
         const uint32_t rbase = row_base<D>(l32, hi), tbase = tr_base<D>(lane);
         const float c2 = p.scale_log2;
-        f32x16_t accv[NKB][DB], acck[NKB][DB];       // dV^T, dK^T of both key blocks
+        f32x16_t accv[NKB][DB], acck[NKB][DB];       // dV^T, dK^T of the wave's key blocks
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
@@ -229,12 +241,13 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
         // stage j - 1. Iteration j computes S, P, dP and dV of stage j and dS
         // and dK of stage j - 1, in four phases of one MFMA stream each with
         // the VALU work of another product beside it:
-        //   A. S(j)        beside dS(j - 1) = P (dP - delta), rounded to T
+        //   A. S(j)        beside half of dS(j - 1) = P (dP - delta), rounded to T
         //   B. dK(j - 1)   beside half of P(j) = exp2(S c - lse'), rounded to T
         //   C. dP(j)       beside the other half of P(j)
-        //   D. dV(j)       beside -lse log2 e, -delta of stage j + 1
+        //   D. dV(j)       beside the other half of dS(j)
         // P(j) (packed) and dP(j) - delta stay in registers into iteration
-        // j + 1. The loads of stage j + 3 go out between the S products.
+        // j + 1. The loads of stage j + AHEAD go out during phases A (Q),
+        // B (dO) and C (lse and delta).
         int c_hl = 0, c_qt = qt_first, c_slot = 0, p_slot = 0;
         u32x4_t pk[NKB][2];                      // P of the stage in flight, rounded to T (B operands of dV)
         f32x16_t pacc[NKB];                      // its dP - delta
@@ -242,16 +255,26 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
         u32x4_t dsk[NKB][2];                     // dS of the previous stage, rounded to T (B operands of dK)
         constexpr int NS = NKB * DC;             // S or dP products per stage
         constexpr int NP = 2 * DB * NKB;         // dV or dK products per stage
-        constexpr int TPF = 4;                   // transposed operands read ahead
-        static_assert(TPF == 4 && 2 * DB >= TPF, "phases A and C read B's and D's first four");
+        // operands read ahead: eight MFMAs' worth at 64 keys per wave, four
+        // row or six transposed operands at 32
+        constexpr int RPF = NKB == 2 ? 2 : 4, TPF = NKB == 2 ? 4 : 6;
+        static_assert(DC >= RPF && 2 * DB >= TPF && NS >= 4 && NP >= 4, "prefetch depths");
+        constexpr int HP = 4 * NKB;              // dS or P pairs per half stage
+        // n loads from `first` spread over a phase of `groups` MFMA groups
+        auto loads_at = [&](int i, int groups, int first, int n) {
+#pragma unroll
+            for (int k = 0; k < n; ++k)
+                if (i == 1 + k * groups / n) load(first + k);
+        };
         // Does any (query, key) of stage j fall outside the band? (the per-block
-        // tests of the other kernels over this wave's 64 keys)
+        // tests of the other kernels over this wave's keys)
         auto stage_needs_mask = [&]() {
             return (kw + KPW > kv_len) | (c_qt + QTL > q_len) | ((p.causal != 0) & (wk_last > c_qt + coff)) |
                    ((p.window > 0) & (kw < min(q_len, c_qt + QTL) + coff - p.window));
         };
-        // pair pr = 0..15 of a stage's 32 elements per lane: key block pr / 8,
-        // rows 2 (pr % 8) and 2 (pr % 8) + 1
+        // pair pr = 0 .. 8 NKB - 1 of a stage's 16 NKB elements per lane: key
+        // block pr / 8, rows 2 (pr % 8) and 2 (pr % 8) + 1; the first half
+        // stage is pairs 0 .. HP - 1
         auto exp_pair = [&](int pr, const f32x16_t& nl) {
             const int kb = pr >> 3, r0 = 2 * (pr & 7);
             const float x0 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r0], c2, nl[r0]));
@@ -297,13 +320,13 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
             float fl = 0.f, fd = 0.f;                // stage j + 1's lse and delta (this wave's rows)
             auto read_tq = [&](int i) { tq[i] = tr_operand<D>(qtb, i / DB, i % DB); };
             auto read_td = [&](int i) { td[i] = tr_operand<D>(dtb, i / DB, i % DB); };
-            // A. S(j) beside dS(j - 1) of key block 1; the loads of stage j + 3
-            //    start; B's first operands are read at the end
+            // A. S(j) beside the second half of dS(j - 1); the loads of stage
+            //    j + AHEAD start (Q); B's first operands are read at the end
             if constexpr (!LAST) {
                 const char* qrb = opaque(Qc + rbase);
                 u32x4_t qa[DC];
 #pragma unroll
-                for (int i = 0; i < 2 && i < DC; ++i) qa[i] = row_operand<D>(qrb, i, 0);
+                for (int i = 0; i < RPF; ++i) qa[i] = row_operand<D>(qrb, i, 0);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int kc = 0; kc < DC; ++kc) {
@@ -311,15 +334,18 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                     for (int kb = 0; kb < NKB; ++kb) {
                         const int i = NKB * kc + kb;
                         sacc[kb] = mfma32<T>(qa[kc], kf[kb][kc], kc == 0 ? f32x16_t{} : sacc[kb]);
-                        if (kb == NKB - 1 && kc + 2 < DC) qa[kc + 2] = row_operand<D>(qrb, kc + 2, 0);
-                        if (i == 1) load(0);
-                        if (i == NS / 2 + 1) load(1);
+                        if (kb == NKB - 1 && kc + RPF < DC) qa[kc + RPF] = row_operand<D>(qrb, kc + RPF, 0);
+                        loads_at(i, NS, 0, LQ);
                         if constexpr (!FIRST) {
 #pragma unroll
-                            for (int pr = 8; pr < 16; ++pr)
-                                if ((pr - 8) * NS / 8 == i) ds_pair(pr);
-                            if (i == NS - 2) { read_tq(0); read_tq(1); }
-                            if (i == NS - 1) { read_tq(2); read_tq(3); }
+                            for (int h = 0; h < HP; ++h)
+                                if (h * NS / HP == i) ds_pair(HP + h);
+                            if (i == NS - 2)
+#pragma unroll
+                                for (int t = 0; t < TPF / 2; ++t) read_tq(t);
+                            if (i == NS - 1)
+#pragma unroll
+                                for (int t = TPF / 2; t < TPF; ++t) read_tq(t);
                         }
                         if (i == NS - 3) nl = read_col(Qc, 0);
                         __builtin_amdgcn_sched_barrier(0);
@@ -340,11 +366,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                 }
             } else {
 #pragma unroll
-                for (int pr = 8; pr < 16; ++pr) ds_pair(pr);
+                for (int h = 0; h < HP; ++h) ds_pair(HP + h);
 #pragma unroll
                 for (int i = 0; i < TPF; ++i) read_tq(i);
             }
-            // B. dK(j - 1) beside P(j) of key block 0 (the dK and dV products
+            // B. dK(j - 1) beside the first half of P(j) (the dK and dV products
             //    are inline asm with their own hazard wait, mfma32_acc); C's
             //    first operands are read at the end
             __builtin_amdgcn_sched_barrier(0);
@@ -358,29 +384,32 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                         mfma32_acc<T>(acck[kb][db], tq[i2], dsk[kb][qc]);
                         if (kb == NKB - 1 && i2 + TPF < 2 * DB) read_tq(i2 + TPF);
                         if constexpr (!LAST) {
-                            if (i == 1) load(2);
-                            if (i == NP / 2 + 1) load(3);
+                            loads_at(i, NP, LQ, LQ);
 #pragma unroll
-                            for (int pr = 0; pr < 8; ++pr)
-                                if (pr * NP / 8 == i) exp_pair(pr, nl);
+                            for (int h = 0; h < HP; ++h)
+                                if (h * NP / HP == i) exp_pair(h, nl);
                             if (i == NP - 4) dinit = read_col(Qc, 1);
-                            if (i == NP - 2) da[0] = row_operand<D>(drb, 0, 0);
-                            if (i == NP - 1) da[1] = row_operand<D>(drb, 1, 0);
+                            if (i == NP - 2)
+#pragma unroll
+                                for (int r = 0; r < RPF / 2; ++r) da[r] = row_operand<D>(drb, r, 0);
+                            if (i == NP - 1)
+#pragma unroll
+                                for (int r = RPF / 2; r < RPF; ++r) da[r] = row_operand<D>(drb, r, 0);
                         }
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             } else {
-                load(2);
-                load(3);
 #pragma unroll
-                for (int pr = 0; pr < 8; ++pr) exp_pair(pr, nl);
+                for (int k = 0; k < LQ; ++k) load(LQ + k);
+#pragma unroll
+                for (int h = 0; h < HP; ++h) exp_pair(h, nl);
                 dinit = read_col(Qc, 1);
-                da[0] = row_operand<D>(drb, 0, 0);
-                da[1] = row_operand<D>(drb, 1, 0);
+#pragma unroll
+                for (int r = 0; r < RPF; ++r) da[r] = row_operand<D>(drb, r, 0);
             }
             if constexpr (!LAST) {
-                // C. dP(j) onto -delta beside P(j) of key block 1; at the end,
+                // C. dP(j) onto -delta beside the second half of P(j); at the end,
                 //    D's first operands and the columns of stage j + 1 (this
                 //    wave's own loads of that stage have landed once at most
                 //    the two later stages' loads are in flight)
@@ -391,23 +420,26 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                     for (int kb = 0; kb < NKB; ++kb) {
                         const int i = NKB * kc + kb;
                         pacc[kb] = mfma32<T>(da[kc], vf[kb][kc], kc == 0 ? dinit : pacc[kb]);
-                        if (kb == NKB - 1 && kc + 2 < DC) da[kc + 2] = row_operand<D>(drb, kc + 2, 0);
-                        if (i == 1) load(4);
-                        if (i == NS / 2 + 1) load(5);
+                        if (kb == NKB - 1 && kc + RPF < DC) da[kc + RPF] = row_operand<D>(drb, kc + RPF, 0);
+                        loads_at(i, NS, 2 * LQ, 2);
 #pragma unroll
-                        for (int pr = 8; pr < 16; ++pr)
-                            if ((pr - 8) * NS / 8 == i) exp_pair(pr, nl);
+                        for (int h = 0; h < HP; ++h)
+                            if (h * NS / HP == i) exp_pair(HP + h, nl);
                         if (i == NS - 3) {
                             wait_vmcnt<(AHEAD - 1) * NL>();
                             fix_read(n_slot, fl, fd);
                         }
-                        if (i == NS - 2) { read_td(0); read_td(1); }
-                        if (i == NS - 1) { read_td(2); read_td(3); }
+                        if (i == NS - 2)
+#pragma unroll
+                            for (int t = 0; t < TPF / 2; ++t) read_td(t);
+                        if (i == NS - 1)
+#pragma unroll
+                            for (int t = TPF / 2; t < TPF; ++t) read_td(t);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
-                // D. dV(j) beside dS(j) of key block 0 (block 1 follows in the
-                //    next iteration's phase A); stage j + 1's columns written
+                // D. dV(j) beside the first half of dS(j) (the second follows in
+                //    the next iteration's phase A); stage j + 1's columns written
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i2 = 0; i2 < 2 * DB; ++i2) {
@@ -419,8 +451,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                         if (kb == NKB - 1 && i2 + TPF < 2 * DB) read_td(i2 + TPF);
                         if (i == 2) fix_write(n_slot, fl, fd);
 #pragma unroll
-                        for (int pr = 0; pr < 8; ++pr)
-                            if (pr * NP / 8 == i) ds_pair(pr);
+                        for (int h = 0; h < HP; ++h)
+                            if (h * NP / HP == i) ds_pair(h);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
@@ -448,7 +480,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
             fix_cols(0);
             __syncthreads();
             // every wave's loads of stage j + 1 have landed by the end of
-            // iteration j (each waited for its own in phase D): the barrier
+            // iteration j (each waited for its own in phase C): the barrier
             // after it publishes them
             int n_slot = c_slot == NBUF - 1 ? 0 : c_slot + 1;
             prep();
@@ -470,12 +502,14 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
             // MFMAs, and may copy accumulators out at the end of this block):
             // these asm statements take every accumulator as an operand, the
             // first one after 32 wait states, so no read can come earlier.
-            asm volatile("s_nop 15\n\ts_nop 15" : "+a"(acck[0][0]), "+a"(acck[1][0]));
+            asm volatile("s_nop 15\n\ts_nop 15" : "+a"(acck[0][0]));
 #pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                if (db > 0) asm volatile("" : "+a"(acck[0][db]), "+a"(acck[1][db]));
-                asm volatile("" : "+a"(accv[0][db]), "+a"(accv[1][db]));
-            }
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    if (kb + db > 0) asm volatile("" : "+a"(acck[kb][db]));
+                    asm volatile("" : "+a"(accv[kb][db]));
+                }
         }
         // the reloads issued past the last stage land before the wave ends
         wait_vmcnt<0>();
@@ -505,13 +539,14 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
 }
 
 
-template <typename T, int DV, bool OUT_F32>
+template <typename T, int D, int DV, bool OUT_F32>
 hipError_t launch_wide(const BwdArgs& a, hipStream_t st) {
+    constexpr int NKB = D == 128 ? 2 : 1, KB = 4 * 32 * NKB;
     BwdKParams p = make_params(a);
-    p.n_tiles = (int)(a.geo.total_kv / 512) + a.geo.num_seqs + 1;   // pairs of 256-key blocks
+    p.n_tiles = (int)(a.geo.total_kv / (2 * KB)) + a.geo.num_seqs + 1;   // pairs of key blocks
     const int64_t blocks = (int64_t)p.n_tiles * a.geo.hkv;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((bwd_dkv_wide_kernel<T, 128, DV, OUT_F32>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((bwd_dkv_wide_kernel<T, D, DV, NKB, OUT_F32>), dim3((unsigned)blocks), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 
@@ -519,10 +554,11 @@ template <typename T>
 hipError_t launch_wide_dims(const BwdArgs& a, hipStream_t st) {
     const bool f = a.out_f32 != 0;
     switch (a.geo.d) {
-        case 80: return f ? launch_wide<T, 80, true>(a, st) : launch_wide<T, 80, false>(a, st);
-        case 88: return f ? launch_wide<T, 88, true>(a, st) : launch_wide<T, 88, false>(a, st);
-        case 96: return f ? launch_wide<T, 96, true>(a, st) : launch_wide<T, 96, false>(a, st);
-        case 128: return f ? launch_wide<T, 128, true>(a, st) : launch_wide<T, 128, false>(a, st);
+        case 80: return f ? launch_wide<T, 128, 80, true>(a, st) : launch_wide<T, 128, 80, false>(a, st);
+        case 88: return f ? launch_wide<T, 128, 88, true>(a, st) : launch_wide<T, 128, 88, false>(a, st);
+        case 96: return f ? launch_wide<T, 128, 96, true>(a, st) : launch_wide<T, 128, 96, false>(a, st);
+        case 128: return f ? launch_wide<T, 128, 128, true>(a, st) : launch_wide<T, 128, 128, false>(a, st);
+        case 256: return f ? launch_wide<T, 256, 256, true>(a, st) : launch_wide<T, 256, 256, false>(a, st);
         default: return hipErrorNotSupported;
     }
 }

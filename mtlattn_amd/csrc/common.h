@@ -388,8 +388,8 @@ __device__ inline uint32_t bias_base(int rr, int hi) { return (uint32_t)(rr * 25
 // (s_waitcnt vmcnt(N), other counters untouched); N <= 15.
 template <int N>
 __device__ inline void wait_vmcnt() {
-    static_assert(N >= 0 && N < 16, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8));
+    static_assert(N >= 0 && N < 64, "vmcnt range");   // 6 bits: [3:0] and [15:14]
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 // Scheduling hint for the region just emitted: N MFMAs that each consume R

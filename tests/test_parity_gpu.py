@@ -299,8 +299,11 @@ def test_mfma_padded_head_dims(mt):
 def test_mfma_wide_head_dims(mt):
     """Head dims 160/256 run the matrix-core kernels on 256-wide tiles: one
     launch per kernel where the registers allow it (every forward except the
-    biased D = 256 one, dQ, dK/dV at D = 160), else 128-column slices."""
+    biased D = 256 one, dQ, dK/dV at D = 160), else 128-column slices; dK/dV
+    at D = 256 without a bias runs all 256 columns in one pass (one wave per
+    SIMD, 32 keys per wave)."""
     b, h = torch.bfloat16, torch.float16
+    _bwd(mt, "bwd D=256 fp16 non-causal ragged MHA", [129, 300, 31], [129, 300, 31], 8, 8, 256, h, 6e-3)
     for D in (160, 256):
         _fwd(mt, f"D={D} bf16 GQA causal ragged", [300, 77, 513], [300, 77, 513], 16, 4, D, b, atol=4e-2,
              causal=True)
