@@ -427,14 +427,16 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
     const int n_q_tiles = q_hi > q_lo ? (q_hi - q_lo + QTL - 1) / QTL : 0;
     const int n_stages = n_q_tiles * p.g;
 
-    // Stage st covers query tile (n_q_tiles - 1 - st / g) of head hk g + st % g:
-    // tiles run top-down with the heads inner, so every workgroup of a
-    // sequence reads the same (tile, head) at the same time and the L2 serves
-    // the repeats (each workgroup stops at its own causal start q_lo).
+    // Stages run over the query tiles top-down with the heads inner, so every
+    // workgroup of a sequence reads the same (tile, head) at the same time and
+    // the L2 serves the repeats (each workgroup stops at its own causal start
+    // q_lo); under a sliding window the walk starts at a tile fixed by the
+    // tile index and wraps (first_q_tile), which keeps that property.
     // Stages are visited in order, so each per-stage quantity (head, first
     // query, ring slot, source rows) is a cursor advanced one stage at a time:
     // no division by g or by the ring depth in the loop.
-    const int qt_first = q_lo + (n_q_tiles - 1) * QTL;
+    const int qt_first = first_q_tile(q_lo, n_q_tiles, QTL, p.window > 0);
+    const int64_t cyc = (int64_t)n_q_tiles * QTL;        // rows of the walk's wrap
     // Direct loads of stage `st`: Q and dO tiles by four loader waves
     // (ldw = 0..3); lse by loaders 0 (and 2), delta by loaders 1 (and 3):
     // column ldw & 1, rows 64 (ldw >> 1) + lane, 4 bytes per lane.
@@ -472,6 +474,12 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
             ld_q += q_wrap;
             ld_do += do_wrap;
             ld_l += l_wrap;
+            if (ld_qt < q_lo) {   // wrap to the top tile (first_q_tile)
+                ld_qt += (int)cyc;
+                ld_q += cyc * p.q_rs;
+                ld_do += cyc * p.do_rs;
+                ld_l += cyc * p.hq;
+            }
         } else {
             ld_q += DV;
             ld_do += DV;
@@ -782,6 +790,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkv_kernel(BwdKParams p) {
         if (++c_hl == p.g) {
             c_hl = 0;
             c_qt -= QTL;
+            if (c_qt < q_lo) c_qt += (int)cyc;
         }
     }
 
@@ -873,7 +882,8 @@ __global__ __launch_bounds__(NW * 64, kWaves / NW) void bwd_dkv_sym_kernel(BwdKP
     const int q_hi = p.window > 0 ? min(q_len, k_last_wg - coff + p.window) : q_len;
     const int n_q_tiles = q_hi > q_lo ? (q_hi - q_lo + QTL - 1) / QTL : 0;
     const int n_stages = n_q_tiles * p.g;
-    const int qt_first = q_lo + (n_q_tiles - 1) * QTL;
+    const int qt_first = first_q_tile(q_lo, n_q_tiles, QTL, p.window > 0);
+    const int64_t cyc = (int64_t)n_q_tiles * QTL;        // rows of the walk's wrap
 
     // Direct loads of a stage: the Q and dO tiles by all NW waves, the lse
     // column by wave 0 and the delta column by wave 1 (one row per lane).
@@ -904,6 +914,12 @@ __global__ __launch_bounds__(NW * 64, kWaves / NW) void bwd_dkv_sym_kernel(BwdKP
             ld_q += q_wrap;
             ld_do += do_wrap;
             ld_l += l_wrap;
+            if (ld_qt < q_lo) {   // wrap to the top tile (first_q_tile)
+                ld_qt += (int)cyc;
+                ld_q += cyc * p.q_rs;
+                ld_do += cyc * p.do_rs;
+                ld_l += cyc * p.hq;
+            }
         } else {
             ld_q += DV;
             ld_do += DV;
@@ -1026,6 +1042,7 @@ __global__ __launch_bounds__(NW * 64, kWaves / NW) void bwd_dkv_sym_kernel(BwdKP
         if (++c_hl == p.g) {
             c_hl = 0;
             c_qt -= QTL;
+            if (c_qt < q_lo) c_qt += (int)cyc;
         }
     }
 

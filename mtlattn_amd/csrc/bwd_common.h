@@ -49,6 +49,21 @@ __device__ inline void store4(void* base, int64_t off, float a, float b, float c
 // Staged lse / delta columns as the dK/dV products use them: lse (which = 0)
 // becomes -lse log2(e), with rows of no allowed key (lse = -inf) giving -inf
 // so that every P of theirs is exp2(-inf) = 0; delta (which = 1) becomes -delta.
+// First query tile (its first row) of a dK/dV workgroup's walk over the
+// n tiles q_lo, q_lo + qtl, ... of its query range. The walk descends from
+// there and, reaching q_lo, wraps to the top tile. Without a window it starts
+// at the top tile: every workgroup of a sequence then reads the same (tile,
+// head) at the same time from the top, and the L2 serves the repeats. Under
+// a sliding window the ranges of neighbouring key blocks are shifted copies
+// of equal length, so the walk starts at the tile whose index is a multiple
+// of n: each tile X then comes at step (start - X) mod n in every workgroup
+// whose range holds it, and co-resident workgroups again read it together.
+__device__ inline int first_q_tile(int q_lo, int n, int qtl, bool cyclic) {
+    if (!cyclic || n <= 0) return q_lo + (n - 1) * qtl;
+    const int lo_t = q_lo / qtl;
+    return q_lo + (n - lo_t % n) % n * qtl;
+}
+
 __device__ inline float neg_lse2(float v) { return v == kNegInf ? kNegInf : -v * kLog2e; }
 __device__ inline void neg_col(float* x, int which) {
     const float v = *x;

@@ -84,19 +84,23 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
     // for every pair, so the in-order dispatch of workgroups keeps the CUs
     // evenly loaded (single blocks, heaviest first per sequence, left each
     // XCD's last sequence's heavy blocks running alone at the end).
-    const int s = find_seq_for_tile(p.cu_kv, p.num_seqs, 2 * KB, t, p.total_kv);
-    const int tb = tile_base(p.cu_kv, s, 2 * KB, p.total_kv);
+    // Under a sliding window every block but a sequence's last few has the
+    // same work, and pairs would not be: tiles are then single blocks.
+    const bool paired = p.window <= 0;
+    const int TK = paired ? 2 * KB : KB;               // keys per tile
+    const int s = find_seq_for_tile(p.cu_kv, p.num_seqs, TK, t, p.total_kv);
+    const int tb = tile_base(p.cu_kv, s, TK, p.total_kv);
     if (t < tb) return;
     const SeqRange qr = seq_range(p.cu_q, s, p.total_q);
     const SeqRange kr = seq_range(p.cu_kv, s, p.total_kv);
     const int q_len = qr.end - qr.start, kv_len = kr.end - kr.start;
     const int pi = t - tb;
     const int nb = (kv_len + KB - 1) / KB;
-    if (pi >= (nb + 1) / 2) return;
+    if (pi >= (paired ? (nb + 1) / 2 : nb)) return;
     const int coff = kv_len - q_len;
     for (int bi = 0; bi < 2; ++bi) {
         const int blk = bi == 0 ? pi : nb - 1 - pi;
-        if (bi == 1 && blk == pi) break;
+        if (bi == 1 && (!paired || blk == pi)) break;
         // the second block reloads the ring's slots: every wave is done with them
         if (bi == 1) __syncthreads();
         const int k0 = blk * KB;
@@ -130,7 +134,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
         const int q_hi = p.window > 0 ? min(q_len, k_last_wg - coff + p.window) : q_len;
         const int n_q_tiles = q_hi > q_lo ? (q_hi - q_lo + QTL - 1) / QTL : 0;
         const int n_stages = n_q_tiles * p.g;
-        const int qt_first = q_lo + (n_q_tiles - 1) * QTL;
+        const int qt_first = first_q_tile(q_lo, n_q_tiles, QTL, p.window > 0);
+        const int64_t cyc = (int64_t)n_q_tiles * QTL;        // rows of the walk's wrap
 
         // Direct loads of a stage: the Q and dO tiles by all four waves (two
         // 1 KB loads of each per wave), and every wave's own copy of the lse and
@@ -198,6 +203,13 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                 ld_do += do_wrap;
                 ld_l += l_wrap;
                 ld_d += l_wrap;
+                if (ld_qt < q_lo) {   // wrap to the top tile (first_q_tile)
+                    ld_qt += (int)cyc;
+                    ld_q += cyc * p.q_rs;
+                    ld_do += cyc * p.do_rs;
+                    ld_l += cyc * p.hq;
+                    ld_d += cyc * p.hq;
+                }
             } else {
                 ld_q += DV;
                 ld_do += DV;
@@ -275,21 +287,76 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
         // pair pr = 0 .. 8 NKB - 1 of a stage's 16 NKB elements per lane: key
         // block pr / 8, rows 2 (pr % 8) and 2 (pr % 8) + 1; the first half
         // stage is pairs 0 .. HP - 1
-        auto exp_pair = [&](int pr, const f32x16_t& nl) {
+        // Inside the phases each pair runs as a short pipeline over
+        // consecutive MFMA groups -- P: the exponents' FMAs, the
+        // exponentials, the rounding to T; dS: the products, the rounding --
+        // so no group waits for a result computed in the same group (the
+        // exponential's latency alone is most of an MFMA's 32 cycles).
+        float xt[8 * NKB][2];                    // pairs between their steps
+        auto exp_fma = [&](int pr, const f32x16_t& nl) {
             const int kb = pr >> 3, r0 = 2 * (pr & 7);
-            const float x0 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r0], c2, nl[r0]));
-            const float x1 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r0 + 1], c2, nl[r0 + 1]));
-            pk[kb][r0 >> 3][(r0 & 7) >> 1] = T::pack2(x0, x1);
+            xt[pr][0] = fmaf(sacc[kb][r0], c2, nl[r0]);
+            xt[pr][1] = fmaf(sacc[kb][r0 + 1], c2, nl[r0 + 1]);
+        };
+        auto exp_exp = [&](int pr) {
+            xt[pr][0] = __builtin_amdgcn_exp2f(xt[pr][0]);
+            xt[pr][1] = __builtin_amdgcn_exp2f(xt[pr][1]);
+        };
+        auto exp_pack = [&](int pr) {
+            const int kb = pr >> 3, r0 = 2 * (pr & 7);
+            pk[kb][r0 >> 3][(r0 & 7) >> 1] = T::pack2(xt[pr][0], xt[pr][1]);
+        };
+        auto exp_pair = [&](int pr, const f32x16_t& nl) {
+            exp_fma(pr, nl);
+            exp_exp(pr);
+            exp_pack(pr);
+        };
+        auto ds_mul = [&](int pr) {
+            const int kb = pr >> 3, r0 = 2 * (pr & 7);
+            const uint32_t wv = pk[kb][r0 >> 3][(r0 & 7) >> 1];
+            xt[pr][0] = lo16<T>(wv) * pacc[kb][r0];
+            xt[pr][1] = hi16<T>(wv) * pacc[kb][r0 + 1];
         };
         // (the empty asm keeps each pair in the phase it is written in: left
         // alone, the compiler moves the pairs next to their use, the dK
         // products, where they run serially)
-        auto ds_pair = [&](int pr) {
+        auto ds_pack = [&](int pr) {
             const int kb = pr >> 3, r0 = 2 * (pr & 7);
-            const uint32_t wv = pk[kb][r0 >> 3][(r0 & 7) >> 1];
-            uint32_t d = T::pack2(lo16<T>(wv) * pacc[kb][r0], hi16<T>(wv) * pacc[kb][r0 + 1]);
+            uint32_t d = T::pack2(xt[pr][0], xt[pr][1]);
             asm volatile("" : "+v"(d));
             dsk[kb][r0 >> 3][(r0 & 7) >> 1] = d;
+        };
+        auto ds_pair = [&](int pr) {
+            ds_mul(pr);
+            ds_pack(pr);
+        };
+        // the steps of pairs first .. first + HP - 1 due in group i of a phase
+        // of n groups (pair h starts in group h n / HP; a P pair's rounding
+        // past the phase's last group runs after it: ps_tail)
+        auto ps_exp = [&](int i, int n, int first, const f32x16_t& nl) {
+#pragma unroll
+            for (int h = 0; h < HP; ++h) {
+                const int g0 = h * n / HP;
+                if (i == g0) exp_fma(first + h, nl);
+                if (i == g0 + 1) exp_exp(first + h);
+                if (i == g0 + 2) exp_pack(first + h);
+            }
+        };
+        auto ps_tail = [&](int n, int first) {
+#pragma unroll
+            for (int h = 0; h < HP; ++h) {
+                const int g0 = h * n / HP;
+                if (g0 + 1 >= n) exp_exp(first + h);
+                if (g0 + 2 >= n) exp_pack(first + h);
+            }
+        };
+        auto ps_ds = [&](int i, int n, int first) {
+#pragma unroll
+            for (int h = 0; h < HP; ++h) {
+                const int g0 = h * n / HP;
+                if (i == g0) ds_mul(first + h);
+                if (i == (g0 + 1 < n ? g0 + 1 : n - 1)) ds_pack(first + h);
+            }
         };
         // (the lane half from the per-stage lane copy: see prep)
         auto read_col = [&](const char* slot, int which) {   // 16 rows of this wave's column, C layout
@@ -334,12 +401,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                     for (int kb = 0; kb < NKB; ++kb) {
                         const int i = NKB * kc + kb;
                         sacc[kb] = mfma32<T>(qa[kc], kf[kb][kc], kc == 0 ? f32x16_t{} : sacc[kb]);
+                        __builtin_amdgcn_sched_barrier(0);   // the MFMA first in its group
                         if (kb == NKB - 1 && kc + RPF < DC) qa[kc + RPF] = row_operand<D>(qrb, kc + RPF, 0);
                         loads_at(i, NS, 0, LQ);
                         if constexpr (!FIRST) {
-#pragma unroll
-                            for (int h = 0; h < HP; ++h)
-                                if (h * NS / HP == i) ds_pair(HP + h);
+                            ps_ds(i, NS, HP);
                             if (i == NS - 2)
 #pragma unroll
                                 for (int t = 0; t < TPF / 2; ++t) read_tq(t);
@@ -382,12 +448,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                     for (int kb = 0; kb < NKB; ++kb) {
                         const int i = NKB * i2 + kb;
                         mfma32_acc<T>(acck[kb][db], tq[i2], dsk[kb][qc]);
+                        __builtin_amdgcn_sched_barrier(0);
                         if (kb == NKB - 1 && i2 + TPF < 2 * DB) read_tq(i2 + TPF);
                         if constexpr (!LAST) {
                             loads_at(i, NP, LQ, LQ);
-#pragma unroll
-                            for (int h = 0; h < HP; ++h)
-                                if (h * NP / HP == i) exp_pair(h, nl);
+                            ps_exp(i, NP, 0, nl);
                             if (i == NP - 4) dinit = read_col(Qc, 1);
                             if (i == NP - 2)
 #pragma unroll
@@ -399,6 +464,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
+                if constexpr (!LAST) ps_tail(NP, 0);
             } else {
 #pragma unroll
                 for (int k = 0; k < LQ; ++k) load(LQ + k);
@@ -420,11 +486,10 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                     for (int kb = 0; kb < NKB; ++kb) {
                         const int i = NKB * kc + kb;
                         pacc[kb] = mfma32<T>(da[kc], vf[kb][kc], kc == 0 ? dinit : pacc[kb]);
+                        __builtin_amdgcn_sched_barrier(0);
                         if (kb == NKB - 1 && kc + RPF < DC) da[kc + RPF] = row_operand<D>(drb, kc + RPF, 0);
                         loads_at(i, NS, 2 * LQ, 2);
-#pragma unroll
-                        for (int h = 0; h < HP; ++h)
-                            if (h * NS / HP == i) exp_pair(HP + h, nl);
+                        ps_exp(i, NS, HP, nl);
                         if (i == NS - 3) {
                             wait_vmcnt<(AHEAD - 1) * NL>();
                             fix_read(n_slot, fl, fd);
@@ -438,6 +503,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
+                ps_tail(NS, HP);
                 // D. dV(j) beside the first half of dS(j) (the second follows in
                 //    the next iteration's phase A); stage j + 1's columns written
                 __builtin_amdgcn_sched_barrier(0);
@@ -448,11 +514,10 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
                     for (int kb = 0; kb < NKB; ++kb) {
                         const int i = NKB * i2 + kb;
                         mfma32_acc<T>(accv[kb][db], td[i2], pk[kb][qc]);
+                        __builtin_amdgcn_sched_barrier(0);
                         if (kb == NKB - 1 && i2 + TPF < 2 * DB) read_td(i2 + TPF);
                         if (i == 2) fix_write(n_slot, fl, fd);
-#pragma unroll
-                        for (int h = 0; h < HP; ++h)
-                            if (h * NP / HP == i) ds_pair(h);
+                        ps_ds(i, NP, 0);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
@@ -465,6 +530,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
             if (++c_hl == p.g) {
                 c_hl = 0;
                 c_qt -= QTL;
+                if (c_qt < q_lo) c_qt += (int)cyc;
             }
         };
 
@@ -543,7 +609,9 @@ template <typename T, int D, int DV, bool OUT_F32>
 hipError_t launch_wide(const BwdArgs& a, hipStream_t st) {
     constexpr int NKB = D == 128 ? 2 : 1, KB = 4 * 32 * NKB;
     BwdKParams p = make_params(a);
-    p.n_tiles = (int)(a.geo.total_kv / (2 * KB)) + a.geo.num_seqs + 1;   // pairs of key blocks
+    // pairs of key blocks (single blocks under a sliding window)
+    const int tk = a.geo.window > 0 ? KB : 2 * KB;
+    p.n_tiles = (int)(a.geo.total_kv / tk) + a.geo.num_seqs + 1;
     const int64_t blocks = (int64_t)p.n_tiles * a.geo.hkv;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL((bwd_dkv_wide_kernel<T, D, DV, NKB, OUT_F32>), dim3((unsigned)blocks), dim3(256), 0, st, p);
