@@ -296,6 +296,24 @@ def test_mfma_padded_head_dims(mt):
              bias=_make_bias(512, 8, 512, True))
 
 
+def test_windowed_backward_walk(mt):
+    """Under a sliding window each dK/dV workgroup walks its query tiles
+    from the tile whose index is a multiple of the walk's length and wraps
+    to the top (first_q_tile, bwd_common.h): several key blocks per
+    sequence with different starting tiles, windows that are not multiples
+    of the tile sizes, cross lengths, GQA, on the one-wave-per-SIMD kernel
+    (D = 128, 256; single key blocks under a window) and the wave-pair
+    kernel (with a bias)."""
+    b, h = torch.bfloat16, torch.float16
+    _bwd(mt, "bwd window 700 GQA 8/2 ragged D=128", [1500, 2300], [1500, 2300], 8, 2, 128, b, 4e-2,
+         causal=True, window=700)
+    _bwd(mt, "bwd window 333 cross D=128 fp16", [900, 400], [1300, 1000], 8, 8, 128, h, 6e-3, causal=True,
+         window=333)
+    _bwd(mt, "bwd window 500 D=256", [1200], [1200], 4, 2, 256, b, 4e-2, causal=True, window=500)
+    _bwd(mt, "bwd window 600 broadcast bias D=128", [1100], [1100], 8, 2, 128, h, 6e-3, causal=True,
+         window=600, bias=_make_bias(1100, 8, 1100, True))
+
+
 def test_mfma_wide_head_dims(mt):
     """Head dims 160/256 run the matrix-core kernels on 256-wide tiles: one
     launch per kernel where the registers allow it (every forward except the
