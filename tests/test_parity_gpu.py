@@ -296,6 +296,42 @@ def test_mfma_padded_head_dims(mt):
              bias=_make_bias(512, 8, 512, True))
 
 
+def test_mpp_hooks_fp32_outputs(mt):
+    """The reference's backward test entries _C.mpp_bwd_dq and _C.mpp_bwd_dkv
+    (src/ext.mm:597-711) return fp32 dQ and (dK, dV) from the 16-bit kernels,
+    given the forward's LSE and delta = rowsum(dO * O): checked against the
+    oracle's gradients on the one-wave-per-SIMD dK/dV kernel (D = 128 causal
+    GQA, D = 256 windowed) and the wave-pair kernel (a broadcast bias)."""
+    cases = [("D=128 bf16 causal GQA 8/2 ragged", [300, 77, 513], 8, 2, 128, torch.bfloat16, True, 0, None, 4e-2),
+             ("D=256 fp16 window 200", [400, 250], 4, 4, 256, torch.float16, True, 200, None, 6e-3),
+             ("D=128 fp16 broadcast bias", [384], 8, 8, 128, torch.float16, False, 0,
+              _make_bias(384, 8, 384, True), 6e-3)]
+    for name, lens, Hq, Hkv, D, dt, causal, window, bias, atol in cases:
+        _banner(f"mpp hooks {name}")
+        q, k, v = _inputs(lens, lens, Hq, Hkv, D, dt, 0)
+        dout = randn((sum(lens), Hq, D), dt, torch.Generator().manual_seed(1))
+        cu = cu_of(lens)
+        scale = 1.0 / math.sqrt(D)
+        qd, kd, vd, dd, cud = (t.cuda() for t in (q, k, v, dout, cu))
+        bd = None if bias is None else bias.cuda()
+        lse = torch.empty(sum(lens), Hq, dtype=torch.float32, device="cuda")
+        o = mt._C.varlen_attention(qd, kd, vd, cud, cud, max(lens), scale, causal, window, lse, bd)
+        delta = (o.float() * dd.float()).sum(-1)
+        dq = mt._C.mpp_bwd_dq(qd, kd, vd, dd, lse, delta, cud, cud, max(lens), scale, causal, window, bd)
+        dk, dv = mt._C.mpp_bwd_dkv(qd, kd, vd, dd, lse, delta, cud, cud, max(lens), scale, causal, window, bd)
+        torch.cuda.synchronize()
+        _, _, rq, rk, rv = oracle.varlen_forward_backward(q, k, v, dout, cu, cu, None, causal, window, bias)
+        errs = {}
+        for nm, a, b in (("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
+            assert a.dtype == torch.float32 and torch.isfinite(a).all(), f"{name}: {nm}"
+            errs[nm] = (a.cpu() - b).abs().max().item()
+            errs[nm + "_rms_rel"] = err_stats(a, b, dt)["rms_rel"]
+        print("  " + " ".join(f"{k_}={v_:.3e}" for k_, v_ in errs.items()) + f" atol={atol}", flush=True)
+        for nm in ("dQ", "dK", "dV"):
+            assert errs[nm] < atol, f"{name}: {nm} {errs}"
+            assert errs[nm + "_rms_rel"] <= RMS_BOUND[dt], f"{name}: {nm} rms_rel {errs[nm + '_rms_rel']:.3e}"
+
+
 def test_windowed_backward_walk(mt):
     """Under a sliding window each dK/dV workgroup walks its query tiles
     from the tile whose index is a multiple of the walk's length and wraps
