@@ -48,14 +48,16 @@ namespace {
 //      D. dV(j)       beside the first half of dS(j) and stage j + 1's lse
 //                     and delta columns turned into -lse log2 e and -delta
 //  * Stages visit the query tiles top-down with the GQA group's heads inner,
-//    as the other dK/dV kernels do, on an LDS ring (Q, dO, and each wave's
+//    as the other dK/dV kernels do (under a sliding window from the tile that
+//    first_q_tile picks, wrapping to the top), on an LDS ring (Q, dO, and each wave's
 //    own lse and delta columns; 5 slots of 18 KB or 4 of 34 KB): the loads
 //    of stage j + NBUF - 2 go out between the products of iteration j, and
 //    every wave waits for its own loads of stage j + 1 in phase C, then one
 //    barrier per iteration.
 //  * A workgroup takes key blocks b and nb - 1 - b of a sequence (nb
 //    blocks): under causal masking every such pair is the same amount of
-//    work, which keeps the in-order dispatch balanced.
+//    work, which keeps the in-order dispatch balanced (under a sliding window
+//    one block: there every block but the last few has the same work).
 // The arithmetic is that of the other dK/dV kernels: P and dS rounded to T,
 // dS from the rounded P, masks as -inf logits (scale > 0, host-checked).
 // ---------------------------------------------------------------------------
