@@ -228,13 +228,15 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv_wide_kernel(BwdKParams p) {
             neg_col(c, 0);
             neg_col(c + 64, 1);
         };
+        // (in the loop: the lane from the per-stage copy, so that no
+        // loop-invariant address is kept, and spilled, across the stages)
         auto fix_read = [&](int slot, float& lv, float& dv) {
-            const float* c = reinterpret_cast<const float*>(smem + slot * SLOT + wcol) + lane;
+            const float* c = reinterpret_cast<const float*>(smem + slot * SLOT + wcol) + ln;
             lv = c[0];
             dv = c[64];
         };
         auto fix_write = [&](int slot, float lv, float dv) {
-            float* c = reinterpret_cast<float*>(smem + slot * SLOT + wcol) + lane;
+            float* c = reinterpret_cast<float*>(smem + slot * SLOT + wcol) + ln;
             c[0] = neg_lse2(lv);
             c[64] = -dv;
         };
