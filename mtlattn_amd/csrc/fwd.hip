@@ -8,12 +8,13 @@
 //     hpw * (8 / hpw) * 32 = 256 query-head rows. Small grids without a
 //     bias (D = 128; D = 64 causal) run 4-wave workgroups instead, two per
 //     CU (hpw = gcd(g, 2), a 2-deep ring).
-//   * Key tiles of 64 rows (32 for the 256-wide head dims in one launch) go
-//     straight from HBM into a 3-deep (or 2-deep) LDS ring with
+//   * Key tiles of 64 rows (128 on a 2-deep ring at the 128-wide head dims
+//     without a bias, 32 for the 256-wide ones in one launch) go straight
+//     from HBM into a 3-deep (or 2-deep) LDS ring with
 //     global_load_lds_dwordx4 (no register staging), K and V both row-major
 //     and swizzled; the P.V product reads V^T operands with
 //     ds_read_b64_tr_b16 transposed loads. Without a bias, each wave's loads
-//     of tile i + 2 are issued one at a time between its S products of
+//     of tile i + AHEAD are issued one at a time between its S products of
 //     tile i rather than all at once after the tile barrier.
 //   * Per wave and key tile:  S^T = K Q^T  (v_mfma_f32_32x32x16, 2 x D/16
 //     instructions), online softmax in base 2 on the C registers (each lane
@@ -71,7 +72,7 @@ struct FwdKParams {
 // instead of every wave loading its rows from global memory.
 template <typename T, int DK, int DV, int DVL, int DO, int SM, int BROWS = 0, int KT = kKT, int NW = kWaves, int NBUF = 3>
 __global__ __launch_bounds__(NW * 64, kWaves / NW) void fwd_mfma_kernel(FwdKParams p) {
-    static_assert(KT == 64 || (KT == 32 && BROWS == 0), "32-key tiles: no staged bias");
+    static_assert(KT == 64 || ((KT == 32 || KT == 128) && BROWS == 0), "32- and 128-key tiles: no staged bias");
     constexpr int NKB = KT / 32;             // 32-key blocks per tile
     constexpr int NPC = KT / 16;             // 16-key P chunks per tile
     constexpr bool BIAS = SM != 0;
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(NW * 64, kWaves / NW) void fwd_mfma_kernel(FwdKPara
     // The bias of a whole tile (this lane's 32 keys: 4-key groups at
     // 32 kb + 8 g + 4 hi) is loaded up front, all loads in flight together,
     // and consumed after the S products; 16-byte loads when aligned.
-    auto load_bias = [&](int kt, f32x4_t (&bv)[8]) {
+    auto load_bias = [&](int kt, f32x4_t (&bv)[4 * NKB]) {
         if (kt + KT <= p.bias_cols && p.bias_v4) {
 #pragma unroll
             for (int i = 0; i < 4 * NKB; ++i)
@@ -241,18 +242,18 @@ __global__ __launch_bounds__(NW * 64, kWaves / NW) void fwd_mfma_kernel(FwdKPara
         constexpr bool SPREAD = SM == 0 && DB * 16 + DC * 4 <= 160;
         if (!SPREAD && !reg_bias && it + AHEAD < n_kv_tiles) stage(it + AHEAD);
         const int kt = kv_lo + it * KT;
-        f32x4_t bv[8];
+        f32x4_t bv[4 * NKB];
         if (reg_bias) load_bias(kt, bv);
         if (LDSB) {
             // this lane's 4-key groups of its query row from the staged tile
             const char* bt = opaque(smem + (it % NBUF) * STAGE + KTILE + VTILE + bias_base(32 * (w % wph) + l32, hi));
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < 4 * NKB; ++i)
                 bv[i] = *reinterpret_cast<const f32x4_t*>(lds_xor(bt, 16 * (8 * (i >> 2) + 2 * (i & 3))));
             if (kt + KT > p.bias_cols) {   // keys at or past the bias columns read as 0
                 asm volatile("");
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
+                for (int i = 0; i < 4 * NKB; ++i)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         if (kt + 32 * (i >> 2) + 8 * (i & 3) + 4 * hi + j >= p.bias_cols) bv[i][j] = 0.f;
@@ -582,6 +583,12 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
         else if (sm == 1)
             hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 1>), dim3((unsigned)blocks), dim3(kThreads), 0,
                                st, p);
+        else if constexpr (DK == 128 && DVL == 128)
+            // 128-key tiles on a 2-deep ring (128 KB): the same keys ahead
+            // as 64-key tiles three deep, half the barriers and per-tile
+            // softmax bookkeeping (C3 forward 1.15-1.20 -> 1.08-1.09 ms)
+            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 0, 0, 128, kWaves, 2>), dim3((unsigned)blocks),
+                               dim3(kThreads), 0, st, p);
         else
             hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 0>), dim3((unsigned)blocks), dim3(kThreads), 0,
                                st, p);
