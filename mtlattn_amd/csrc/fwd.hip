@@ -9,7 +9,8 @@
 //     bias (D = 128; D = 64 causal) run 4-wave workgroups instead, two per
 //     CU (hpw = gcd(g, 2), a 2-deep ring).
 //   * Key tiles of 64 rows (128 on a 2-deep ring at the 128-wide head dims
-//     without a bias, 32 for the 256-wide ones in one launch) go straight
+//     without a bias; 32 at D = 256 and 64 on a 2-deep ring at D = 160 in
+//     one launch) go straight
 //     from HBM into a 3-deep (or 2-deep) LDS ring with
 //     global_load_lds_dwordx4 (no register staging), K and V both row-major
 //     and swizzled; the P.V product reads V^T operands with
@@ -555,6 +556,14 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
                                        dim3(kThreads), 0, st, p);
                     return hipGetLastError();
                 }
+            }
+            if constexpr (DV <= 192) {
+                // D = 160: 64-key tiles on a 2-deep ring (246 VGPRs): 0.278
+                // -> 0.258 ms at 2 x 4096 causal, 16/4 heads (at D = 256
+                // they spill)
+                hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DK, DV, 0, 0, 64, kWaves, 2>), dim3((unsigned)blocks),
+                                   dim3(kThreads), 0, st, p);
+                return hipGetLastError();
             }
             hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DK, DV, 0, 0, 32>), dim3((unsigned)blocks), dim3(kThreads),
                                0, st, p);
