@@ -592,12 +592,16 @@ hipError_t launch_typed(const FwdArgs& a, hipStream_t st) {
         else if (sm == 1)
             hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 1>), dim3((unsigned)blocks), dim3(kThreads), 0,
                                st, p);
-        else if constexpr (DK == 128 && DVL == 128)
+        else if (DK == 128 && DVL == 128 && !(g.window > 0 && g.window < 1024))
             // 128-key tiles on a 2-deep ring (128 KB): the same keys ahead
             // as 64-key tiles three deep, half the barriers and per-tile
-            // softmax bookkeeping (C3 forward 1.15-1.20 -> 1.08-1.09 ms)
-            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 0, 0, 128, kWaves, 2>), dim3((unsigned)blocks),
-                               dim3(kThreads), 0, st, p);
+            // softmax bookkeeping (C3 forward 1.15-1.16 -> 1.10-1.13 ms on
+            // one box, non-causal -4%, window 4096 -2%); a window below 1024
+            // keys keeps 64-key tiles (the band's tile rounding costs more:
+            // window 256 +7% with 128)
+            hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 0, 0, (DK == 128 && DVL == 128) ? 128 : 64, kWaves,
+                                                (DK == 128 && DVL == 128) ? 2 : 3>),
+                               dim3((unsigned)blocks), dim3(kThreads), 0, st, p);
         else
             hipLaunchKernelGGL((fwd_mfma_kernel<T, DK, DV, DVL, DO, 0>), dim3((unsigned)blocks), dim3(kThreads), 0,
                                st, p);
