@@ -19,6 +19,7 @@ Conventions shared with the reference:
 """
 
 import math
+import weakref
 
 import torch
 
@@ -238,6 +239,48 @@ def _basic_ok(query, key, value, dropout_p, min_seqlen):
     return query.shape[2] >= min_seqlen
 
 
+# The padding path's one host decision -- a device reduction read back to the
+# host -- is made once per mask tensor and reused while that tensor is alive
+# and unmodified (same object, version counter, storage, shape and strides):
+# a model passes the same mask to every layer's attention call, so a forward
+# pass waits on the device once for it, not once per layer. Entries go when
+# their mask is freed.
+_PAD_DECISIONS = {}
+
+
+def _padding_decision(attn_mask, B, Hq, Nq, Nkv):
+    """(ok, lens) for a self-attention mask over [B, Hq, Nq, Nkv]: ok when it
+    depends only on (batch, key) with the kept keys a prefix (and, for a float
+    mask, adds exactly 0 to them); lens = kept keys per batch (int32, on the
+    mask's device), or None when the mask does not broadcast to that shape.
+    Cached per mask tensor (see _PAD_DECISIONS)."""
+    sig = (attn_mask._version, attn_mask.data_ptr(), tuple(attn_mask.shape), tuple(attn_mask.stride()),
+           B, Hq, Nq, Nkv)
+    hit = _PAD_DECISIONS.get(id(attn_mask))
+    if hit is not None and hit[0]() is attn_mask and hit[1] == sig:
+        return hit[2], hit[3]
+    keep0 = attn_mask if attn_mask.dtype == torch.bool else attn_mask > -1e30
+    try:
+        keep = keep0.expand(B, Hq, Nq, Nkv)
+    except RuntimeError:
+        return False, None
+    kv_keep = keep[:, 0, 0, :]
+    lens = kv_keep.sum(dim=1, dtype=torch.int32)
+    idx = torch.arange(Nkv, device=attn_mask.device)
+    # both tests in one device reduction, compared at the mask's own
+    # broadcast shape, not the expanded [B, H, N, N]
+    ok = torch.logical_and((keep0 == kv_keep[:, None, None, :]).all(),
+                           (kv_keep == (idx[None, :] < lens[:, None])).all())
+    if attn_mask.dtype != torch.bool:
+        # a float mask is a padding mask only if it adds nothing to the keys
+        # it keeps (else its values are an additive bias)
+        ok = torch.logical_and(ok, (attn_mask.masked_fill(~keep0, 0) == 0).all())
+    ok = bool(ok)
+    k = id(attn_mask)
+    _PAD_DECISIONS[k] = (weakref.ref(attn_mask, lambda _r, k=k: _PAD_DECISIONS.pop(k, None)), sig, ok, lens)
+    return ok, lens
+
+
 def _try_padding_varlen(query, key, value, attn_mask, is_causal, scale):
     """Self-attention key-padding mask -> packed varlen call (reference:
     mtlattn/__init__.py:202-249). Applies when the mask depends only on
@@ -250,24 +293,9 @@ def _try_padding_varlen(query, key, value, attn_mask, is_causal, scale):
     Hkv, Nkv = key.shape[1], key.shape[2]
     if Nq != Nkv:
         return None
-    keep0 = attn_mask if attn_mask.dtype == torch.bool else attn_mask > -1e30
-    try:
-        keep = keep0.expand(B, Hq, Nq, Nkv)
-    except RuntimeError:
-        return None
-    kv_keep = keep[:, 0, 0, :]
-    lens = kv_keep.sum(dim=1, dtype=torch.int32)
-    idx = torch.arange(Nkv, device=query.device)
-    # the one host decision: does the mask depend only on (batch, key), with
-    # the kept keys a prefix? (both tests in one device reduction, compared at
-    # the mask's own broadcast shape, not the expanded [B, H, N, N])
-    ok = torch.logical_and((keep0 == kv_keep[:, None, None, :]).all(),
-                           (kv_keep == (idx[None, :] < lens[:, None])).all())
-    if attn_mask.dtype != torch.bool:
-        # a float mask is a padding mask only if it adds nothing to the keys
-        # it keeps (else its values are an additive bias)
-        ok = torch.logical_and(ok, (attn_mask.masked_fill(~keep0, 0) == 0).all())
-    if not bool(ok):
+    # the one host decision, made once per mask tensor (_padding_decision)
+    ok, lens = _padding_decision(attn_mask, B, Hq, Nq, Nkv)
+    if not ok:
         return None
     # pack, attend, unpack on the device: no lengths on the host, no
     # per-batch copies (rows past cu[B] belong to no sequence)

@@ -138,6 +138,43 @@ def test_padding_mask_detection_rejects_non_padding():
                                  torch.ones(2, 1, 1, 7, dtype=torch.bool), False, 0.3) is None
 
 
+def test_padding_decision_cached_per_mask():
+    """The padding path's host decision is made once per mask tensor: a second
+    call with the same, unmodified mask reuses it (the same lens tensor, no
+    new device reduction); an in-place change, another shape or another mask
+    decides again; the entry goes when the mask is freed."""
+    import gc
+    B, H, N = 3, 2, 8
+    m = torch.zeros(B, 1, 1, N, dtype=torch.bool)
+    for b, n in enumerate((5, 8, 1)):
+        m[b, :, :, :n] = True
+    ok, lens = M._padding_decision(m, B, H, N, N)
+    assert ok and lens.tolist() == [5, 8, 1]
+    ok2, lens2 = M._padding_decision(m, B, H, N, N)
+    assert ok2 and lens2 is lens
+    assert id(m) in M._PAD_DECISIONS
+    # another broadcast shape of the same mask is decided afresh
+    ok3, lens3 = M._padding_decision(m, B, 4, N, N)
+    assert ok3 and lens3 is not lens
+    # in place: key 6 of batch 0 kept -> no longer a prefix
+    m[0, 0, 0, 6] = True
+    ok4, _ = M._padding_decision(m, B, H, N, N)
+    assert not ok4
+    # a float mask with a nonzero value on a kept key is a bias, not padding
+    f = torch.zeros(B, 1, 1, N)
+    f[:, :, :, 6:] = float("-inf")
+    assert M._padding_decision(f, B, H, N, N)[0]
+    f2 = f.clone()
+    f2[1, 0, 0, 0] = 0.5
+    assert not M._padding_decision(f2, B, H, N, N)[0]
+    # a query-dependent mask
+    assert not M._padding_decision(torch.ones(B, 1, N, N, dtype=torch.bool).tril(), B, H, N, N)[0]
+    k = id(m)
+    del m
+    gc.collect()
+    assert k not in M._PAD_DECISIONS
+
+
 def test_binding_rejects_cpu_tensors():
     q = torch.randn(4, 2, 8)
     cu = torch.tensor([0, 4], dtype=torch.int32)
