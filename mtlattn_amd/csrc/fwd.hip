@@ -86,6 +86,7 @@ __global__ __launch_bounds__(NW * 64, kWaves / NW) void fwd_mfma_kernel(FwdKPara
     constexpr int BTILE = BROWS * KT * 4;   // bytes of one staged bias tile
     constexpr int STAGE = KTILE + VTILE + BTILE;   // K, V (row-major), bias
     constexpr int AHEAD = NBUF - 1;          // tiles loading ahead of the one in use (ring of NBUF)
+    static_assert(NBUF == 2 || NBUF == 3, "the prologue and the waits below assume one or two tiles ahead");
     constexpr int LOADS = STAGE / 1024 / NW;   // direct loads per wave per tile
     static_assert(LOADS <= 15 && STAGE % (1024 * NW) == 0 && (!LDSB || NW == kWaves), "staging");
     __shared__ __attribute__((aligned(1024))) char smem[NBUF * STAGE];
