@@ -525,6 +525,21 @@ def test_window_cases(mt):
     _fwd(mt, "SWA GQA bf16", [900], [900], 32, 8, 128, torch.bfloat16, causal=True, window=300)
 
 
+def test_window_cases_long(mt):
+    """Windows of 1024 keys and more at the 128-wide head dims without a bias:
+    the forward's 128-key tiles (shorter windows take 64-key ones), with the
+    window's first tile rounded down to a tile boundary, ragged and cross
+    (kv longer than q) sequences, and the non-causal band."""
+    b, h = torch.bfloat16, torch.float16
+    _fwd(mt, "SWA w=1500 GQA bf16 ragged", [3000, 1700], [3000, 1700], 16, 4, 128, b, causal=True,
+         window=1500)
+    _fwd(mt, "SWA w=1024 D=96 fp16", [2100], [2100], 8, 8, 96, h, causal=True, window=1024)
+    _fwd(mt, "SWA w=1100 cross (kv longer)", [700, 300], [2500, 1300], 8, 2, 128, h, causal=True,
+         window=1100)
+    _fwd(mt, "SWA non-causal w=1200", [1800], [1800], 8, 2, 128, h, causal=False, window=1200)
+    _bwd(mt, "bwd bf16 window 1500 GQA", [2000], [2000], 16, 4, 128, b, 4e-2, causal=True, window=1500)
+
+
 # backward (tests/test_correctness.py:390-407)
 def test_bwd_fp32(mt):
     f = torch.float32
