@@ -156,6 +156,11 @@ def test_padding_decision_cached_per_mask():
     # another broadcast shape of the same mask is decided afresh
     ok3, lens3 = M._padding_decision(m, B, 4, N, N)
     assert ok3 and lens3 is not lens
+    # a change through another view of the same storage (views share the
+    # version counter): batch 2 keeps keys 0-1, still a prefix, new lengths
+    m.view(B, N)[2, 1] = True
+    ok5, lens5 = M._padding_decision(m, B, H, N, N)
+    assert ok5 and lens5.tolist() == [5, 8, 2]
     # in place: key 6 of batch 0 kept -> no longer a prefix
     m[0, 0, 0, 6] = True
     ok4, _ = M._padding_decision(m, B, H, N, N)
